@@ -1,0 +1,147 @@
+"""Write-gate oracle (torch on the CPU, float32) and its float64 loop pin.
+
+TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``.
+
+Restates ``GatingRMSNorm`` (src/modeling_layers.py:113-131) and
+``GatingPredictor`` (:134-205):
+
+    x_in = concat([rms(pre_k)*w_pre, rms(post_k)*w_post (, rms(v)*w_v)])  (:173-183)
+    h    = act(W1[h] @ x_in + b1[h])           grouped 1x1 conv1 (:148-154, :186-189)
+    g    = sigmoid(w2[h] . h + b2[h])           grouped 1x1 conv2 (:155-161, :191-195)
+    conv path only: g = max(g, g_epsilon)       (:198-205)
+
+``rms(x) = x * rsqrt(mean(x^2) + 1e-6)`` in float32 (:123-128).  ``act`` is
+``nn.GELU()`` (exact erf form) unless ``g_act_fn == "silu"`` (:154).
+
+Parameter names and shapes are the reference's state-dict keys:
+``pre_key_norm.weight (D)``, ``post_key_norm.weight (D)``,
+``value_norm.weight (D)``, ``conv1.weight (Hkv*inner, n_in*D, 1)``,
+``conv1.bias (Hkv*inner)``, ``conv2.weight (Hkv, inner, 1)``,
+``conv2.bias (Hkv)`` with ``inner = int(D * g_expand)``.
+
+The build's scores are float32 computed from float32 copies of the inputs and
+weights; the reference runs the same graph in the model dtype.
+"""
+import math
+
+import torch
+
+RMS_EPS = 1e-6
+
+
+def rms_norm(x, weight):
+    """float32 normalisation, cast back to the input dtype, then ``* weight``
+    (src/modeling_layers.py:124-128): bf16 inputs see their normalised value
+    rounded to bf16 before the weight; float32 inputs are unaffected."""
+    in_dtype = x.dtype
+    xf = x.to(torch.float32)
+    var = xf.pow(2).mean(-1, keepdim=True)
+    y = (xf * torch.rsqrt(var + RMS_EPS)).to(in_dtype).to(torch.float32)
+    return weight.to(torch.float32) * y
+
+
+def gate_scores(pre_key, post_key, value, params, g_inputs=("pre_k", "post_k"),
+                g_act_fn="gelu", fast_path=True, g_epsilon=1e-3):
+    """(B,Hkv,S,D) inputs -> (B,Hkv,S) float32 scores."""
+    B, H, S, D = post_key.shape
+    states = []
+    if "pre_k" in g_inputs:
+        states.append(rms_norm(pre_key, params["pre_key_norm.weight"]))
+    if "post_k" in g_inputs:
+        states.append(rms_norm(post_key, params["post_key_norm.weight"]))
+    if "v" in g_inputs:
+        states.append(rms_norm(value, params["value_norm.weight"]))
+    x = torch.cat(states, dim=-1)                       # (B,H,S,n_in*D)
+    n_in = x.shape[-1]
+    w1 = params["conv1.weight"].to(torch.float32).reshape(H, -1, n_in)
+    b1 = params["conv1.bias"].to(torch.float32).reshape(1, H, 1, -1)
+    hdn = torch.einsum("bhli,hji->bhlj", x, w1) + b1
+    hdn = torch.nn.functional.silu(hdn) if g_act_fn == "silu" else torch.nn.functional.gelu(hdn)
+    w2 = params["conv2.weight"].to(torch.float32).reshape(H, 1, -1)
+    b2 = params["conv2.bias"].to(torch.float32).reshape(1, H, 1, 1)
+    logit = torch.einsum("bhlj,hoj->bhlo", hdn, w2) + b2
+    g = torch.sigmoid(logit.squeeze(-1))
+    if not fast_path:
+        g = torch.clamp(g, min=g_epsilon)
+    return g
+
+
+def gate_logits(pre_key, post_key, value, params, **kw):
+    """Pre-sigmoid logits (used to place the threshold at a quantile)."""
+    g = gate_scores(pre_key, post_key, value, params, **kw).double()
+    return torch.log(g) - torch.log1p(-g)
+
+
+def gate_scores_loop(pre_key, post_key, params, g_act_fn="gelu"):
+    """Scalar float64 loop of the same MLP for ('pre_k','post_k'); tiny inputs only."""
+    B, H, S, D = post_key.shape
+    w1 = params["conv1.weight"].double().reshape(H, -1, 2 * D)
+    b1 = params["conv1.bias"].double().reshape(H, -1)
+    w2 = params["conv2.weight"].double().reshape(H, -1)
+    b2 = params["conv2.bias"].double()
+    wp = params["pre_key_norm.weight"].double().tolist()
+    wk = params["post_key_norm.weight"].double().tolist()
+    out = torch.zeros(B, H, S, dtype=torch.float64)
+
+    def norm(vec, w):
+        ms = sum(t * t for t in vec) / len(vec)
+        r = 1.0 / math.sqrt(ms + RMS_EPS)
+        return [wi * t * r for wi, t in zip(w, vec)]
+
+    for b in range(B):
+        for h in range(H):
+            inner = w1.shape[1]
+            for s in range(S):
+                x = norm(pre_key[b, h, s].double().tolist(), wp) + norm(post_key[b, h, s].double().tolist(), wk)
+                acc = float(b2[h])
+                for j in range(inner):
+                    z = float(b1[h, j]) + sum(a * c for a, c in zip(w1[h, j].tolist(), x))
+                    if g_act_fn == "silu":
+                        a = z / (1.0 + math.exp(-z))
+                    else:
+                        a = 0.5 * z * (1.0 + math.erf(z / math.sqrt(2.0)))
+                    acc += float(w2[h, j]) * a
+                out[b, h, s] = 1.0 / (1.0 + math.exp(-acc))
+    return out
+
+
+def init_params(head_dim, num_kv_heads, g_expand=4.0, n_inputs=2, generator=None):
+    """Random gate parameters with the reference's default init.
+
+    ``reset_parameters`` (src/modeling_layers.py:163-168): RMSNorm weights 1,
+    Conv1d default init = U(-1/sqrt(fan_in), 1/sqrt(fan_in)) for weight and
+    bias, fan_in = in_channels/groups * kernel_size.
+    """
+    inner = int(head_dim * g_expand)
+    fan1 = n_inputs * head_dim
+    fan2 = inner
+    b1 = 1.0 / math.sqrt(fan1)
+    b2 = 1.0 / math.sqrt(fan2)
+
+    def u(shape, bound):
+        return (torch.rand(shape, generator=generator, dtype=torch.float32) * 2 - 1) * bound
+
+    return {
+        "pre_key_norm.weight": torch.ones(head_dim),
+        "post_key_norm.weight": torch.ones(head_dim),
+        "conv1.weight": u((num_kv_heads * inner, fan1, 1), b1),
+        "conv1.bias": u((num_kv_heads * inner,), b1),
+        "conv2.weight": u((num_kv_heads, inner, 1), b2),
+        "conv2.bias": u((num_kv_heads,), b2),
+    }
+
+
+def shift_bias_to_admit(params, pre_key, post_key, value, frac=0.2, threshold=0.1):
+    """Shift ``conv2.bias[h]`` so about ``frac`` of tokens score above ``threshold``.
+
+    new_b2[h] = b2[h] + logit(threshold) - q_{1-frac}(logits over tokens of head h)
+    (the config-1 recipe).  Works on a copy; returns the new params.
+    """
+    p = {k: v.clone() for k, v in params.items()}
+    lg = gate_logits(pre_key, post_key, value, p)          # (B,H,S)
+    H = lg.shape[1]
+    tgt = math.log(threshold / (1 - threshold))
+    for h in range(H):
+        qv = torch.quantile(lg[:, h].reshape(-1), 1.0 - frac).item()
+        p["conv2.bias"][h] += float(tgt - qv)
+    return p

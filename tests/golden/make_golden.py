@@ -1,0 +1,179 @@
+"""Write golden vectors with the reference's own implementation.
+
+Run once in the development container (the only place the reference
+checkout exists):  ``python tests/golden/make_golden.py /path/to/WG-KV``.
+
+Only functions that no closed form or reference test pins are run here:
+
+* ``GatingPredictor.forward`` (src/modeling_layers.py:134-205), fast and conv
+  paths -- float32 scores;
+* the dual-cache state machine through ``self_attn_forward_patch_inference``
+  (:1452-1509) -> ``prefill_wrapper`` (:1183-1376), ``decode_wrapper``
+  (:1379-1449), ``migrate_local_kv_to_global`` (:674-763),
+  ``refresh_local_is_global`` (:1169-1180).
+
+The reference attention kernels are replaced by stubs that record the decode
+metadata (``cache_seqlens``, ``block_table``) and return zeros: attention is
+pinned separately.  Outputs are written as ``.npz`` data (no pickles) plus a
+checksum of the inputs, which the tests regenerate from the same seeds.
+"""
+import importlib.util
+import json
+import os
+import sys
+import types
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+import scenarios  # noqa: E402
+
+
+def load_reference(root):
+    import transformers  # noqa: F401  (the module uses relative imports inside it)
+    path = os.path.join(root, "src", "modeling_layers.py")
+    spec = importlib.util.spec_from_file_location("transformers._wgkv_reference_layers", path)
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules[spec.name] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def make_gate(ref, H, D, g_expand, params, fast_path):
+    g = ref.GatingPredictor(D, H, ["pre_k", "post_k"], "gelu", g_expand, 1e-3, True, fast_path)
+    sd = {k: v.clone() for k, v in params.items()}
+    g.load_state_dict(sd, strict=True)
+    return g.eval()
+
+
+def gate_golden(ref):
+    out = {}
+    for name, sc in scenarios.GATE_SCENARIOS.items():
+        params, pre_k, post_k, value = scenarios.gate_inputs(sc)
+        with torch.no_grad():
+            fast = make_gate(ref, sc["H"], sc["D"], sc["g_expand"], params, True)(pre_k, post_k, value)
+            conv = make_gate(ref, sc["H"], sc["D"], sc["g_expand"], params, False)(pre_k, post_k, value)
+        out[f"{name}.fast"] = fast.numpy()
+        out[f"{name}.conv"] = conv.numpy()
+        out[f"{name}.inputs_sha256"] = np.frombuffer(
+            scenarios.checksum(pre_k, post_k, *params.values()).encode(), dtype=np.uint8)
+    np.savez_compressed(os.path.join(HERE, "gate_golden.npz"), **out)
+    print("gate:", {k: v.shape for k, v in out.items() if not k.endswith("sha256")})
+
+
+def fake_attention_module(ref, sc, layer_idx, record, gate):
+    cfg = types.SimpleNamespace(
+        num_hidden_layers=sc["L"], num_key_value_heads=sc["H"], local_window_size=sc["W"],
+        block_size=16, max_total_tokens=sc["L"] * sc["H"] * sc["max_tokens_per_head"],
+        max_tokens_per_head=sc["max_tokens_per_head"], use_quest=False, g_defer=sc["g_defer"],
+        snapkv_enabled=False, use_baseline=False, g_expand=4.0, random_sparsity=None,
+        g_threshold=0.1,
+    )
+    self = types.SimpleNamespace()
+    self.config = cfg
+    self.layer_idx = layer_idx
+    self.head_dim = sc["D"]
+    self.num_key_value_groups = sc["G"]
+    self.scaling = sc["D"] ** -0.5
+    self.prefill_wrapper = ref.prefill_wrapper
+    self.decode_wrapper = ref.decode_wrapper
+
+    def prefill_kernel(q, k, v, *meta, softmax_scale=None, causal=True, return_softmax_lse=False):
+        return torch.zeros_like(q)
+
+    def decode_kernel_handle(q, k_cache, v_cache, cache_seqlens, block_table, softmax_scale):
+        record.append((cache_seqlens.clone(), block_table.clone()))
+        return lambda: torch.zeros_like(q)
+
+    self.prefill_kernel = prefill_kernel
+    self.decode_kernel_handle = decode_kernel_handle
+    self.decode_kernel_executor = lambda f: f()
+    if gate is not None:
+        self.g_predictors = gate
+    return self
+
+
+def logical_hash(cache, L, H, W, P, D, cur_len):
+    parts = []
+    kc = cache.block_pool_k.view(cache.total_blocks, P, D)
+    vc = cache.block_pool_v.view(cache.total_blocks, P, D)
+    for l in range(L):
+        for h in range(H):
+            T = cur_len + int(cache.global_lengths[l, h])
+            n = (T + P - 1) // P
+            ids = cache.block_table[l, h, :n].long()
+            parts.append(kc[ids].reshape(-1, D)[:T])
+            parts.append(vc[ids].reshape(-1, D)[:T])
+    return scenarios.checksum(*parts)
+
+
+def cache_golden(ref):
+    out = {}
+    meta = {}
+    for name, sc in scenarios.CACHE_SCENARIOS.items():
+        inp = scenarios.cache_inputs(sc)
+        L, H, W, D = sc["L"], sc["H"], sc["W"], sc["D"]
+        gates = None
+        if sc["g_defer"]:
+            gates = [make_gate(ref, H, D, 4.0, scenarios.defer_bias_shift(p), True) for p in inp["gates"]]
+        record = []
+        mods = [fake_attention_module(ref, sc, l, record, gates[l] if gates else None) for l in range(L)]
+        cache = types.SimpleNamespace()
+        with torch.no_grad():
+            for l in range(L):
+                q, pk, k, v, mask = inp["prompt"][l]
+                ref.self_attn_forward_patch_inference(
+                    mods[l], cache, (1, sc["S"]), q, pk, k, v, mask.to(torch.float32))
+            out[f"{name}.after_prefill.block_table"] = cache.block_table.numpy().copy()
+            out[f"{name}.after_prefill.global_lengths"] = cache.global_lengths.numpy().copy()
+            out[f"{name}.after_prefill.local_is_global"] = cache.local_is_global.numpy().copy()
+            meta[f"{name}.after_prefill"] = dict(next_free_block=int(cache.next_free_block),
+                                                 local_ptr=int(cache.local_ptr),
+                                                 local_length=int(cache.local_length))
+            for step in inp["steps"]:
+                for l in range(L):
+                    q, pk, k, v, mask = step[l]
+                    g = None if mask is None else mask.to(torch.float32)
+                    ref.self_attn_forward_patch_inference(mods[l], cache, (1, 1), q, pk, k, v, g)
+        cur_len = cache.local_length
+        out[f"{name}.final.block_table"] = cache.block_table.numpy().copy()
+        out[f"{name}.final.global_lengths"] = cache.global_lengths.numpy().copy()
+        out[f"{name}.final.local_is_global"] = cache.local_is_global.numpy().copy()
+        out[f"{name}.decode_seqlens"] = torch.stack([r[0].reshape(-1) for r in record]).numpy()
+        out[f"{name}.decode_block_table_sha256"] = np.frombuffer(
+            scenarios.checksum(*[r[1] for r in record]).encode(), dtype=np.uint8)
+        meta[name] = dict(next_free_block=int(cache.next_free_block), local_ptr=int(cache.local_ptr),
+                          local_length=int(cache.local_length),
+                          logical_sha256=logical_hash(cache, L, H, W, 16, D, cur_len),
+                          inputs_sha256=scenarios.checksum(
+                              *[t for lay in inp["prompt"] for t in lay],
+                              *[t for st in inp["steps"] for lay in st for t in lay if t is not None]))
+        print(name, meta[name])
+    # capacity error: one head admits more than max_tokens_per_head allows
+    sc = dict(scenarios.CACHE_SCENARIOS["long_prompt"], max_tokens_per_head=256)
+    inp = scenarios.cache_inputs(sc)
+    cache = types.SimpleNamespace()
+    mod = fake_attention_module(ref, sc, 0, [], None)
+    q, pk, k, v, mask = inp["prompt"][0]
+    try:
+        ref.self_attn_forward_patch_inference(mod, cache, (1, sc["S"]), q, pk, k, v, mask.to(torch.float32))
+        meta["capacity_error_raises"] = False
+    except AssertionError:
+        meta["capacity_error_raises"] = True
+    np.savez_compressed(os.path.join(HERE, "cache_golden.npz"), **out)
+    with open(os.path.join(HERE, "cache_golden.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+
+
+def main():
+    root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    ref = load_reference(root)
+    torch.set_num_threads(4)
+    gate_golden(ref)
+    cache_golden(ref)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,115 @@
+"""Seeded input scenarios shared by the golden-vector writer and the tests.
+
+Inputs are regenerated from ``torch.Generator`` seeds (CPU Mersenne
+Twister); each fixture stores a checksum of its inputs so a change of RNG
+stream is detected instead of silently compared.
+"""
+import hashlib
+
+import numpy as np
+import torch
+
+# name -> scenario description (all batch 1, the reference's inference batch)
+CACHE_SCENARIOS = {
+    # prompt longer than the window: prefill scatter + migration every step
+    "long_prompt": dict(L=2, H=2, G=2, D=64, W=128, S=1000, steps=200, rates=(0.2, 0.5),
+                        step_rate=0.3, max_tokens_per_head=4096, g_defer=False, seed=1),
+    # prompt shorter than the window: ring fills during decode, then migrates
+    "short_prompt": dict(L=2, H=2, G=2, D=64, W=128, S=100, steps=160, rates=(0.3, 0.6),
+                         step_rate=0.5, max_tokens_per_head=4096, g_defer=False, seed=2),
+    # deferred gating: decode steps carry no scores, the full window is re-gated
+    "defer": dict(L=2, H=2, G=2, D=64, W=64, S=300, steps=150, rates=(0.25, 0.25),
+                  step_rate=None, max_tokens_per_head=4096, g_defer=True, seed=3),
+    # three layers, page-boundary lengths
+    "three_layers": dict(L=3, H=2, G=1, D=64, W=64, S=64 * 7 + 16, steps=70, rates=(0.5, 0.0625),
+                         step_rate=0.25, max_tokens_per_head=2048, g_defer=False, seed=4),
+}
+
+GATE_SCENARIOS = {
+    "llama_cfg1": dict(H=2, D=64, g_expand=4.0, S=384, seed=10),
+    "qwen3_like": dict(H=2, D=128, g_expand=1.5, S=96, seed=11),
+}
+
+
+def checksum(*tensors):
+    h = hashlib.sha256()
+    for t in tensors:
+        if t is None:
+            continue
+        a = t.detach().contiguous()
+        if a.dtype == torch.bfloat16:
+            a = a.view(torch.int16)
+        h.update(a.numpy().tobytes())
+    return h.hexdigest()
+
+
+def gate_params(H, D, g_expand, gen):
+    inner = int(D * g_expand)
+    b1 = 1.0 / np.sqrt(2 * D)
+    b2 = 1.0 / np.sqrt(inner)
+    return {
+        "pre_key_norm.weight": 1.0 + 0.1 * torch.randn(D, generator=gen),
+        "post_key_norm.weight": 1.0 + 0.1 * torch.randn(D, generator=gen),
+        "conv1.weight": (torch.rand(H * inner, 2 * D, 1, generator=gen) * 2 - 1) * b1,
+        "conv1.bias": (torch.rand(H * inner, generator=gen) * 2 - 1) * b1,
+        "conv2.weight": (torch.rand(H, inner, 1, generator=gen) * 2 - 1) * b2,
+        "conv2.bias": (torch.rand(H, generator=gen) * 2 - 1) * b2,
+    }
+
+
+def gate_inputs(sc):
+    gen = torch.Generator().manual_seed(sc["seed"])
+    H, D, S = sc["H"], sc["D"], sc["S"]
+    params = gate_params(H, D, sc["g_expand"], gen)
+    pre_k = torch.randn(1, H, S, D, generator=gen)
+    post_k = torch.randn(1, H, S, D, generator=gen)
+    value = torch.randn(1, H, S, D, generator=gen)
+    return params, pre_k, post_k, value
+
+
+def cache_inputs(sc):
+    """Prompt tensors, per-step tensors and masks for a cache scenario.
+
+    Returns dict with ``prompt`` = (q, pre_k, k, v, mask) and ``steps`` =
+    list of (q, pre_k, k, v, mask-or-None) per step, one entry per layer.
+    Masks are drawn directly (rate per head) so the cache logic is tested
+    independently of the gate; the deferred scenario re-gates with a gate of
+    ``gate_params`` whose bias is shifted per layer.
+    """
+    gen = torch.Generator().manual_seed(sc["seed"])
+    L, H, G, D, S = sc["L"], sc["H"], sc["G"], sc["D"], sc["S"]
+    Hq = H * G
+
+    def bf(*shape):
+        return torch.randn(*shape, generator=gen).to(torch.bfloat16)
+
+    prompt = []
+    for _ in range(L):
+        q, pk, k, v = bf(1, Hq, S, D), bf(1, H, S, D), bf(1, H, S, D), bf(1, H, S, D)
+        rates = torch.tensor(sc["rates"], dtype=torch.float32)[:H].view(1, H, 1)
+        mask = torch.rand(1, H, S, generator=gen) < rates
+        prompt.append((q, pk, k, v, mask))
+    steps = []
+    for _ in range(sc["steps"]):
+        per_layer = []
+        for _ in range(L):
+            q, pk, k, v = bf(1, Hq, 1, D), bf(1, H, 1, D), bf(1, H, 1, D), bf(1, H, 1, D)
+            mask = None
+            if sc["step_rate"] is not None:
+                mask = torch.rand(1, H, 1, generator=gen) < sc["step_rate"]
+            per_layer.append((q, pk, k, v, mask))
+        steps.append(per_layer)
+    gates = None
+    if sc["g_defer"]:
+        gates = []
+        for _ in range(L):
+            p = gate_params(H, D, 4.0, gen)
+            gates.append(p)
+    return {"prompt": prompt, "steps": steps, "gates": gates}
+
+
+def defer_bias_shift(gate_params_, shift=-0.25):
+    """A fixed bias shift so that a fraction of the window is re-admitted."""
+    p = {k: v.clone() for k, v in gate_params_.items()}
+    p["conv2.bias"] = p["conv2.bias"] + shift
+    return p
