@@ -1,0 +1,405 @@
+// Ragged paged decode attention over the dual cache (gfx950).
+//
+// Work split: the logical sequence of every (batch row b, KV head h) is cut
+// into 16-token sub-pages; sub-pages are grouped into chunks of `cp`
+// sub-pages (cp a multiple of 16, chosen on the device so that the whole
+// batch gives about kTargetChunks chunks).  One workgroup (4 waves) owns one
+// chunk, and its waves take 64-token "quads" (4 sub-pages) in turn.  Every
+// K/V byte of the cache is read exactly once, for all G query heads of the
+// KV head together.
+//
+// Per quad and wave:
+//   * K is read in the MFMA B-operand layout (lane n%16 = token row, lane/16
+//     = 16-byte slice of the row) and multiplied with the query heads on
+//     v_mfma_f32_16x16x32_bf16 (query head i replicated in rows 4r+i);
+//   * softmax runs in the log2 domain with one running max per query head,
+//     uniform over the wave, and a per-lane running denominator;
+//   * P goes through a 1 KB LDS slot per wave and V is read fully coalesced
+//     (consecutive 16-byte slices of consecutive rows) and accumulated on the
+//     VALU in fp32.
+// At the end of a chunk the 4 waves merge through LDS; a single-chunk head
+// writes its output directly, otherwise the chunk writes (m, l, acc) partials
+// that wgkv_decode_merge combines with the usual log-sum-exp rule.
+#include "wgkv_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+constexpr int kMaxBH = 2048;
+constexpr int kTargetChunks = 2048;
+constexpr int kMaxChunks = kTargetChunks + kMaxBH;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint16_t* kc;
+  const uint16_t* vc;
+  int64_t num_pages;
+  int page_size, page_shift;  // page_size = 16 << page_shift
+  const int32_t* seqlens;
+  int64_t sl_sb;
+  const int32_t* bt;
+  int64_t bt_sb, bt_sh;
+  int max_pages;
+  uint16_t* out;
+  int64_t out_sb, out_sh;
+  int B, Hkv;
+  float scale_log2;
+  float* part;  // [kMaxChunks][4] m, then [kMaxChunks][4] l, then [kMaxChunks][4][D] acc
+};
+
+__device__ __forceinline__ int clamped_tokens(const DecodeArgs& a, int bh) {
+  const int b = bh / a.Hkv, h = bh - b * a.Hkv;
+  int T = a.seqlens[(int64_t)b * a.sl_sb + h];
+  const int cap = a.max_pages * a.page_size;
+  T = T < 0 ? 0 : (T > cap ? cap : T);
+  return T;
+}
+
+// Device-side split planner (replaces the host planner of the reference,
+// src/modeling_layers.py:1032-1055).  Leaves s_pref[bh] = first chunk of
+// (b,h) and s_pref[BH] = number of chunks; returns cp.
+__device__ int build_plan(const DecodeArgs& a, int* s_pref, int* s_tmp) {
+  const int BH = a.B * a.Hkv;
+  const int t = threadIdx.x;
+  const int per = (BH + kThreads - 1) / kThreads;
+  const int lo = min(BH, t * per), hi = min(BH, lo + per);
+  int subs = 0;
+  for (int bh = lo; bh < hi; ++bh) subs += (clamped_tokens(a, bh) + 15) >> 4;
+  int total = 0;
+  block_exclusive_scan_256(subs, s_tmp, &total);
+  int cp = (total + kTargetChunks - 1) / kTargetChunks;
+  cp = max(16, (cp + 15) & ~15);
+  int chunks = 0;
+  for (int bh = lo; bh < hi; ++bh) {
+    const int ns = (clamped_tokens(a, bh) + 15) >> 4;
+    chunks += max(1, (ns + cp - 1) / cp);
+  }
+  int n_chunks = 0;
+  int run = block_exclusive_scan_256(chunks, s_tmp, &n_chunks);
+  for (int bh = lo; bh < hi; ++bh) {
+    s_pref[bh] = run;
+    const int ns = (clamped_tokens(a, bh) + 15) >> 4;
+    run += max(1, (ns + cp - 1) / cp);
+  }
+  if (t == 0) s_pref[BH] = n_chunks;
+  __syncthreads();
+  return cp;
+}
+
+__device__ __forceinline__ int find_owner(const int* s_pref, int BH, int w) {
+  int lo = 0, hi = BH - 1;  // largest bh with s_pref[bh] <= w
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_pref[mid] <= w) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// First pool row (token slot) of sub-page `sp` of a head; page ids outside
+// the pool are clamped so that a corrupt table cannot read out of bounds.
+__device__ __forceinline__ int64_t subpage_row(const DecodeArgs& a, const int32_t* bt_row, int sp) {
+  int pg = bt_row[sp >> a.page_shift];
+  pg = pg < 0 ? 0 : (pg >= a.num_pages ? (int)(a.num_pages - 1) : pg);
+  const int within = sp & ((1 << a.page_shift) - 1);
+  return (int64_t)pg * a.page_size + within * 16;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
+  constexpr int KS = D / 32;       // MFMA k-steps per row
+  constexpr int CH = D / 8;        // 16-byte slices per row
+  constexpr int RPI = 64 / CH;     // rows per coalesced V load
+  constexpr int NV = 64 / RPI;     // V loads per quad
+
+  __shared__ int s_pref[kMaxBH + 1];
+  __shared__ int s_tmp[kThreads];
+  __shared__ f32x4_t s_p[kWaves][64];
+  __shared__ float s_acc[kWaves][RPI][G][D];
+  __shared__ float s_ml[kWaves][2][4];
+
+  const int cp = build_plan(a, s_pref, s_tmp);
+  const int BH = a.B * a.Hkv;
+  const int w = blockIdx.x;
+  if (w >= s_pref[BH]) return;
+  const int bh = find_owner(s_pref, BH, w);
+  const int ci = w - s_pref[bh];
+  const int n_chunks_bh = s_pref[bh + 1] - s_pref[bh];
+  const int b = bh / a.Hkv, h = bh - b * a.Hkv;
+  const int T = clamped_tokens(a, bh);
+  const int nsub = (T + 15) >> 4;
+  const int s0 = ci * cp;
+  const int s1 = min(nsub, s0 + cp);
+  const int tok_end = min(T, s1 * 16);
+
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int32_t* bt_row = a.bt + (int64_t)b * a.bt_sb + (int64_t)h * a.bt_sh;
+
+  // Query heads as the MFMA A operand: row m holds head m%4 (zero if >= G).
+  bf16x8_t qa[KS];
+  {
+    const int qh = n & 3;
+    const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)(h * G + (qh < G ? qh : 0)) * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) {
+      u32x4_t v = *(const u32x4_t*)(qrow + (j * 4 + g) * 8);
+      if (qh >= G) v = (u32x4_t){0u, 0u, 0u, 0u};
+      qa[j] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+
+  float m_run[G], l_lane[G], acc[G][8];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    m_run[i] = -INFINITY;
+    l_lane[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[i][e] = 0.f;
+  }
+
+  const int nq = (s1 - s0 + 3) >> 2;
+  for (int jq = wid; jq < nq; jq += kWaves) {
+    const int sp0 = s0 + jq * 4;
+    int64_t off[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) off[p] = subpage_row(a, bt_row, min(sp0 + p, s1 - 1)) * D;
+
+    u32x4_t kr[4][KS];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int j = 0; j < KS; ++j)
+        kr[p][j] = *(const u32x4_t*)(a.kc + off[p] + n * D + (j * 4 + g) * 8);
+    u32x4_t vr[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int r = i * RPI + lane / CH;
+      const int p = (i * RPI) >> 4;
+      vr[i] = *(const u32x4_t*)(a.vc + off[p] + (r & 15) * D + (lane % CH) * 8);
+    }
+
+    f32x4_t c[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      c[p] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KS; ++j)
+        c[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[j], __builtin_bit_cast(bf16x8_t, kr[p][j]), c[p], 0, 0, 0);
+    }
+
+    const bool ok = (sp0 + g) * 16 + n < tok_end;
+    float s[G], pr[4];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float x = g == 0 ? c[0][i] : g == 1 ? c[1][i] : g == 2 ? c[2][i] : c[3][i];
+      s[i] = ok ? x * a.scale_log2 : -INFINITY;
+    }
+    bool grew = false;
+    float alpha[G];
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float mn = fmaxf(m_run[i], wave_max(s[i]));
+      grew |= mn > m_run[i];
+      alpha[i] = fast_exp2(m_run[i] - mn);
+      m_run[i] = mn;
+    }
+    if (grew) {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        l_lane[i] *= alpha[i];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[i][e] *= alpha[i];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      pr[i] = fast_exp2(s[i] - m_run[i]);
+      l_lane[i] += pr[i];
+    }
+    s_p[wid][g * 16 + n] = (f32x4_t){pr[0], pr[1], pr[2], pr[3]};
+    wave_lds_sync();
+
+    const bool full = sp0 * 16 + 64 <= tok_end;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int r = i * RPI + lane / CH;
+      const f32x4_t pp = s_p[wid][r];
+      u32x4_t v = vr[i];
+      if (!full && sp0 * 16 + r >= tok_end) v = (u32x4_t){0u, 0u, 0u, 0u};
+      float vf[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vf[2 * e] = bf16lo(v[e]);
+        vf[2 * e + 1] = bf16hi(v[e]);
+      }
+#pragma unroll
+      for (int qi = 0; qi < G; ++qi)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[qi][e] = fmaf(pp[qi], vf[e], acc[qi][e]);
+    }
+    wave_lds_sync();
+  }
+
+  // ---- merge the 4 waves ---------------------------------------------------
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const float lw = wave_sum(l_lane[i]);
+    if (lane == 0) {
+      s_ml[wid][0][i] = m_run[i];
+      s_ml[wid][1][i] = lw;
+    }
+  }
+  {
+    const int slot = lane / CH, cc = lane % CH;
+#pragma unroll
+    for (int i = 0; i < G; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_acc[wid][slot][i][cc * 8 + e] = acc[i][e];
+  }
+  __syncthreads();
+
+  float* part_m = a.part;
+  float* part_l = a.part + kMaxChunks * 4;
+  float* part_acc = a.part + kMaxChunks * 8;
+  for (int v = threadIdx.x; v < G * D; v += kThreads) {
+    const int i = v / D, d = v - i * D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_ml[ww][0][i]);
+    float L = 0.f, A = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kWaves; ++ww) {
+      const float mw = s_ml[ww][0][i];
+      if (mw == -INFINITY) continue;
+      const float sc = fast_exp2(mw - M);
+      float sum = 0.f;
+#pragma unroll
+      for (int sl = 0; sl < RPI; ++sl) sum += s_acc[ww][sl][i][d];
+      L = fmaf(sc, s_ml[ww][1][i], L);
+      A = fmaf(sc, sum, A);
+    }
+    if (n_chunks_bh == 1) {
+      const float o = L > 0.f ? A / L : 0.f;
+      a.out[(int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d] = f32_to_bf16(o);
+    } else {
+      if (d == 0) {
+        part_m[w * 4 + i] = M;
+        part_l[w * 4 + i] = L;
+      }
+      part_acc[((int64_t)w * 4 + i) * D + d] = A;
+    }
+  }
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
+  __shared__ int s_pref[kMaxBH + 1];
+  __shared__ int s_tmp[kThreads];
+  build_plan(a, s_pref, s_tmp);
+  const int bh = blockIdx.x;
+  const int c0 = s_pref[bh], c1 = s_pref[bh + 1];
+  if (c1 - c0 <= 1) return;  // written directly by the split kernel
+  const int b = bh / a.Hkv, h = bh - b * a.Hkv;
+  const float* part_m = a.part;
+  const float* part_l = a.part + kMaxChunks * 4;
+  const float* part_acc = a.part + kMaxChunks * 8;
+  for (int v = threadIdx.x; v < G * D; v += kThreads) {
+    const int i = v / D, d = v - i * D;
+    float M = -INFINITY;
+    for (int c = c0; c < c1; ++c) M = fmaxf(M, part_m[c * 4 + i]);
+    float L = 0.f, A = 0.f;
+    for (int c = c0; c < c1; ++c) {
+      const float mc = part_m[c * 4 + i];
+      if (mc == -INFINITY) continue;
+      const float sc = fast_exp2(mc - M);
+      L = fmaf(sc, part_l[c * 4 + i], L);
+      A = fmaf(sc, part_acc[((int64_t)c * 4 + i) * D + d], A);
+    }
+    const float o = L > 0.f ? A / L : 0.f;
+    a.out[(int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d] = f32_to_bf16(o);
+  }
+}
+
+template <int D, int G>
+hipError_t launch(const DecodeArgs& a, hipStream_t st) {
+  const int BH = a.B * a.Hkv;
+  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(kTargetChunks + BH), dim3(kThreads), 0, st, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" size_t wgkv_paged_decode_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t head_dim) {
+  (void)batch;
+  (void)num_kv_heads;
+  return (size_t)kMaxChunks * 4 * (2 + (size_t)(head_dim > 0 ? head_dim : 0)) * sizeof(float);
+}
+
+extern "C" int wgkv_paged_decode_attn(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h,
+    const void* k_cache, const void* v_cache, int64_t num_pages, int32_t page_size,
+    const int32_t* cache_seqlens, int64_t sl_stride_b,
+    const int32_t* block_table, int64_t bt_stride_b, int64_t bt_stride_h, int32_t max_pages,
+    void* out, int64_t out_stride_b, int64_t out_stride_h,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale,
+    void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (!q || !k_cache || !v_cache || !cache_seqlens || !block_table || !out) return WGKV_ERR_ARG;
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 || num_pages <= 0 || max_pages <= 0) return WGKV_ERR_ARG;
+  if (num_q_heads % num_kv_heads) return WGKV_ERR_ARG;
+  if ((int64_t)batch * num_kv_heads > kMaxBH) return WGKV_ERR_UNSUPPORTED;
+  const int G = num_q_heads / num_kv_heads;
+  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (G != 1 && G != 2 && G != 4) return WGKV_ERR_UNSUPPORTED;
+  int shift;
+  if (page_size == 16) shift = 0;
+  else if (page_size == 32) shift = 1;
+  else if (page_size == 64) shift = 2;
+  else return WGKV_ERR_UNSUPPORTED;
+  // 16-byte vector loads: rows and bases must be 16-byte aligned.
+  if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15) return WGKV_ERR_UNSUPPORTED;
+  if ((q_stride_b | q_stride_h) & 7) return WGKV_ERR_UNSUPPORTED;
+  if (!workspace || workspace_bytes < wgkv_paged_decode_workspace_bytes(batch, num_kv_heads, head_dim))
+    return WGKV_ERR_WORKSPACE;
+
+  DecodeArgs a;
+  a.q = (const uint16_t*)q;
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.kc = (const uint16_t*)k_cache;
+  a.vc = (const uint16_t*)v_cache;
+  a.num_pages = num_pages;
+  a.page_size = page_size;
+  a.page_shift = shift;
+  a.seqlens = cache_seqlens;
+  a.sl_sb = sl_stride_b;
+  a.bt = block_table;
+  a.bt_sb = bt_stride_b;
+  a.bt_sh = bt_stride_h;
+  a.max_pages = max_pages;
+  a.out = (uint16_t*)out;
+  a.out_sb = out_stride_b;
+  a.out_sh = out_stride_h;
+  a.B = batch;
+  a.Hkv = num_kv_heads;
+  a.scale_log2 = softmax_scale * kLog2e;
+  a.part = (float*)workspace;
+
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (head_dim == 128) {
+    e = G == 4 ? launch<128, 4>(a, st) : G == 2 ? launch<128, 2>(a, st) : launch<128, 1>(a, st);
+  } else {
+    e = G == 4 ? launch<64, 4>(a, st) : G == 2 ? launch<64, 2>(a, st) : launch<64, 1>(a, st);
+  }
+  return e == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}

@@ -1,0 +1,107 @@
+// Shared device helpers for the write-gated dual-cache kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/wgkv.h"
+
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+
+#define WGKV_DEVICE __device__ __forceinline__
+
+// ---- bf16 <-> f32 ---------------------------------------------------------
+// A bf16 value is the high half of an f32, so widening is a shift / mask.
+WGKV_DEVICE float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+WGKV_DEVICE float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even f32 -> bf16 (NaN kept quiet).
+WGKV_DEVICE uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ---- DPP row (16-lane) reductions -----------------------------------------
+// quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_half_mirror, row_mirror: after
+// the four steps every lane of a 16-lane row holds the row-wide result.
+#define WGKV_DPP_QP_1032 0xB1
+#define WGKV_DPP_QP_2301 0x4E
+#define WGKV_DPP_ROW_MIRROR 0x140
+#define WGKV_DPP_ROW_HALF_MIRROR 0x141
+
+template <int CTRL>
+WGKV_DEVICE float dpp_f32(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, false));
+}
+
+WGKV_DEVICE float row_max16(float x) {
+  x = fmaxf(x, dpp_f32<WGKV_DPP_QP_1032>(x));
+  x = fmaxf(x, dpp_f32<WGKV_DPP_QP_2301>(x));
+  x = fmaxf(x, dpp_f32<WGKV_DPP_ROW_HALF_MIRROR>(x));
+  x = fmaxf(x, dpp_f32<WGKV_DPP_ROW_MIRROR>(x));
+  return x;
+}
+
+WGKV_DEVICE float row_sum16(float x) {
+  x += dpp_f32<WGKV_DPP_QP_1032>(x);
+  x += dpp_f32<WGKV_DPP_QP_2301>(x);
+  x += dpp_f32<WGKV_DPP_ROW_HALF_MIRROR>(x);
+  x += dpp_f32<WGKV_DPP_ROW_MIRROR>(x);
+  return x;
+}
+
+// Wave-uniform max / sum over all 64 lanes.
+WGKV_DEVICE float wave_max(float x) {
+  x = row_max16(x);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+WGKV_DEVICE float wave_sum(float x) {
+  x = row_sum16(x);
+  float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+  float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+  float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+  float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+  return (a + b) + (c + d);
+}
+
+WGKV_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Orders this wave's LDS writes before its later LDS reads of other lanes'
+// data (LDS operations of one wave complete in issue order).
+WGKV_DEVICE void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Block-wide exclusive scan of one int per thread (blockDim.x == 256).
+WGKV_DEVICE int block_exclusive_scan_256(int v, int* s_tmp /* >= 256 ints */, int* total) {
+  const int t = threadIdx.x;
+  s_tmp[t] = v;
+  __syncthreads();
+  for (int off = 1; off < 256; off <<= 1) {
+    int add = t >= off ? s_tmp[t - off] : 0;
+    __syncthreads();
+    s_tmp[t] += add;
+    __syncthreads();
+  }
+  int incl = s_tmp[t];
+  if (total) *total = s_tmp[255];
+  __syncthreads();
+  return incl - v;
+}
+
+#define WGKV_HIP_CHECK(expr)                       \
+  do {                                             \
+    hipError_t _e = (expr);                        \
+    if (_e != hipSuccess) return WGKV_ERR_HIP;     \
+  } while (0)

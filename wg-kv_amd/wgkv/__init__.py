@@ -1,0 +1,24 @@
+"""MI355X-native write-gated dual-cache KV path (WG-KV hot path).
+
+Host side of the path: the reference's layer/cache API on top of the HIP
+C-ABI library ``libwgkv.so`` (include/wgkv.h).  Device work always goes
+through that library; there is no CPU fallback.
+"""
+from . import _lib, ops  # noqa: F401
+from .ops import (  # noqa: F401
+    flash_attn_with_kvcache_wrapper,
+    flash_attn_with_kvcache_wrapper_handle,
+    flash_attn_with_kvcache_wrapper_triton,
+    flash_attn_with_kvcache_wrapper_triton_handle,
+    paged_decode_attn,
+    paged_decode_attn_handle,
+)
+
+__all__ = [
+    "paged_decode_attn",
+    "paged_decode_attn_handle",
+    "flash_attn_with_kvcache_wrapper",
+    "flash_attn_with_kvcache_wrapper_handle",
+    "flash_attn_with_kvcache_wrapper_triton",
+    "flash_attn_with_kvcache_wrapper_triton_handle",
+]

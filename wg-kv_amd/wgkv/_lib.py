@@ -1,0 +1,92 @@
+"""ctypes binding of the C ABI in include/wgkv.h.
+
+torch is imported first so that the library binds to the HIP runtime torch
+already loaded (both carry the SONAME libamdhip64.so.7); a second runtime in
+the process would not share device memory or streams with torch.
+
+There is no fallback: if the library is missing, every operation raises.
+"""
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede loading libwgkv.so)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libwgkv.so")
+
+OK = 0
+ERR_ARG = 1
+ERR_UNSUPPORTED = 2
+ERR_CAPACITY = 3
+ERR_WORKSPACE = 4
+ERR_HIP = 5
+
+c_i32 = ctypes.c_int32
+c_i64 = ctypes.c_int64
+c_ptr = ctypes.c_void_p
+c_f32 = ctypes.c_float
+c_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); kept in the order of include/wgkv.h
+SIGNATURES = {
+    "wgkv_version": (ctypes.c_int, []),
+    "wgkv_status_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "wgkv_paged_decode_workspace_bytes": (c_size, [c_i32, c_i32, c_i32]),
+    "wgkv_paged_decode_attn": (ctypes.c_int, [
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_ptr, c_i64, c_i32,
+        c_ptr, c_i64,
+        c_ptr, c_i64, c_i64, c_i32,
+        c_ptr, c_i64, c_i64,
+        c_i32, c_i32, c_i32, c_i32,
+        c_f32,
+        c_ptr, c_size,
+        c_ptr]),
+}
+
+_lib = None
+
+
+class WGKVError(RuntimeError):
+    def __init__(self, status, where):
+        self.status = status
+        super().__init__(f"{where}: {status_string(status)} (status {status})")
+
+
+class WGKVCapacityError(WGKVError, AssertionError):
+    """Raised for cache overflow; an AssertionError like the reference's asserts."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"HIP library {LIB_PATH} is not built; run __graft_entry__.build() "
+                "(python -c 'import __graft_entry__ as g; g.build()') first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def status_string(status):
+    return lib().wgkv_status_string(status).decode()
+
+
+def check(status, where):
+    if status == OK:
+        return
+    if status == ERR_CAPACITY:
+        raise WGKVCapacityError(status, where)
+    if status in (ERR_UNSUPPORTED,):
+        raise WGKVError(status, where)
+    raise WGKVError(status, where)
+
+
+def stream_handle(device=None):
+    """hipStream_t of torch's current stream on ``device``."""
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
