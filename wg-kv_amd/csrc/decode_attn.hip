@@ -48,6 +48,7 @@ struct DecodeArgs {
   int B, Hkv;
   float scale_log2;
   float* part;  // [kMaxChunks][4] m, then [kMaxChunks][4] l, then [kMaxChunks][4][D] acc
+  int* plan;    // [kMaxBH + 1] first chunk of each (b,h), written by the split kernel
 };
 
 __device__ __forceinline__ int clamped_tokens(const DecodeArgs& a, int bh) {
@@ -107,8 +108,37 @@ __device__ __forceinline__ int64_t subpage_row(const DecodeArgs& a, const int32_
   return (int64_t)pg * a.page_size + within * 16;
 }
 
+// K of 4 sub-pages in the MFMA B-operand layout: lane (n, g) holds row n,
+// 16-byte slice j*4+g, for k-step j.  K/V are streamed once, so the loads are
+// non-temporal.
+template <int D>
+__device__ __forceinline__ void load_k(const DecodeArgs& a, u32x4_t (&kr)[4][D / 32], const int64_t (&off)[4],
+                                       int n, int g) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p)
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j)
+      kr[p][j] = __builtin_nontemporal_load((const u32x4_t*)(a.kc + off[p] + n * D + (j * 4 + g) * 8));
+}
+
+// V of 4 sub-pages, fully coalesced: load i covers rows i*RPI .. i*RPI+RPI-1
+// of the quad, lane -> (row lane/CH, 16-byte slice lane%CH).
+template <int D>
+__device__ __forceinline__ void load_v(const DecodeArgs& a, u32x4_t (&vr)[D / 8], const int64_t (&off)[4],
+                                       int lane) {
+  constexpr int CH = D / 8, RPI = 64 / CH;
+#pragma unroll
+  for (int i = 0; i < 64 / RPI; ++i) {
+    const int r = i * RPI + lane / CH;
+    const int p = (i * RPI) >> 4;
+    vr[i] = __builtin_nontemporal_load((const u32x4_t*)(a.vc + off[p] + (r & 15) * D + (lane % CH) * 8));
+  }
+}
+
 template <int D, int G>
-__global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
+// 165 registers at D=128, G=4: three waves per SIMD (measured faster than two).
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_split_kernel(
+    DecodeArgs a) {
   constexpr int KS = D / 32;       // MFMA k-steps per row
   constexpr int CH = D / 8;        // 16-byte slices per row
   constexpr int RPI = 64 / CH;     // rows per coalesced V load
@@ -122,6 +152,8 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
 
   const int cp = build_plan(a, s_pref, s_tmp);
   const int BH = a.B * a.Hkv;
+  if (blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= BH; i += kThreads) a.plan[i] = s_pref[i];
   const int w = blockIdx.x;
   if (w >= s_pref[BH]) return;
   const int bh = find_owner(s_pref, BH, w);
@@ -166,20 +198,10 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
     int64_t off[4];
 #pragma unroll
     for (int p = 0; p < 4; ++p) off[p] = subpage_row(a, bt_row, min(sp0 + p, s1 - 1)) * D;
-
     u32x4_t kr[4][KS];
-#pragma unroll
-    for (int p = 0; p < 4; ++p)
-#pragma unroll
-      for (int j = 0; j < KS; ++j)
-        kr[p][j] = *(const u32x4_t*)(a.kc + off[p] + n * D + (j * 4 + g) * 8);
     u32x4_t vr[NV];
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int r = i * RPI + lane / CH;
-      const int p = (i * RPI) >> 4;
-      vr[i] = *(const u32x4_t*)(a.vc + off[p] + (r & 15) * D + (lane % CH) * 8);
-    }
+    load_k<D>(a, kr, off, n, g);
+    load_v<D>(a, vr, off, lane);
 
     f32x4_t c[4];
 #pragma unroll
@@ -296,32 +318,74 @@ __global__ __launch_bounds__(kThreads) void decode_split_kernel(DecodeArgs a) {
   }
 }
 
+// Log-sum-exp merge of a head's chunk partials in one pass: each thread keeps
+// a running (max, sum, acc) over its share of the chunks (all loads of the
+// pass are independent), then the shares are combined through LDS.  The plan
+// comes from the split kernel, which ran before on the same stream.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
-  __shared__ int s_pref[kMaxBH + 1];
-  __shared__ int s_tmp[kThreads];
-  build_plan(a, s_pref, s_tmp);
+  constexpr int NQ = G * D / 4;          // float4 quads of the output row
+  constexpr int GROUPS = kThreads / NQ;  // chunk groups summed in parallel
+  __shared__ f32x4_t s_a[kThreads];
+  __shared__ float s_m[kThreads], s_l[kThreads];
   const int bh = blockIdx.x;
-  const int c0 = s_pref[bh], c1 = s_pref[bh + 1];
+  const int c0 = a.plan[bh], c1 = a.plan[bh + 1];
   if (c1 - c0 <= 1) return;  // written directly by the split kernel
   const int b = bh / a.Hkv, h = bh - b * a.Hkv;
   const float* part_m = a.part;
   const float* part_l = a.part + kMaxChunks * 4;
   const float* part_acc = a.part + kMaxChunks * 8;
-  for (int v = threadIdx.x; v < G * D; v += kThreads) {
-    const int i = v / D, d = v - i * D;
-    float M = -INFINITY;
-    for (int c = c0; c < c1; ++c) M = fmaxf(M, part_m[c * 4 + i]);
-    float L = 0.f, A = 0.f;
-    for (int c = c0; c < c1; ++c) {
-      const float mc = part_m[c * 4 + i];
-      if (mc == -INFINITY) continue;
-      const float sc = fast_exp2(mc - M);
-      L = fmaf(sc, part_l[c * 4 + i], L);
-      A = fmaf(sc, part_acc[((int64_t)c * 4 + i) * D + d], A);
+  const int t = threadIdx.x;
+  const int vq = t % NQ, grp = t / NQ;
+  const int i = (vq * 4) / D;
+
+  // Chunks are read in batches of kBatch with every load issued before the
+  // (branch-free) online update consumes them.
+  constexpr int kBatch = 8;
+  float M = -INFINITY, L = 0.f;
+  f32x4_t A = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  for (int cb = c0 + grp; cb < c1; cb += GROUPS * kBatch) {
+    float mc[kBatch], lc[kBatch];
+    f32x4_t ac[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int c = min(cb + k * GROUPS, c1 - 1);
+      mc[k] = part_m[c * 4 + i];
+      lc[k] = part_l[c * 4 + i];
+      ac[k] = *(const f32x4_t*)(part_acc + (int64_t)c * 4 * D + vq * 4);
     }
-    const float o = L > 0.f ? A / L : 0.f;
-    a.out[(int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d] = f32_to_bf16(o);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const bool valid = cb + k * GROUPS < c1 && mc[k] != -INFINITY;
+      const float mn = valid ? fmaxf(M, mc[k]) : M;
+      const float sa = M == -INFINITY ? 0.f : fast_exp2(M - mn);
+      const float sb = valid ? fast_exp2(mc[k] - mn) : 0.f;
+      L = L * sa + lc[k] * sb;
+      A = A * sa + ac[k] * sb;
+      M = mn;
+    }
+  }
+  s_m[t] = M;
+  s_l[t] = L;
+  s_a[t] = A;
+  __syncthreads();
+  if (t < NQ) {
+    float Mx = -INFINITY;
+    for (int gg = 0; gg < GROUPS; ++gg) Mx = fmaxf(Mx, s_m[gg * NQ + t]);
+    float Lt = 0.f;
+    f32x4_t At = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int gg = 0; gg < GROUPS; ++gg) {
+      const float mg = s_m[gg * NQ + t];
+      if (mg == -INFINITY) continue;
+      const float sc = fast_exp2(mg - Mx);
+      Lt += sc * s_l[gg * NQ + t];
+      At += sc * s_a[gg * NQ + t];
+    }
+    const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+    const int d = vq * 4 - i * D;
+    uint16_t* o = a.out + (int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(Lt > 0.f ? At[e] * inv : 0.f);
   }
 }
 
@@ -340,7 +404,8 @@ hipError_t launch(const DecodeArgs& a, hipStream_t st) {
 extern "C" size_t wgkv_paged_decode_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t head_dim) {
   (void)batch;
   (void)num_kv_heads;
-  return (size_t)kMaxChunks * 4 * (2 + (size_t)(head_dim > 0 ? head_dim : 0)) * sizeof(float);
+  return (size_t)kMaxChunks * 4 * (2 + (size_t)(head_dim > 0 ? head_dim : 0)) * sizeof(float) +
+         (size_t)(kMaxBH + 1) * sizeof(int);
 }
 
 extern "C" int wgkv_paged_decode_attn(
@@ -393,6 +458,7 @@ extern "C" int wgkv_paged_decode_attn(
   a.Hkv = num_kv_heads;
   a.scale_log2 = softmax_scale * kLog2e;
   a.part = (float*)workspace;
+  a.plan = (int*)((char*)workspace + (size_t)kMaxChunks * 4 * (2 + head_dim) * sizeof(float));
 
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
