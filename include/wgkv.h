@@ -69,6 +69,91 @@ int wgkv_paged_decode_attn(
     void* workspace, size_t workspace_bytes,
     void* stream);
 
+/* ------------------------------------------------------------------------
+ * Vertical-slash metadata of the sparse prefill, built on the device.
+ *
+ * Replaces generate_sparse_indices (src/modeling_layers.py:384-409) with its
+ * helpers generate_block_offset (:321-349) and generate_column_index
+ * (:352-381); same outputs, no host synchronisation:
+ *   g_mask        u8 (B, Hkv, S)  strides gm_stride_b, gm_stride_h; s contiguous
+ *   block_count   i32 (R)          R = ceil(S / block)
+ *   block_offset  i32 (R, P+1)     P = min(W / block, R)
+ *   column_count  i32 (B, Hkv, R)  admitted positions < r*block - W + 1 (0 for r < P)
+ *   column_index  i32 (B, Hkv, col_cap)  admitted positions < 1 + block*((S-1)/block),
+ *                                  ascending; entries past a head's count are unspecified
+ *   column_total  i32 (B, Hkv) or NULL: number of listed positions per head
+ * The reference sizes column_index to the largest per-head count (a host
+ * sync); here the caller passes col_cap (S always suffices) and positions past
+ * col_cap are dropped.  W must be a multiple of block (reference :394).
+ * ---------------------------------------------------------------------- */
+int wgkv_build_prefill_meta(
+    const uint8_t* g_mask, int64_t gm_stride_b, int64_t gm_stride_h,
+    int32_t batch, int32_t num_kv_heads, int32_t seq_len, int32_t local_window, int32_t block,
+    int32_t* block_count, int32_t* block_offset,
+    int32_t* column_count, int32_t* column_index, int32_t col_cap, int32_t* column_total,
+    void* stream);
+
+/* ------------------------------------------------------------------------
+ * Dual cache: pool of total_pages pages of page_size rows of head_dim bf16,
+ * one pool for K and one for V (reference layout, src/modeling_layers.py:
+ * 1209-1216).  Local pages of (layer l, head h) are the first W/page entries
+ * of block_table[l][h] and hold ring slot s at pool row (l*H + h)*W + s
+ * (:1265-1271, :1282-1284).  block_table is (L, H, max_pages_per_head)
+ * contiguous, global_lengths (L, H), local_is_global u8 (L, H, W),
+ * local_pre_key bf16 (L, H, W, D) or NULL, next_free_block a device int32.
+ * On a capacity failure nothing is written and *status = WGKV_ERR_CAPACITY
+ * (the caller reads status when it needs to raise).
+ * ---------------------------------------------------------------------- */
+
+/* Prefill admission of one layer, batch 1 (the reference's inference batch,
+ * :1614).  Replaces the local-ring write (:1290-1300) and the per-head global
+ * scatter loop (:1302-1331) of prefill_wrapper:
+ *   key/value   bf16 (H, S, D)  strides kv_stride_h, kv_stride_s; d contiguous
+ *   pre_key     bf16 (H, S, D)  or NULL (stored in local_pre_key when given)
+ *   g_mask      u8 (H, S)       admission flags (g > threshold)
+ * Admitted positions of [0, S-W) are compacted in ascending order into fresh
+ * contiguous pages bump-allocated in head order from *next_free_block; the
+ * last min(S, W) positions fill ring slots 0.. with their flags.  Capacity:
+ * min(S,W) + admitted <= max_tokens_per_head per head with admissions, and
+ * the pages fit in total_pages (:1312-1321). */
+size_t wgkv_prefill_admit_workspace_bytes(int32_t num_kv_heads, int32_t seq_len);
+
+int wgkv_prefill_admit(
+    const void* key, const void* value, int64_t kv_stride_h, int64_t kv_stride_s,
+    const void* pre_key, int64_t pk_stride_h, int64_t pk_stride_s,
+    const uint8_t* g_mask, int64_t gm_stride_h,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t seq_len, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
+    int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
+    int32_t* next_free_block, int32_t* status,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Decode-step cache update.
+ * do_migrate: lazy promotion, replacing migrate_local_kv_to_global (:674-763):
+ *   ring slot local_ptr of every (layer, head) flagged in local_is_global is
+ *   appended to that head's global pages; a new page is bump-allocated when
+ *   the global length is a multiple of page_size, in row-major (layer, head)
+ *   order; capacity W + len + 1 <= max_tokens_per_head and total_pages.
+ * do_write: the ring write of decode_wrapper (:1390-1413) for `layer`:
+ *   key/value bf16 (H, D) (stride kv_stride_h) go to slot local_length if the
+ *   ring is filling, else local_ptr; g_mask u8 (H) sets the slot's flag, or,
+ *   if g_mask is NULL (deferred gating), pre_key (H, D) is stored in
+ *   local_pre_key; cache_seqlens i32 (H) (may be NULL) receives
+ *   min(local_length+1, W) + global_lengths[layer] (:1429-1432).
+ * local_ptr / local_length are the host-side ring state before this step. */
+int wgkv_decode_append(
+    const void* key, const void* value, int64_t kv_stride_h,
+    const void* pre_key, int64_t pk_stride_h,
+    const uint8_t* g_mask,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
+    int32_t local_ptr, int32_t local_length, int32_t do_migrate, int32_t do_write,
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
+    int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
+    int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,11 +10,13 @@ from .ops import (  # noqa: F401
     flash_attn_with_kvcache_wrapper_handle,
     flash_attn_with_kvcache_wrapper_triton,
     flash_attn_with_kvcache_wrapper_triton_handle,
+    generate_sparse_indices,
     paged_decode_attn,
     paged_decode_attn_handle,
 )
 
 __all__ = [
+    "generate_sparse_indices",
     "paged_decode_attn",
     "paged_decode_attn_handle",
     "flash_attn_with_kvcache_wrapper",

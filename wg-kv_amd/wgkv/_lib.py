@@ -42,6 +42,34 @@ SIGNATURES = {
         c_f32,
         c_ptr, c_size,
         c_ptr]),
+    "wgkv_build_prefill_meta": (ctypes.c_int, [
+        c_ptr, c_i64, c_i64,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_ptr, c_ptr,
+        c_ptr, c_ptr, c_i32, c_ptr,
+        c_ptr]),
+    "wgkv_prefill_admit_workspace_bytes": (c_size, [c_i32, c_i32]),
+    "wgkv_prefill_admit": (ctypes.c_int, [
+        c_ptr, c_ptr, c_i64, c_i64,
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_i64,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32, c_i64,
+        c_ptr, c_ptr, c_ptr, c_i32,
+        c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr,
+        c_ptr, c_size, c_ptr]),
+    "wgkv_decode_append": (ctypes.c_int, [
+        c_ptr, c_ptr, c_i64,
+        c_ptr, c_i64,
+        c_ptr,
+        c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32, c_i64,
+        c_i32, c_i32, c_i32, c_i32,
+        c_ptr, c_ptr, c_ptr, c_i32,
+        c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr, c_ptr,
+        c_ptr]),
 }
 
 _lib = None

@@ -1,0 +1,81 @@
+"""The dual cache: one paged pool shared by the local ring and the per-head
+global caches of every (layer, KV head).
+
+Attribute names, dtypes and shapes are those the reference's prefill_wrapper
+sets on its cache object (src/modeling_layers.py:1196-1288), so harnesses
+that read them (scripts/profiling.py:150-184) work unchanged:
+
+* ``block_table``  int32 (L, Hkv, ceil(max_tokens_per_head/16)), sentinel total_blocks-1
+* ``block_pool_k`` / ``block_pool_v``  (total_blocks*16, D) in the K/V dtype
+* ``local_is_global`` bool (L, Hkv, W); ``global_lengths`` int32 (L, Hkv)
+* ``local_region_starts`` int32 (L, Hkv) = (l*Hkv + h) * W
+* ``local_ptr``, ``local_length`` host ints; ``total_blocks`` host int
+* ``local_pre_key`` (L, Hkv, W, D) when gating is deferred
+
+The bump pointer lives on the device (``next_free_block_dev``) so that no
+decode step synchronises with the host; ``next_free_block`` reads it back.
+``status`` is a device int32 set to a non-zero code by a kernel that found
+the cache full (and then wrote nothing).
+"""
+import torch
+
+from . import _lib
+
+
+class DualCache:
+    """Cache object for gating_mode 3; pass it as ``past_key_value``."""
+
+    def __init__(self):
+        self.gated_kv_initialized = False
+
+    # -- set up at layer-0 prefill, as the reference does (:1196-1288) -----
+    def initialize(self, config, head_dim, dtype, device):
+        if self.gated_kv_initialized:
+            raise AssertionError("dual cache is already initialised")  # reference :1197
+        L = config.num_hidden_layers
+        H = config.num_key_value_heads
+        W = config.local_window_size
+        P = config.block_size
+        if W % P:
+            raise AssertionError("local_window_size % block_size != 0")
+        lb = W // P
+        self.num_layers, self.num_kv_heads, self.head_dim = L, H, head_dim
+        self.local_window_size, self.block_size = W, P
+        self.max_tokens_per_head = config.max_tokens_per_head
+        self.total_blocks = (config.max_total_tokens + P - 1) // P
+        max_blocks_per_head = (config.max_tokens_per_head + P - 1) // P
+        n_local = L * H * lb
+        if n_local >= self.total_blocks:
+            raise AssertionError("max_total_tokens cannot hold the local windows")
+        i32 = dict(dtype=torch.int32, device=device)
+        self.block_table = torch.full((L, H, max_blocks_per_head), self.total_blocks - 1, **i32)
+        self.block_table[:, :, :lb] = torch.arange(n_local, **i32).view(L, H, lb)
+        self.block_pool_k = torch.empty(self.total_blocks * P, head_dim, dtype=dtype, device=device)
+        self.block_pool_v = torch.empty(self.total_blocks * P, head_dim, dtype=dtype, device=device)
+        self.local_is_global = torch.zeros(L, H, W, dtype=torch.bool, device=device)
+        self.global_lengths = torch.zeros(L, H, **i32)
+        self.local_region_starts = ((torch.arange(L, **i32)[:, None] * H + torch.arange(H, **i32)[None, :]) * W)
+        self.local_pre_key = (torch.empty(L, H, W, head_dim, dtype=dtype, device=device)
+                              if getattr(config, "g_defer", False) else None)
+        self.local_ptr = 0
+        self.local_length = 0
+        self.next_free_block_dev = torch.full((1,), n_local, **i32)
+        self.status = torch.zeros(1, **i32)
+        self.cache_seqlens = torch.zeros(L, 1, H, **i32)   # decode lengths, one row per layer
+        self.gated_kv_initialized = True
+
+    @property
+    def next_free_block(self):
+        return int(self.next_free_block_dev.item())
+
+    def raise_if_failed(self, where):
+        code = int(self.status.item())
+        if code:
+            self.status.zero_()
+            raise _lib.WGKVCapacityError(code, where)
+
+    def k_cache(self):
+        return self.block_pool_k.view(self.total_blocks, self.block_size, self.head_dim)
+
+    def v_cache(self):
+        return self.block_pool_v.view(self.total_blocks, self.block_size, self.head_dim)

@@ -1,0 +1,195 @@
+"""Write-gated attention functions behind the reference's swap points.
+
+The reference binds these as function attributes of its attention module
+(src/modeling_llama.py:240-250) and calls them with an explicit ``self``:
+``self_attn_forward_patch``, ``prefill_wrapper``, ``decode_wrapper``,
+``prefill_kernel``, ``decode_kernel_handle``, ``decode_kernel_executor``.
+Same names, signatures and call order here; the device work goes through the
+HIP library (kernels (1)-(4)).  ``self`` needs ``config``, ``layer_idx``,
+``head_dim``, ``scaling``, ``num_key_value_groups`` and the attributes above
+(and ``g_predictors`` when the gate is learned).
+
+Only inference (gating_mode 3) is on the hot path; the training modes and the
+comparison baselines (DuoAttention, AdaEA, QUEST, SnapKV) are outside it and
+raise NotImplementedError.
+"""
+from dataclasses import dataclass, field
+from typing import List, Optional
+
+import torch
+
+from . import ops
+from .cache import DualCache
+
+
+@dataclass
+class WGKVConfig:
+    """The configuration fields the path reads, with the reference's names and
+    defaults (src/configuration_llama.py:185-214; Qwen3 differs only in
+    g_expand = 1.5, src/configuration_qwen3.py:183)."""
+    hidden_size: int = 4096
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    head_dim: Optional[int] = None
+    rope_theta: float = 10000.0
+    attention_bias: bool = False
+    local_window_size: int = 256
+    g_inputs: List[str] = field(default_factory=lambda: ["pre_k", "post_k"])
+    g_act_fn: str = "gelu"
+    g_expand: float = 4.0
+    g_epsilon: float = 1e-3
+    g_rms: bool = True
+    g_threshold: float = 0.1
+    use_baseline: bool = False
+    block_size: int = 16
+    max_total_tokens: Optional[int] = None
+    max_tokens_per_head: Optional[int] = None
+    random_sparsity: Optional[float] = None
+    g_fast_path: bool = False
+    g_defer: bool = False
+    use_triton_kernel: bool = False
+    use_duo_attn: bool = False
+    use_adaea: bool = False
+    use_quest: bool = False
+    snapkv_enabled: bool = False
+    check_capacity: bool = True  # read the device status after cache writes (a host sync)
+
+    def __post_init__(self):
+        if self.head_dim is None:
+            self.head_dim = self.hidden_size // self.num_attention_heads
+
+
+def _layer_cache_check(self, cache, where):
+    if getattr(self.config, "check_capacity", True):
+        cache.raise_if_failed(where)
+
+
+def get_random_g_scores(self, batch_size, kv_seq_len, device):
+    """src/modeling_layers.py:1160-1166: 1 where U[0,1) >= random_sparsity."""
+    r = torch.rand(batch_size, self.config.num_key_value_heads, kv_seq_len, dtype=torch.bfloat16, device=device)
+    return (r >= self.config.random_sparsity).to(torch.bfloat16)
+
+
+def refresh_local_is_global(self, past_key_value, device):
+    """src/modeling_layers.py:1169-1180: re-gate the whole local window of this
+    layer (deferred gating) and store the flags."""
+    c = past_key_value
+    layer = self.layer_idx
+    H, W, D = c.num_kv_heads, c.local_window_size, c.head_dim
+    if self.config.random_sparsity is not None:
+        g = get_random_g_scores(self, 1, W, device)
+        c.local_is_global[layer] = g[0] > self.config.g_threshold
+        return
+    if self.config.g_expand != 0.0:
+        start = layer * H * W
+        k = c.block_pool_k[start:start + H * W].view(1, H, W, D)
+        v = c.block_pool_v[start:start + H * W].view(1, H, W, D)
+        self.g_predictors.scores_and_mask(c.local_pre_key[layer].unsqueeze(0), k, v, self.config.g_threshold,
+                                          mask_out=c.local_is_global[layer].unsqueeze(0))
+
+
+def migrate_local_kv_to_global(self, past_key_value, device, local_blocks_per_head):
+    """src/modeling_layers.py:674-763 on the device (no host syncs)."""
+    ops.decode_append(past_key_value, 0, migrate=True, write=False)
+    _layer_cache_check(self, past_key_value, "migrate_local_kv_to_global")
+
+
+def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
+                    batch_size, q_seq_len, device, g_mask, local_blocks_per_head):
+    """src/modeling_layers.py:1183-1376.  Tensors are (B, H, S, D); B = 1."""
+    c = past_key_value
+    if self.layer_idx == 0:
+        c.initialize(self.config, self.head_dim, key_states.dtype, device)
+    defer = c.local_pre_key is not None
+    ops.prefill_admit(c, self.layer_idx, key_states[0], value_states[0], g_mask[0],
+                      pre_key=pre_key[0] if (defer and pre_key is not None) else None)
+    _layer_cache_check(self, c, f"prefill_wrapper (layer {self.layer_idx})")
+    c.local_length = min(q_seq_len, self.config.local_window_size)  # :1297
+    meta = ops.generate_sparse_indices(g_mask, self.config.local_window_size, batch_size,
+                                       self.config.num_key_value_heads, q_seq_len, device)
+    return self.prefill_kernel(
+        query_states.transpose(1, 2), key_states.transpose(1, 2), value_states.transpose(1, 2),
+        *meta, softmax_scale=self.scaling, causal=True, return_softmax_lse=False)
+
+
+def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
+                   device, g_mask, local_blocks_per_head):
+    """src/modeling_layers.py:1379-1449.  Tensors are (1, H, 1, D)."""
+    c = past_key_value
+    W = self.config.local_window_size
+    insert_pos = c.local_length if c.local_length < W else c.local_ptr
+    seqlens = c.cache_seqlens[self.layer_idx]
+    ops.decode_append(c, self.layer_idx, key_states[0, :, 0], value_states[0, :, 0],
+                      g_mask=None if g_mask is None else g_mask[0, :, 0],
+                      pre_key=pre_key[0, :, 0] if g_mask is None else None,
+                      migrate=False, write=True, cache_seqlens=seqlens[0])
+    if g_mask is None and insert_pos == W - 1:
+        refresh_local_is_global(self, c, device)
+    if self.layer_idx == self.config.num_hidden_layers - 1:
+        if c.local_length < W:
+            c.local_length += 1
+        else:
+            c.local_ptr = (c.local_ptr + 1) % W
+    handle = self.decode_kernel_handle(
+        query_states.transpose(1, 2), c.k_cache(), c.v_cache(), seqlens,
+        c.block_table[self.layer_idx].unsqueeze(0), self.scaling)
+    return self.decode_kernel_executor(handle)
+
+
+def self_attn_forward_patch_inference(self, past_key_value, input_shape, query_states, pre_key, key_states,
+                                      value_states, g_scores, g_mask=None):
+    """src/modeling_layers.py:1452-1509.  ``g_mask`` may be passed directly
+    (the fused gate produces it); otherwise it is ``g_scores > g_threshold``."""
+    batch_size, q_seq_len = input_shape
+    device = query_states.device
+    is_prefilling = q_seq_len > 1
+    if g_mask is None and g_scores is not None:
+        g_mask = g_scores > self.config.g_threshold
+    if self.config.local_window_size % self.config.block_size:
+        raise AssertionError("local_window_size % block_size != 0")
+    lbph = self.config.local_window_size // self.config.block_size
+    if (not is_prefilling) and self.layer_idx == 0 and past_key_value.local_length == self.config.local_window_size:
+        migrate_local_kv_to_global(self, past_key_value, device, lbph)
+    if is_prefilling:
+        return self.prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
+                                    batch_size, q_seq_len, device, g_mask, lbph)
+    return self.decode_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
+                               device, g_mask, lbph)
+
+
+def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, input_shape, query_states,
+                            pre_key, key_states, value_states):
+    """src/modeling_layers.py:1534-1629, inference mode (gating_mode 3)."""
+    batch_size, _ = input_shape
+    device = query_states.device
+    cfg = self.config
+    if gating_mode != 3:
+        raise NotImplementedError("only inference (gating_mode 3) is on the MI355X path")
+    if cfg.use_duo_attn or cfg.use_adaea:
+        raise NotImplementedError("DuoAttention / AdaEA baselines are outside the hot path")
+    kv_seq_len = key_states.size(2)
+    g_scores = None
+    g_mask = None
+    if cfg.use_baseline:
+        g_mask = torch.ones(batch_size, cfg.num_key_value_heads, kv_seq_len, dtype=torch.bool, device=device)
+    elif not (kv_seq_len == 1 and cfg.g_defer):
+        if cfg.random_sparsity is not None:
+            g_scores = get_random_g_scores(self, batch_size, kv_seq_len, device)
+        elif cfg.g_expand != 0.0:
+            g_scores, g_mask = self.g_predictors.scores_and_mask(pre_key, key_states, value_states, cfg.g_threshold)
+    if batch_size != 1:
+        raise AssertionError("gating_mode 3 runs batch 1")
+    if attention_mask is not None:
+        raise AssertionError("gating_mode 3 takes no attention mask")
+    if past_key_value is None:
+        raise AssertionError("gating_mode 3 needs a cache (DualCache)")
+    out = self_attn_forward_patch_inference(self, past_key_value, input_shape, query_states, pre_key,
+                                            key_states, value_states, g_scores, g_mask=g_mask)
+    return out, None, None
+
+
+__all__ = [
+    "WGKVConfig", "DualCache", "get_random_g_scores", "refresh_local_is_global", "migrate_local_kv_to_global",
+    "prefill_wrapper", "decode_wrapper", "self_attn_forward_patch_inference", "self_attn_forward_patch",
+]

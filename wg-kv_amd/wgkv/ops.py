@@ -111,3 +111,107 @@ flash_attn_with_kvcache_wrapper_triton_handle = paged_decode_attn_handle
 
 def flash_attn_with_kvcache_wrapper_triton(*args, **kwargs):
     return paged_decode_attn_handle(*args, **kwargs)()
+
+
+# ---------------------------------------------------------------------------
+# kernel (4), prefill half: vertical-slash metadata
+# ---------------------------------------------------------------------------
+def generate_sparse_indices(g_mask, local_window_size, batch_size, num_kv_heads, seq_len, device=None,
+                            block_size=64, exact_width=False):
+    """Device-built metadata with the signature of src/modeling_layers.py:385-409.
+
+    Returns ``(block_count (1,1,R), block_offset (1,1,R,P+1), column_count
+    (B,Hkv,R), column_index (B,Hkv,1,N))``.  ``N`` is ``seq_len`` (an upper
+    bound, no host sync) unless ``exact_width`` is set, in which case the
+    per-head totals are read back and ``N`` is the reference's
+    ``max_global_size``.  Only the valid prefixes carry meaning, as in the
+    reference's own test (utils/test_sparse_indices.py:30-48).
+    """
+    if local_window_size % block_size != 0:
+        raise AssertionError("local_window_size must be a multiple of block_size")
+    if g_mask.shape != (batch_size, num_kv_heads, seq_len):
+        raise AssertionError("g_mask must be (batch, num_kv_heads, seq_len)")
+    _require_cuda(g_mask)
+    dev = g_mask.device
+    m = g_mask if g_mask.dtype == torch.uint8 else g_mask.to(torch.bool).view(torch.uint8)
+    if m.stride(2) != 1:
+        m = m.contiguous()
+    R = (seq_len + block_size - 1) // block_size
+    P = min(local_window_size // block_size, R)
+    i32 = dict(dtype=torch.int32, device=dev)
+    block_count = torch.empty(1, 1, R, **i32)
+    block_offset = torch.empty(1, 1, R, P + 1, **i32)
+    column_count = torch.empty(batch_size, num_kv_heads, R, **i32)
+    column_index = torch.empty(batch_size, num_kv_heads, 1, seq_len, **i32)
+    column_total = torch.empty(batch_size, num_kv_heads, **i32)
+    st = _lib.lib().wgkv_build_prefill_meta(
+        _ptr(m), m.stride(0), m.stride(1),
+        batch_size, num_kv_heads, seq_len, local_window_size, block_size,
+        _ptr(block_count), _ptr(block_offset),
+        _ptr(column_count), _ptr(column_index), seq_len, _ptr(column_total),
+        _lib.stream_handle(dev))
+    _lib.check(st, "wgkv_build_prefill_meta")
+    if exact_width:
+        width = int(column_total.max().item())
+        column_index = column_index[..., :width]
+    return block_count, block_offset, column_count, column_index
+
+
+# ---------------------------------------------------------------------------
+# kernel (1), cache half: prefill admission and the decode-step append
+# ---------------------------------------------------------------------------
+def _u8(mask):
+    return mask if mask.dtype == torch.uint8 else mask.to(torch.bool).view(torch.uint8)
+
+
+def prefill_admit(cache, layer, key, value, g_mask, pre_key=None):
+    """Admission of one layer's prompt into ``cache`` (batch 1).
+
+    key/value/pre_key (H, S, D) bf16 views (d contiguous), g_mask (H, S).
+    Capacity failures are recorded in ``cache.status`` (read by the caller).
+    """
+    H, S, D = key.shape
+    _require_cuda(key, value, g_mask)
+    m = _u8(g_mask)
+    if m.stride(1) != 1:
+        m = m.contiguous()
+    L = _lib.lib()
+    ws = workspace(key.device, L.wgkv_prefill_admit_workspace_bytes(H, S))
+    lpk = cache.local_pre_key if (pre_key is not None and cache.local_pre_key is not None) else None
+    st = L.wgkv_prefill_admit(
+        _ptr(key), _ptr(value), key.stride(0), key.stride(1),
+        _ptr(pre_key) if lpk is not None else None,
+        pre_key.stride(0) if lpk is not None else 0, pre_key.stride(1) if lpk is not None else 0,
+        _ptr(m), m.stride(0),
+        layer, cache.num_layers, H, S, D,
+        cache.local_window_size, cache.block_size, cache.max_tokens_per_head, cache.total_blocks,
+        _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
+        _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(lpk),
+        _ptr(cache.next_free_block_dev), _ptr(cache.status),
+        _ptr(ws), ws.numel(), _lib.stream_handle(key.device))
+    _lib.check(st, "wgkv_prefill_admit")
+
+
+def decode_append(cache, layer, key=None, value=None, g_mask=None, pre_key=None, migrate=False, write=True,
+                  cache_seqlens=None):
+    """Decode-step cache update of ``cache``: optional lazy promotion (all
+    layers) and the ring write of ``layer``'s token.  key/value/pre_key (H, D)."""
+    H = cache.num_kv_heads
+    D = cache.head_dim
+    L = _lib.lib()
+    m = None
+    if write and g_mask is not None:
+        m = _u8(g_mask).reshape(H).contiguous()
+    st = L.wgkv_decode_append(
+        _ptr(key) if write else None, _ptr(value) if write else None, key.stride(0) if write else 0,
+        _ptr(pre_key) if (write and pre_key is not None) else None,
+        pre_key.stride(0) if (write and pre_key is not None) else 0,
+        _ptr(m),
+        layer, cache.num_layers, H, D,
+        cache.local_window_size, cache.block_size, cache.max_tokens_per_head, cache.total_blocks,
+        cache.local_ptr, cache.local_length, int(migrate), int(write),
+        _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
+        _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(cache.local_pre_key),
+        _ptr(cache.next_free_block_dev), _ptr(cache_seqlens), _ptr(cache.status),
+        _lib.stream_handle(cache.block_pool_k.device))
+    _lib.check(st, "wgkv_decode_append")
