@@ -154,6 +154,35 @@ int wgkv_decode_append(
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
     void* stream);
 
+/* ------------------------------------------------------------------------
+ * Write-gate scores and admission flags.
+ *
+ * Replaces GatingPredictor.forward (src/modeling_layers.py:170-205) with its
+ * GatingRMSNorm inputs (:113-131) and the admission test g > g_threshold
+ * (:1465, :1180).  Inputs (B, H, S, D) with per-input strides, d contiguous,
+ * dtype bf16 (in_dtype 0) or f32 (1); inputs_mask bit 0/1/2 selects pre_k /
+ * post_k / v (concatenated in that order, :173-183).  Weights f32 with the
+ * reference's state-dict shapes: norm weights (D); w1 = conv1.weight
+ * (H*inner, n_in*D); b1 (H*inner); w2 = conv2.weight (H, inner); b2 (H).
+ * With rms != 0 each input row is x*rsqrt(mean(x^2)+1e-6), cast to the input
+ * dtype, times its norm weight.  act 0 = exact-erf GELU, 1 = SiLU.
+ * clamp_min > 0 applies the conv path's clamp (:205).  Outputs (may be NULL,
+ * not both): scores f32 (B,H,S), mask u8 (B,H,S) = scores > threshold.
+ * Supported: D in {64,128}, inner a multiple of 64, n_in*D <= 384.
+ * ---------------------------------------------------------------------- */
+int wgkv_gate_scores(
+    const void* pre_key, int64_t pk_sb, int64_t pk_sh, int64_t pk_ss,
+    const void* post_key, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+    const void* value, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+    int32_t in_dtype, int32_t inputs_mask,
+    const float* w_pre, const float* w_post, const float* w_v,
+    const float* w1, const float* b1, const float* w2, const float* b2,
+    int32_t batch, int32_t num_kv_heads, int32_t seq_len, int32_t head_dim, int32_t inner,
+    int32_t act, int32_t rms, float clamp_min, float threshold,
+    float* scores, int64_t sc_sb, int64_t sc_sh,
+    uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
+    void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,236 @@
+// Write-gate MLP scores and admission flags (gfx950, fp32).
+//
+// Replaces GatingPredictor.forward (src/modeling_layers.py:170-205) with the
+// RMS norms of GatingRMSNorm (:113-131) and the threshold of :1465:
+//   x  = concat(rms(pre_k)*w_pre, rms(post_k)*w_post[, rms(v)*w_v])   (n_in*D)
+//   h  = act(W1[h] x + b1[h])                                        (inner)
+//   g  = sigmoid(w2[h] . h + b2[h]);  conv path: g = max(g, clamp_min)
+//   mask = g > threshold
+// One workgroup = 64 tokens of one (batch, KV head).  The normalised inputs
+// go to LDS (fp32, rows padded for conflict-free 16-byte reads); the hidden
+// columns are dealt round-robin to the 4 waves in 16-column tiles, so W1[h]
+// is read once per workgroup; x @ W1^T runs on v_mfma_f32_16x16x4f32 with
+// each lane feeding four consecutive k from one 16-byte load; the epilogue
+// applies bias, activation and w2 and reduces over columns in registers.
+#include "wgkv_common.h"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTok = 64;
+
+struct GateArgs {
+  const void* in[3];
+  int64_t sb[3], sh[3], ss[3];
+  int n_in, in_f32, rms;
+  const float* w_norm[3];
+  const float* w1;
+  const float* b1;
+  const float* w2;
+  const float* b2;
+  int B, H, S, D, inner, act;
+  float clamp_min, threshold;
+  float* scores;
+  int64_t sc_sb, sc_sh;
+  uint8_t* mask;
+  int64_t mk_sb, mk_sh;
+};
+
+__device__ __forceinline__ float load_in(const GateArgs& a, int i, int b, int h, int s, int d) {
+  const int64_t off = (int64_t)b * a.sb[i] + (int64_t)h * a.sh[i] + (int64_t)s * a.ss[i] + d;
+  if (a.in_f32) return ((const float*)a.in[i])[off];
+  return __uint_as_float((uint32_t)((const uint16_t*)a.in[i])[off] << 16);
+}
+
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float((uint32_t)f32_to_bf16(x) << 16);
+}
+
+__device__ __forceinline__ float gelu_erf(float z) { return 0.5f * z * (1.0f + erff(z * 0.70710678118654752f)); }
+__device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
+
+template <int K>  // n_in * D
+__global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
+  constexpr int LDX = K + 4;  // padded row (floats)
+  __shared__ float xs[kTok * LDX];
+  __shared__ float s_part[4][kTok];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int tile = blockIdx.x, bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int s0 = tile * kTok;
+  const int D = a.D;
+
+  // ---- normalised inputs -> LDS: wave w handles tokens w*16 .. w*16+15 ----
+  for (int tt = 0; tt < 16; ++tt) {
+    const int m = wid * 16 + tt;
+    const int s = min(s0 + m, a.S - 1);  // rows past S are computed and discarded
+    for (int i = 0; i < a.n_in; ++i) {
+      float v[2];
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int d = lane + e * 64;
+        v[e] = d < D ? load_in(a, i, b, h, s, d) : 0.f;
+        sq += v[e] * v[e];
+      }
+      float scale = 1.f;
+      if (a.rms) {
+        const float var = wave_sum(sq) / (float)D;
+        scale = 1.0f / sqrtf(var + 1e-6f);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int d = lane + e * 64;
+        if (d < D) {
+          float y = a.rms ? v[e] * scale : v[e];
+          if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
+          xs[m * LDX + i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- x @ W1[h]^T on fp32 MFMA, epilogue act(. + b1) . w2 ----------------
+  const int n = lane & 15, kq = lane >> 4;
+  const int ntot = a.inner / 16;  // 16-column tiles of the hidden layer
+  const float* w1h = a.w1 + (int64_t)h * a.inner * K;
+  const float* b1h = a.b1 + (int64_t)h * a.inner;
+  const float* w2h = a.w2 + (int64_t)h * a.inner;
+  float logit[4][4];  // [m-tile][row i] partial logits of tokens mt*16 + 4*kq + i
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) logit[mt][i] = 0.f;
+
+  for (int t0 = wid; t0 < ntot; t0 += 16) {  // up to 4 column tiles t0, t0+4, t0+8, t0+12
+    f32x4_t c[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[mt][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    int cols[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int tj = t0 + 4 * j;
+      cols[j] = (tj < ntot ? tj : t0) * 16 + n;  // out-of-range tiles recompute tile t0 and are skipped below
+    }
+    for (int k0 = 0; k0 < K; k0 += 16) {
+      f32x4_t bw[4], ax[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bw[j] = *(const f32x4_t*)(w1h + (int64_t)cols[j] * K + k0 + 4 * kq);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) ax[mt] = *(const f32x4_t*)(&xs[(mt * 16 + n) * LDX + k0 + 4 * kq]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            c[mt][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[mt][e], bw[j][e], c[mt][j], 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (t0 + 4 * j >= ntot) break;
+      const float bias = b1h[cols[j]], wo = w2h[cols[j]];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float z = c[mt][j][i] + bias;
+          logit[mt][i] = fmaf(wo, a.act ? silu(z) : gelu_erf(z), logit[mt][i]);
+        }
+    }
+  }
+  // sum over the 16 columns held by the lanes of each row, then over waves
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = row_sum16(logit[mt][i]);
+      if (n == 0) s_part[wid][mt * 16 + 4 * kq + i] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < kTok) {
+    const int m = threadIdx.x;
+    const int s = s0 + m;
+    if (s < a.S) {
+      const float z = ((s_part[0][m] + s_part[1][m]) + (s_part[2][m] + s_part[3][m])) + a.b2[h];
+      float g = 1.0f / (1.0f + expf(-z));
+      if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+      if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
+      if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int wgkv_gate_scores(
+    const void* pre_key, int64_t pk_sb, int64_t pk_sh, int64_t pk_ss,
+    const void* post_key, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+    const void* value, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+    int32_t in_dtype, int32_t inputs_mask,
+    const float* w_pre, const float* w_post, const float* w_v,
+    const float* w1, const float* b1, const float* w2, const float* b2,
+    int32_t batch, int32_t num_kv_heads, int32_t seq_len, int32_t head_dim, int32_t inner,
+    int32_t act, int32_t rms, float clamp_min, float threshold,
+    float* scores, int64_t sc_sb, int64_t sc_sh,
+    uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
+    void* stream) {
+  if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0) return WGKV_ERR_ARG;
+  if (!w1 || !b1 || !w2 || !b2 || (!scores && !mask)) return WGKV_ERR_ARG;
+  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (inner <= 0 || inner % 64) return WGKV_ERR_UNSUPPORTED;
+  if (in_dtype != 0 && in_dtype != 1) return WGKV_ERR_UNSUPPORTED;
+  GateArgs a = {};
+  const void* srcs[3] = {pre_key, post_key, value};
+  const float* wn[3] = {w_pre, w_post, w_v};
+  const int64_t strides[3][3] = {{pk_sb, pk_sh, pk_ss}, {k_sb, k_sh, k_ss}, {v_sb, v_sh, v_ss}};
+  int n_in = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (!(inputs_mask >> i & 1)) continue;
+    if (!srcs[i] || (rms && !wn[i])) return WGKV_ERR_ARG;
+    a.in[n_in] = srcs[i];
+    a.sb[n_in] = strides[i][0];
+    a.sh[n_in] = strides[i][1];
+    a.ss[n_in] = strides[i][2];
+    a.w_norm[n_in] = wn[i];
+    ++n_in;
+  }
+  if (n_in == 0) return WGKV_ERR_ARG;
+  a.n_in = n_in;
+  a.in_f32 = in_dtype == 1;
+  a.rms = rms;
+  a.w1 = w1;
+  a.b1 = b1;
+  a.w2 = w2;
+  a.b2 = b2;
+  a.B = batch;
+  a.H = num_kv_heads;
+  a.S = seq_len;
+  a.D = head_dim;
+  a.inner = inner;
+  a.act = act;
+  a.clamp_min = clamp_min;
+  a.threshold = threshold;
+  a.scores = scores;
+  a.sc_sb = sc_sb;
+  a.sc_sh = sc_sh;
+  a.mask = mask;
+  a.mk_sb = mk_sb;
+  a.mk_sh = mk_sh;
+  if (((uintptr_t)w1 & 15) != 0) return WGKV_ERR_UNSUPPORTED;
+  const int K = n_in * head_dim;
+  dim3 grid((seq_len + kTok - 1) / kTok, batch * num_kv_heads);
+  hipStream_t st = (hipStream_t)stream;
+  switch (K) {
+    case 64: hipLaunchKernelGGL(gate_kernel<64>, grid, dim3(kThreads), 0, st, a); break;
+    case 128: hipLaunchKernelGGL(gate_kernel<128>, grid, dim3(kThreads), 0, st, a); break;
+    case 192: hipLaunchKernelGGL(gate_kernel<192>, grid, dim3(kThreads), 0, st, a); break;
+    case 256: hipLaunchKernelGGL(gate_kernel<256>, grid, dim3(kThreads), 0, st, a); break;
+    case 384: hipLaunchKernelGGL(gate_kernel<384>, grid, dim3(kThreads), 0, st, a); break;
+    default: return WGKV_ERR_UNSUPPORTED;
+  }
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}

@@ -70,6 +70,18 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr,
         c_ptr]),
+    "wgkv_gate_scores": (ctypes.c_int, [
+        c_ptr, c_i64, c_i64, c_i64,
+        c_ptr, c_i64, c_i64, c_i64,
+        c_ptr, c_i64, c_i64, c_i64,
+        c_i32, c_i32,
+        c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr, c_ptr, c_ptr,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_f32, c_f32,
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_i64, c_i64,
+        c_ptr]),
 }
 
 _lib = None

@@ -1,0 +1,112 @@
+"""The write gate as a module with the reference's parameters.
+
+Parameter names and shapes are GatingPredictor's (src/modeling_layers.py:
+134-161), so gate checkpoints (keys ``...g_predictors.pre_key_norm.weight``,
+``.post_key_norm.weight``, ``.conv1.{weight,bias}``, ``.conv2.{weight,bias}``)
+load with ``load_state_dict``.  The forward runs the HIP kernel
+``wgkv_gate_scores`` (fp32 arithmetic, fp32 scores); bf16 parameters are
+widened to fp32 copies before the call.
+"""
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .ops import _ptr, _require_cuda
+
+_INPUT_BITS = {"pre_k": 1, "post_k": 2, "v": 4}
+
+
+class GatingRMSNorm(nn.Module):
+    """Holds the norm weight (src/modeling_layers.py:113-131); the norm itself
+    runs inside the gate kernel."""
+
+    def __init__(self, hidden_size, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.variance_epsilon = eps
+
+
+class GatingPredictor(nn.Module):
+    def __init__(self, head_dim, num_kv_heads, g_inputs, g_act_fn, g_expand, g_epsilon, g_rms, g_fast_path):
+        super().__init__()
+        self.g_inputs = list(g_inputs)
+        self.g_epsilon = g_epsilon
+        self.g_fast_path = g_fast_path
+        self.g_rms = g_rms
+        self.act = 1 if g_act_fn == "silu" else 0
+        self.head_dim = head_dim
+        self.num_kv_heads = num_kv_heads
+        self.input_dim = head_dim * len(self.g_inputs)
+        self.inner_dim = int(head_dim * g_expand)
+        self.pre_key_norm = GatingRMSNorm(head_dim) if g_rms and "pre_k" in self.g_inputs else nn.Identity()
+        self.post_key_norm = GatingRMSNorm(head_dim) if g_rms and "post_k" in self.g_inputs else nn.Identity()
+        self.value_norm = GatingRMSNorm(head_dim) if g_rms and "v" in self.g_inputs else nn.Identity()
+        self.conv1 = nn.Conv1d(num_kv_heads * self.input_dim, num_kv_heads * self.inner_dim, 1, groups=num_kv_heads)
+        self.conv2 = nn.Conv1d(num_kv_heads * self.inner_dim, num_kv_heads, 1, groups=num_kv_heads)
+
+    def reset_parameters(self):
+        """src/modeling_layers.py:163-168."""
+        for norm in (self.pre_key_norm, self.post_key_norm, self.value_norm):
+            if isinstance(norm, GatingRMSNorm):
+                nn.init.ones_(norm.weight)
+        self.conv1.reset_parameters()
+        self.conv2.reset_parameters()
+
+    @staticmethod
+    def _f32(p):
+        if p is None:
+            return None
+        p = p.detach()
+        return p if (p.dtype == torch.float32 and p.is_contiguous()) else p.float().contiguous()
+
+    def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True):
+        """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S))."""
+        ref = post_key
+        B, H, S, D = ref.shape
+        if H != self.num_kv_heads or D != self.head_dim:
+            raise AssertionError("gate input shape does not match the predictor")
+        dt = ref.dtype
+        if dt not in (torch.bfloat16, torch.float32):
+            raise TypeError("gate inputs must be bf16 or fp32")
+        ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
+        bits = 0
+        args = []
+        for name in ("pre_k", "post_k", "v"):
+            t = ins[name] if name in self.g_inputs else None
+            if t is not None:
+                if t.dtype != dt or t.shape != ref.shape or t.stride(3) != 1:
+                    raise AssertionError("gate inputs must share shape/dtype with a contiguous last dim")
+                _require_cuda(t)
+                bits |= _INPUT_BITS[name]
+                args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+            else:
+                args += [None, 0, 0, 0]
+        norms = [self.pre_key_norm, self.post_key_norm, self.value_norm]
+        wn = [self._f32(m.weight) if isinstance(m, GatingRMSNorm) else None for m in norms]
+        w1 = self._f32(self.conv1.weight)
+        b1 = self._f32(self.conv1.bias)
+        w2 = self._f32(self.conv2.weight)
+        b2 = self._f32(self.conv2.bias)
+        dev = ref.device
+        scores = None
+        if want_scores:
+            scores = scores_out if scores_out is not None else torch.empty(B, H, S, dtype=torch.float32, device=dev)
+        mask = mask_out if mask_out is not None else torch.empty(B, H, S, dtype=torch.bool, device=dev)
+        mk = mask.view(torch.uint8)
+        st = _lib.lib().wgkv_gate_scores(
+            *args,
+            0 if dt == torch.bfloat16 else 1, bits,
+            _ptr(wn[0]), _ptr(wn[1]), _ptr(wn[2]),
+            _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
+            B, H, S, D, self.inner_dim,
+            self.act, int(self.g_rms), 0.0 if self.g_fast_path else float(self.g_epsilon), float(threshold),
+            _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
+            _ptr(mk), mk.stride(0), mk.stride(1),
+            _lib.stream_handle(dev))
+        _lib.check(st, "wgkv_gate_scores")
+        return scores, mask
+
+    def forward(self, pre_key, post_key, value):
+        """Scores (B, H, S) float32, as the reference's forward returns."""
+        scores, _ = self.scores_and_mask(pre_key, post_key, value, threshold=0.0)
+        return scores
