@@ -183,6 +183,31 @@ int wgkv_gate_scores(
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
     void* stream);
 
+/* ------------------------------------------------------------------------
+ * Sparse (vertical-slash) causal prefill attention.
+ *
+ * Replaces the external sparse_attn_func called by prefill_wrapper
+ * (src/modeling_layers.py:1366-1374; contract pinned by
+ * utils/test_sparse_attn.py:34-93):
+ *   q   bf16 (B, S, Hq, D)   strides q_sb, q_ss, q_sh; d contiguous
+ *   k,v bf16 (B, S, Hkv, D)  strides kv_sb, kv_ss, kv_sh
+ *   out bf16 (B, S, Hq, D)   strides o_sb, o_ss, o_sh
+ *   metadata as produced by wgkv_build_prefill_meta (block = 64):
+ *   block_count (R), block_offset (R, block_offset_width), column_count
+ *   (B, Hkv, R) contiguous, column_index with strides ci_sb, ci_sh.
+ * Row block r of head hq (KV head hq / G) attends to the listed admitted
+ * columns and to the band blocks [o, o+64), causally.  Softmax in fp32.
+ * Supported: D in {64,128}, G in {1,2,4,8}, block 64.
+ * ---------------------------------------------------------------------- */
+int wgkv_sparse_prefill_attn(
+    const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, const void* v, int64_t kv_sb, int64_t kv_ss, int64_t kv_sh,
+    void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* block_count, const int32_t* block_offset, int32_t block_offset_width,
+    const int32_t* column_count, const int32_t* column_index, int64_t ci_sb, int64_t ci_sh,
+    int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block, float softmax_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

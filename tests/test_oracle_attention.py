@@ -89,3 +89,17 @@ def test_masked_prefill_full_mask_is_causal_sdpa():
     b = torch.nn.functional.scaled_dot_product_attention(
         q.double(), k.double().repeat_interleave(2, 1), v.double().repeat_interleave(2, 1), is_causal=True)
     assert torch.allclose(a, b, atol=1e-10)
+
+
+@pytest.mark.parametrize("S,W,G", [(70, 64, 2), (200, 128, 1), (300, 64, 3)])
+def test_sparse_prefill_rows_matches_dense_mask(S, W, G):
+    g = torch.Generator().manual_seed(S + W)
+    H = 2
+    q = torch.randn(1, H * G, S, 16, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, H, S, 16, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, H, S, 16, generator=g).to(torch.bfloat16)
+    gm = (torch.rand(1, H, S, generator=g) < 0.2)
+    rows = [0, 1, 63, 64, S // 2, S - 1]
+    a = attention.sparse_prefill_rows(q, k, v, gm, W, rows)
+    full = attention.masked_prefill(q, k, v, meta.ideal_mask(gm.numpy(), W, G))
+    assert torch.allclose(a, full[:, :, rows], atol=1e-12)

@@ -1,0 +1,280 @@
+// Sparse (vertical-slash) causal prefill attention on bf16 MFMA (gfx950).
+//
+// Replaces the external sparse_attn_func the reference calls at
+// src/modeling_layers.py:1366-1374 (semantics pinned by
+// utils/test_sparse_attn.py:34-93): for row block r (64 query rows) of
+// (batch b, KV head h) the visible keys are
+//   * the admitted columns column_index[b,h,0,:column_count[b,h,r]] ("vertical"), and
+//   * the band blocks [o, o+64) for o in block_offset[r,:block_count[r]],
+// intersected with causality (key <= query).  Query head hq uses KV head
+// hq / G.
+//
+// Workgroup = (row block, b*Hkv + h), 2*G waves: wave w serves query head
+// h*G + w/2, rows (w%2)*32 .. +32 of the block, so each 64-key K/V tile is
+// staged in LDS once for all G heads.  Scores are computed transposed,
+// S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (K from LDS as the A operand, the
+// wave's queries held as the B operand), which leaves each lane with 4
+// consecutive keys of one query row: after the online softmax those
+// probabilities are already the B operand of O^T = V^T P^T, with V^T read
+// from a transposed LDS tile.  Softmax runs in the log2 domain in fp32.
+#include "wgkv_common.h"
+
+namespace {
+
+constexpr int kBlk = 64;     // query rows per block and keys per tile
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct PrefillArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_ss, q_sh;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t kv_sb, kv_ss, kv_sh;
+  uint16_t* out;
+  int64_t o_sb, o_ss, o_sh;
+  const int32_t* block_count;
+  const int32_t* block_offset;
+  int bo_width;
+  const int32_t* column_count;
+  const int32_t* column_index;
+  int64_t ci_sb, ci_sh;  // column_index strides (batch, head); positions contiguous
+  int B, S, Hkv, R;
+  float scale_log2;
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) {
+  constexpr int NT = 128 * G;      // threads
+  constexpr int KS = D / 32;       // k-steps over head_dim
+  constexpr int DT = D / 16;       // 16-wide d tiles
+  constexpr int LDK = D + 8;       // K tile row stride (elements)
+  constexpr int LDV = kBlk + 8;    // V^T tile row stride (elements)
+  __shared__ __attribute__((aligned(16))) uint16_t sK[kBlk * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[D * LDV];
+  __shared__ int s_keys[kBlk];
+
+  const int r = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int b = bh / a.Hkv, h = bh - b * a.Hkv;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int hq = h * G + (wid >> 1);
+  const int row0 = r * kBlk + (wid & 1) * 32;  // first query row of this wave
+
+  // queries as the B operand: lane (row n, slice g) of row tile rt, k-step j
+  bf16x8_t qb[2][KS];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int s = min(row0 + rt * 16 + n, a.S - 1);
+    const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)s * a.q_ss + (int64_t)hq * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < KS; ++j) qb[rt][j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + (j * 4 + g) * 8));
+  }
+
+  float m_run[2] = {-INFINITY, -INFINITY};
+  float l_part[2] = {0.f, 0.f};
+  f32x4_t o[DT][2];
+#pragma unroll
+  for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) o[dt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+  const int nv = a.column_count[((int64_t)b * a.Hkv + h) * a.R + r];
+  const int nb = a.block_count[r];
+  const int n_vtiles = (nv + kBlk - 1) / kBlk;
+  const int32_t* cidx = a.column_index + (int64_t)b * a.ci_sb + (int64_t)h * a.ci_sh;
+  const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
+  const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
+
+  for (int tile = 0; tile < n_vtiles + nb; ++tile) {
+    const bool vert = tile < n_vtiles;
+    int band0 = 0, nvalid = kBlk;
+    if (vert) {
+      nvalid = min(kBlk, nv - tile * kBlk);
+    } else {
+      band0 = a.block_offset[r * a.bo_width + (tile - n_vtiles)];
+    }
+    __syncthreads();  // the previous tile's LDS reads are done
+    for (int t = threadIdx.x; t < kBlk; t += NT) {
+      int key;
+      if (vert) key = cidx[tile * kBlk + min(t, nvalid - 1)];
+      else key = min(band0 + t, a.S - 1);
+      s_keys[t] = key;
+    }
+    __syncthreads();
+    // K tile, row-major: 16-byte slices, D/8 per row
+    for (int e = threadIdx.x; e < kBlk * (D / 8); e += NT) {
+      const int row = e / (D / 8), c = e - row * (D / 8);
+      const u32x4_t v = *(const u32x4_t*)(kbase + (int64_t)s_keys[row] * a.kv_ss + c * 8);
+      *(u32x4_t*)(&sK[row * LDK + c * 8]) = v;
+    }
+    // V^T tile: a thread takes two keys x 8 dims and writes 8 key pairs
+    for (int e = threadIdx.x; e < (kBlk / 2) * (D / 8); e += NT) {
+      const int kp = e % (kBlk / 2), c = e / (kBlk / 2);
+      const u32x4_t v0 = *(const u32x4_t*)(vbase + (int64_t)s_keys[2 * kp] * a.kv_ss + c * 8);
+      const u32x4_t v1 = *(const u32x4_t*)(vbase + (int64_t)s_keys[2 * kp + 1] * a.kv_ss + c * 8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = (v0[w] & 0xffffu) | (v1[w] << 16);
+        const uint32_t hi = (v0[w] >> 16) | (v1[w] & 0xffff0000u);
+        *(uint32_t*)(&sVt[(c * 8 + 2 * w) * LDV + 2 * kp]) = lo;
+        *(uint32_t*)(&sVt[(c * 8 + 2 * w + 1) * LDV + 2 * kp]) = hi;
+      }
+    }
+    __syncthreads();
+
+    // ---- S^T = K Q^T: key tiles kt (16 keys) x row tiles rt ------------------
+    f32x4_t sc[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      bf16x8_t kf[KS];
+#pragma unroll
+      for (int j = 0; j < KS; ++j)
+        kf[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[(kt * 16 + n) * LDK + (j * 4 + g) * 8]));
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+          sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j], qb[rt][j], sc[kt][rt], 0, 0, 0);
+      }
+    }
+    // ---- mask, online softmax (lane: query row rt*16+n, keys kt*16+4g+i) -------
+    bf16x8_t pb[2][2];  // [rt][k-step of 32 keys]
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int qrow = row0 + rt * 16 + n;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kk = kt * 16 + 4 * g + i;
+          bool ok;
+          if (vert) ok = kk < nvalid;
+          else ok = band0 + kk < a.S && band0 + kk <= qrow;
+          const float x = ok ? sc[kt][rt][i] * a.scale_log2 : -INFINITY;
+          sc[kt][rt][i] = x;
+          mx = fmaxf(mx, x);
+        }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mn = fmaxf(m_run[rt], mx);
+      const float alpha = mn == -INFINITY ? 1.f : fast_exp2(m_run[rt] - mn);
+      m_run[rt] = mn;
+      l_part[rt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
+      uint32_t pw[8];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+          const float p0 = mn == -INFINITY ? 0.f : fast_exp2(sc[kt][rt][i] - mn);
+          const float p1 = mn == -INFINITY ? 0.f : fast_exp2(sc[kt][rt][i + 1] - mn);
+          l_part[rt] += p0 + p1;
+          pw[kt * 2 + i / 2] = (uint32_t)f32_to_bf16(p0) | ((uint32_t)f32_to_bf16(p1) << 16);
+        }
+      // k-step s covers key tiles 2s (slots 0-3) and 2s+1 (slots 4-7)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4_t w = (u32x4_t){pw[4 * s], pw[4 * s + 1], pw[4 * s + 2], pw[4 * s + 3]};
+        pb[rt][s] = __builtin_bit_cast(bf16x8_t, w);
+      }
+    }
+    // ---- O^T += V^T P^T ------------------------------------------------------
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint16_t* vt = &sVt[(dt * 16 + n) * LDV + s * 32 + 4 * g];
+        const uint64_t lo = *(const uint64_t*)vt;
+        const uint64_t hi = *(const uint64_t*)(vt + 16);
+        const u32x4_t w = (u32x4_t){(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+        const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, w);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[rt][s], o[dt][rt], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- normalise and store: lane holds O[row rt*16+n][dt*16 + 4g + i] -------
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    float l = l_part[rt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int s = row0 + rt * 16 + n;
+    if (s < a.S) {
+      uint16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh;
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt) {
+        const uint32_t w0 = (uint32_t)f32_to_bf16(o[dt][rt][0] * inv) | ((uint32_t)f32_to_bf16(o[dt][rt][1] * inv) << 16);
+        const uint32_t w1 = (uint32_t)f32_to_bf16(o[dt][rt][2] * inv) | ((uint32_t)f32_to_bf16(o[dt][rt][3] * inv) << 16);
+        *(uint64_t*)(orow + dt * 16 + 4 * g) = (uint64_t)w0 | ((uint64_t)w1 << 32);
+      }
+    }
+  }
+}
+
+template <int D, int G>
+hipError_t launch(const PrefillArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, G>), dim3(a.R, a.B * a.Hkv), dim3(128 * G), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int wgkv_sparse_prefill_attn(
+    const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+    const void* k, const void* v, int64_t kv_sb, int64_t kv_ss, int64_t kv_sh,
+    void* out, int64_t o_sb, int64_t o_ss, int64_t o_sh,
+    const int32_t* block_count, const int32_t* block_offset, int32_t block_offset_width,
+    const int32_t* column_count, const int32_t* column_index, int64_t ci_sb, int64_t ci_sh,
+    int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t block, float softmax_scale, void* stream) {
+  if (!q || !k || !v || !out || !block_count || !block_offset || !column_count || !column_index) return WGKV_ERR_ARG;
+  if (batch <= 0 || seq_len <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return WGKV_ERR_ARG;
+  if (block != kBlk) return WGKV_ERR_UNSUPPORTED;
+  const int G = num_q_heads / num_kv_heads;
+  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return WGKV_ERR_UNSUPPORTED;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) return WGKV_ERR_UNSUPPORTED;
+  if ((q_sb | q_ss | q_sh | kv_sb | kv_ss | kv_sh | o_sb | o_ss | o_sh) & 7) return WGKV_ERR_UNSUPPORTED;
+  PrefillArgs a;
+  a.q = (const uint16_t*)q;
+  a.q_sb = q_sb;
+  a.q_ss = q_ss;
+  a.q_sh = q_sh;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.kv_sb = kv_sb;
+  a.kv_ss = kv_ss;
+  a.kv_sh = kv_sh;
+  a.out = (uint16_t*)out;
+  a.o_sb = o_sb;
+  a.o_ss = o_ss;
+  a.o_sh = o_sh;
+  a.block_count = block_count;
+  a.block_offset = block_offset;
+  a.bo_width = block_offset_width;
+  a.column_count = column_count;
+  a.column_index = column_index;
+  a.ci_sb = ci_sb;
+  a.ci_sh = ci_sh;
+  a.B = batch;
+  a.S = seq_len;
+  a.Hkv = num_kv_heads;
+  a.R = (seq_len + kBlk - 1) / kBlk;
+  a.scale_log2 = softmax_scale * kLog2e;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (head_dim == 128) {
+    e = G == 1 ? launch<128, 1>(a, st) : G == 2 ? launch<128, 2>(a, st) : G == 4 ? launch<128, 4>(a, st) : launch<128, 8>(a, st);
+  } else {
+    e = G == 1 ? launch<64, 1>(a, st) : G == 2 ? launch<64, 2>(a, st) : G == 4 ? launch<64, 4>(a, st) : launch<64, 8>(a, st);
+  }
+  return e == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}

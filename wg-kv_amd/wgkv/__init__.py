@@ -13,9 +13,11 @@ from .ops import (  # noqa: F401
     generate_sparse_indices,
     paged_decode_attn,
     paged_decode_attn_handle,
+    sparse_attn_func,
 )
 
 __all__ = [
+    "sparse_attn_func",
     "generate_sparse_indices",
     "paged_decode_attn",
     "paged_decode_attn_handle",

@@ -215,3 +215,50 @@ def decode_append(cache, layer, key=None, value=None, g_mask=None, pre_key=None,
         _ptr(cache.next_free_block_dev), _ptr(cache_seqlens), _ptr(cache.status),
         _lib.stream_handle(cache.block_pool_k.device))
     _lib.check(st, "wgkv_decode_append")
+
+
+# ---------------------------------------------------------------------------
+# kernel (3): sparse (vertical-slash) causal prefill attention
+# ---------------------------------------------------------------------------
+def sparse_attn_func(q, k, v, block_count, block_offset, column_count, column_index,
+                     softmax_scale=None, causal=True, return_softmax_lse=False, out=None):
+    """The contract of the reference's sparse_attn_func
+    (src/modeling_layers.py:1366-1374): q (B,S,Hq,D), k/v (B,S,Hkv,D) bf16 ->
+    (B,S,Hq,D) bf16; metadata from generate_sparse_indices (block 64)."""
+    if not causal:
+        raise NotImplementedError("only causal sparse prefill is on the path")
+    if return_softmax_lse:
+        raise NotImplementedError("return_softmax_lse is not used by the path")
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    if k.shape != (B, S, Hkv, D) or v.shape != k.shape:
+        raise AssertionError("k/v must be (batch, seq, num_kv_heads, head_dim)")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError("sparse prefill takes bf16 q/k/v")
+    if k.stride() != v.stride():
+        raise ValueError("k and v must share strides")
+    _require_cuda(q, k, v, block_count, block_offset, column_count, column_index)
+    if q.stride(3) != 1 or k.stride(3) != 1:
+        raise ValueError("head_dim must be contiguous")
+    R = (S + 63) // 64
+    if block_count.numel() != R or column_count.shape != (B, Hkv, R):
+        raise AssertionError("metadata does not match (batch, heads, seq) with block 64")
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    bc = block_count.reshape(R).contiguous()
+    bo = block_offset.reshape(R, -1).contiguous()
+    cc = column_count.contiguous()
+    ci = column_index
+    if ci.stride(-1) != 1:
+        ci = ci.contiguous()
+    if out is None:
+        out = torch.empty(B, S, Hq, D, dtype=torch.bfloat16, device=q.device)
+    st = _lib.lib().wgkv_sparse_prefill_attn(
+        _ptr(q), q.stride(0), q.stride(1), q.stride(2),
+        _ptr(k), _ptr(v), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(out), out.stride(0), out.stride(1), out.stride(2),
+        _ptr(bc), _ptr(bo), bo.shape[1],
+        _ptr(cc), _ptr(ci), ci.stride(0), ci.stride(1),
+        B, S, Hq, Hkv, D, 64, float(softmax_scale), _lib.stream_handle(q.device))
+    _lib.check(st, "wgkv_sparse_prefill_attn")
+    return out
