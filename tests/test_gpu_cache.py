@@ -47,7 +47,26 @@ def make_self(sc, layer, gates=None):
     return s
 
 
-@pytest.mark.parametrize("name", [n for n in scenarios.CACHE_SCENARIOS if not scenarios.CACHE_SCENARIOS[n]["g_defer"]])
+def product_gates(sc, inp):
+    from wgkv.gate import GatingPredictor
+    gates = []
+    for p in inp["gates"]:
+        gp = GatingPredictor(sc["D"], sc["H"], ["pre_k", "post_k"], "gelu", 4.0, 1e-3, True, True)
+        gp.load_state_dict({k: v.clone() for k, v in scenarios.defer_bias_shift(p).items()}, strict=True)
+        gates.append(gp.cuda())
+    return gates
+
+
+def oracle_regate(inp):
+    from oracle import gate as ogate
+    params = [scenarios.defer_bias_shift(p) for p in inp["gates"]]
+
+    def regate(layer, pk, k, v):
+        return ogate.gate_scores(pk[None], k[None], v[None], params[layer])[0] > 0.1
+    return regate
+
+
+@pytest.mark.parametrize("name", list(scenarios.CACHE_SCENARIOS))
 def test_cache_matches_reference_golden(name):
     from wgkv import layers
     from wgkv.cache import DualCache
@@ -57,14 +76,17 @@ def test_cache_matches_reference_golden(name):
     L, H, D, W = sc["L"], sc["H"], sc["D"], sc["W"]
     print(f"[cache parity] {name}", flush=True)
     dev = torch.device("cuda:0")
-    mods = [make_self(sc, l) for l in range(L)]
+    gates = product_gates(sc, inp) if sc["g_defer"] else None
+    regate = oracle_regate(inp) if sc["g_defer"] else None
+    mods = [make_self(sc, l, gates) for l in range(L)]
     cache = DualCache()
-    orc = DualCacheOracle(L, H, D, W, L * H * sc["max_tokens_per_head"], sc["max_tokens_per_head"])
+    orc = DualCacheOracle(L, H, D, W, L * H * sc["max_tokens_per_head"], sc["max_tokens_per_head"],
+                          g_defer=sc["g_defer"])
     for l in range(L):
         q, pk, k, v, mask = inp["prompt"][l]
         layers.self_attn_forward_patch_inference(mods[l], cache, (1, sc["S"]), q.to(dev), pk.to(dev), k.to(dev),
                                                  v.to(dev), None, g_mask=mask.to(dev))
-        orc.prefill(l, k[0], v[0], mask[0])
+        orc.prefill(l, k[0], v[0], mask[0], pre_key=pk[0])
     torch.cuda.synchronize()
     assert np.array_equal(cache.block_table.cpu().numpy(), g[f"{name}.after_prefill.block_table"])
     assert np.array_equal(cache.global_lengths.cpu().numpy(), g[f"{name}.after_prefill.global_lengths"])
@@ -75,10 +97,12 @@ def test_cache_matches_reference_golden(name):
     for step in inp["steps"]:
         for l in range(L):
             q, pk, k, v, mask = step[l]
-            out = layers.self_attn_forward_patch_inference(mods[l], cache, (1, 1), q.to(dev), pk.to(dev),
-                                                           k.to(dev), v.to(dev), None, g_mask=mask.to(dev))
+            out = layers.self_attn_forward_patch_inference(
+                mods[l], cache, (1, 1), q.to(dev), pk.to(dev), k.to(dev), v.to(dev), None,
+                g_mask=None if mask is None else mask.to(dev))
             seqlens.append(cache.cache_seqlens[l, 0].clone())
-            sl, bt = orc.decode(l, k[0, :, 0], v[0, :, 0], mask[0, :, 0])
+            sl, bt = orc.decode(l, k[0, :, 0], v[0, :, 0], None if mask is None else mask[0, :, 0],
+                                pre_key=pk[0, :, 0], regate=regate)
             ref = attention.paged_decode(q.transpose(1, 2), orc.block_pool_k.view(-1, 16, D),
                                          orc.block_pool_v.view(-1, 16, D), sl[None], bt[None], sc["D"] ** -0.5)
             err = (out.float().cpu() - ref).abs()

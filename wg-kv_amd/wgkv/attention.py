@@ -1,0 +1,112 @@
+"""A Llama/Qwen3-style attention layer whose forward is the reference's.
+
+LlamaAttention.forward (src/modeling_llama.py:252-323, gating_mode 3):
+project q/k/v, keep the pre-RoPE key (:269), apply RoPE (:270-271), hand over
+to ``self.self_attn_forward_patch`` and project the result with o_proj.  The
+swap-point attributes are bound as in the reference (:240-250), so harnesses
+that re-bind them (scripts/profiling.py:273-341) keep working.  Qwen3's
+variant applies per-head k_norm (and q_norm) before the pre-RoPE key is taken
+(src/modeling_qwen3.py:235-239); ``qk_norm=True`` selects it.
+
+The attention kernels and the dual cache are bf16 (as the reference's are);
+with an fp32 model the gate still sees fp32 keys and produces fp32 scores,
+and q/k/v are rounded to bf16 after gating.
+"""
+import torch
+import torch.nn as nn
+
+from . import layers, ops
+from .gate import GatingPredictor
+
+
+class LlamaRotaryEmbedding(nn.Module):
+    """Default RoPE (src/modeling_llama.py:81-119): cos/sin of
+    position * theta^(-2i/D), duplicated over the two halves."""
+
+    def __init__(self, head_dim, rope_theta=10000.0, device=None):
+        super().__init__()
+        inv = 1.0 / (rope_theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float().to(device) / head_dim))
+        self.register_buffer("inv_freq", inv, persistent=False)
+
+    @torch.no_grad()
+    def forward(self, x, position_ids):
+        inv = self.inv_freq[None, :, None].float().expand(position_ids.shape[0], -1, 1).to(x.device)
+        pos = position_ids[:, None, :].float()
+        freqs = (inv @ pos).transpose(1, 2)
+        emb = torch.cat((freqs, freqs), dim=-1)
+        return emb.cos().to(x.dtype), emb.sin().to(x.dtype)
+
+
+def rotate_half(x):
+    h = x.shape[-1] // 2
+    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+
+
+def apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=1):
+    cos = cos.unsqueeze(unsqueeze_dim)
+    sin = sin.unsqueeze(unsqueeze_dim)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+class HeadRMSNorm(nn.Module):
+    """Qwen3's per-head q_norm / k_norm (RMSNorm over head_dim)."""
+
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x):
+        dt = x.dtype
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return self.weight * xf.to(dt)
+
+
+class LlamaAttention(nn.Module):
+    def __init__(self, config, layer_idx, qk_norm=False):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.head_dim = config.head_dim
+        self.num_key_value_groups = config.num_attention_heads // config.num_key_value_heads
+        self.scaling = self.head_dim ** -0.5
+        bias = config.attention_bias
+        self.q_proj = nn.Linear(config.hidden_size, config.num_attention_heads * self.head_dim, bias=bias)
+        self.k_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
+        self.v_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
+        self.o_proj = nn.Linear(config.num_attention_heads * self.head_dim, config.hidden_size, bias=bias)
+        self.qk_norm = qk_norm
+        if qk_norm:
+            self.q_norm = HeadRMSNorm(self.head_dim)
+            self.k_norm = HeadRMSNorm(self.head_dim)
+        if not config.use_baseline and config.g_expand != 0.0:
+            self.g_predictors = GatingPredictor(self.head_dim, config.num_key_value_heads, config.g_inputs,
+                                                config.g_act_fn, config.g_expand, config.g_epsilon,
+                                                config.g_rms, config.g_fast_path)
+        # swap points (src/modeling_llama.py:240-250)
+        self.self_attn_forward_patch = layers.self_attn_forward_patch
+        self.prefill_wrapper = layers.prefill_wrapper
+        self.decode_wrapper = layers.decode_wrapper
+        self.prefill_kernel = ops.sparse_attn_func
+        self.decode_kernel_handle = ops.paged_decode_attn_handle
+        self.decode_kernel_executor = lambda func: func()
+
+    def forward(self, gating_mode, hidden_states, position_embeddings, attention_mask=None, past_key_value=None,
+                cache_position=None, **kwargs):
+        input_shape = hidden_states.shape[:-1]
+        hidden_shape = (*input_shape, -1, self.head_dim)
+        q = self.q_proj(hidden_states).view(hidden_shape)
+        k = self.k_proj(hidden_states).view(hidden_shape)
+        if self.qk_norm:
+            q, k = self.q_norm(q), self.k_norm(k)
+        q = q.transpose(1, 2)
+        k = k.transpose(1, 2)
+        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        pre_key = k if "pre_k" in self.config.g_inputs else None
+        cos, sin = position_embeddings
+        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        out, attn_weights, g_scores = self.self_attn_forward_patch(
+            self, gating_mode, attention_mask, past_key_value, input_shape, q, pre_key, k, v)
+        out = out.reshape(*input_shape, -1).to(hidden_states.dtype).contiguous()
+        return self.o_proj(out), attn_weights, g_scores

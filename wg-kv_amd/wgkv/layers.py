@@ -178,6 +178,13 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
             g_scores = get_random_g_scores(self, batch_size, kv_seq_len, device)
         elif cfg.g_expand != 0.0:
             g_scores, g_mask = self.g_predictors.scores_and_mask(pre_key, key_states, value_states, cfg.g_threshold)
+    if query_states.dtype != torch.bfloat16:
+        # the cache and attention kernels are bf16 (as the reference's are); the
+        # gate above has already seen the model-dtype keys
+        query_states = query_states.to(torch.bfloat16)
+        key_states = key_states.to(torch.bfloat16)
+        value_states = value_states.to(torch.bfloat16)
+        pre_key = pre_key.to(torch.bfloat16) if pre_key is not None else None
     if batch_size != 1:
         raise AssertionError("gating_mode 3 runs batch 1")
     if attention_mask is not None:

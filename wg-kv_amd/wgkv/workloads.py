@@ -76,3 +76,56 @@ def decode_ragged(ctx=131072, batch=8, Hq=32, Hkv=8, D=128, window=1024, page=16
     f = rng.uniform(lo, hi, size=(batch, Hkv))
     seqlens = window + np.rint(f * (ctx - window)).astype(np.int64)
     return _build(seqlens, Hq, D, page, device, seed, f"decode_ragged_b{batch}_{ctx // 1024}k")
+
+
+def config1_layer(seed=0, hidden=512, Hq=8, Hkv=2, D=64, S=2048, steps=32, W=128, frac=0.2, threshold=0.1,
+                  g_defer=False):
+    """BASELINE config 1 on the host (CPU tensors): weights, prompt, decode inputs.
+
+    torch.manual_seed(seed); q/k/v/o ~ N(0, 0.02); gate with the reference's
+    default init (RMSNorm weights 1, Conv1d uniform), inner = 4*D; prompt
+    x ~ N(0, 1) (1, S, hidden); ``steps`` decode inputs ~ N(0, 1) at explicit
+    positions S, S+1, ...  ``conv2.bias[h]`` is shifted afterwards by
+    logit(threshold) - q_{1-frac}(pre-sigmoid logits of head h over the prompt),
+    so about ``frac`` of the prompt is admitted; that shift needs the gate's
+    scores of the prompt, which the caller computes (``shift_gate_bias``).
+    Returns (config kwargs, weights dict, prompt, decode inputs).
+    """
+    import math
+    torch.manual_seed(seed)
+    inner = 4 * D
+    w = {
+        "q_proj.weight": torch.randn(Hq * D, hidden) * 0.02,
+        "k_proj.weight": torch.randn(Hkv * D, hidden) * 0.02,
+        "v_proj.weight": torch.randn(Hkv * D, hidden) * 0.02,
+        "o_proj.weight": torch.randn(hidden, Hq * D) * 0.02,
+    }
+    conv1 = torch.nn.Conv1d(Hkv * 2 * D, Hkv * inner, 1, groups=Hkv)
+    conv2 = torch.nn.Conv1d(Hkv * inner, Hkv, 1, groups=Hkv)
+    w["g_predictors.pre_key_norm.weight"] = torch.ones(D)
+    w["g_predictors.post_key_norm.weight"] = torch.ones(D)
+    w["g_predictors.conv1.weight"] = conv1.weight.detach().clone()
+    w["g_predictors.conv1.bias"] = conv1.bias.detach().clone()
+    w["g_predictors.conv2.weight"] = conv2.weight.detach().clone()
+    w["g_predictors.conv2.bias"] = conv2.bias.detach().clone()
+    x = torch.randn(1, S, hidden)
+    xs = [torch.randn(1, 1, hidden) for _ in range(steps)]
+    cfg = dict(hidden_size=hidden, num_hidden_layers=1, num_attention_heads=Hq, num_key_value_heads=Hkv,
+               head_dim=D, local_window_size=W, block_size=16, max_tokens_per_head=S + steps + 2 * W,
+               max_total_tokens=Hkv * (S + steps + 2 * W), g_threshold=threshold, g_defer=g_defer,
+               g_fast_path=True, rope_theta=10000.0)
+    cfg["_frac"] = frac
+    cfg["_logit_threshold"] = math.log(threshold / (1 - threshold))
+    return cfg, w, x, xs
+
+
+def shift_gate_bias(weights, logits, frac, logit_threshold):
+    """Shift conv2.bias[h] so that a fraction ``frac`` of the tokens of head h
+    have logits above ``logit_threshold``; ``logits`` (Hkv, S) pre-sigmoid."""
+    w = dict(weights)
+    b = w["g_predictors.conv2.bias"].clone()
+    for h in range(logits.shape[0]):
+        qv = torch.quantile(logits[h].double(), 1.0 - frac).item()
+        b[h] += float(logit_threshold - qv)
+    w["g_predictors.conv2.bias"] = b
+    return w
