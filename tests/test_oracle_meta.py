@@ -84,3 +84,14 @@ def test_column_count_is_rank_of_band_start():
     # listed columns: every admitted position below 1 + 64*((S-1)//64), ascending
     below = pos[pos < 1 + 64 * ((3000 - 1) // 64)]
     assert np.array_equal(ci[0, 0, 0], below)
+
+
+@pytest.mark.parametrize("S,W", [(300, 64), (1000, 128), (129, 256), (2, 64)])
+def test_visible_pairs_counts_the_ideal_mask(S, W):
+    # the closed form bench.py uses for the attention FLOP count
+    import torch
+    from wgkv import workloads
+    gm = torch.rand(3, S, generator=torch.Generator().manual_seed(S)) < 0.3
+    got = workloads.visible_pairs(gm, W).numpy()
+    ref = meta.ideal_mask(gm[None].numpy(), W, 1)[0].sum(axis=(1, 2))
+    assert np.array_equal(got, ref)

@@ -3,7 +3,8 @@
 // Work split: the logical sequence of every (batch row b, KV head h) is cut
 // into 16-token sub-pages; sub-pages are grouped into chunks of `cp`
 // sub-pages (cp a multiple of 16, chosen on the device so that the whole
-// batch gives about kTargetChunks chunks).  One workgroup (4 waves) owns one
+// batch, per-head remainders included, gives at most kRounds * slots chunks,
+// slots = resident workgroups = 3 per CU).  One workgroup (4 waves) owns one
 // chunk, and its waves take 64-token "quads" (4 sub-pages) in turn.  Every
 // K/V byte of the cache is read exactly once, for all G query heads of the
 // KV head together.
@@ -27,8 +28,10 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxBH = 2048;
-constexpr int kTargetChunks = 2048;
-constexpr int kMaxChunks = kTargetChunks + kMaxBH;
+constexpr int kWgPerCu = 3;          // resident workgroups per CU at 165 VGPRs
+constexpr int kRounds = 1;           // chunks per resident workgroup slot
+constexpr int kMaxSlots = 1024;      // cap on CUs * kWgPerCu (workspace sizing)
+constexpr int kMaxChunks = kRounds * kMaxSlots + kMaxBH;
 constexpr float kLog2e = 1.4426950408889634f;
 
 struct DecodeArgs {
@@ -47,6 +50,7 @@ struct DecodeArgs {
   int64_t out_sb, out_sh;
   int B, Hkv;
   float scale_log2;
+  int target_chunks;  // kRounds * slots - B*Hkv: the chunk count then fits kRounds full rounds
   float* part;  // [kMaxChunks][4] m, then [kMaxChunks][4] l, then [kMaxChunks][4][D] acc
   int* plan;    // [kMaxBH + 1] first chunk of each (b,h), written by the split kernel
 };
@@ -71,7 +75,7 @@ __device__ int build_plan(const DecodeArgs& a, int* s_pref, int* s_tmp) {
   for (int bh = lo; bh < hi; ++bh) subs += (clamped_tokens(a, bh) + 15) >> 4;
   int total = 0;
   block_exclusive_scan_256(subs, s_tmp, &total);
-  int cp = (total + kTargetChunks - 1) / kTargetChunks;
+  int cp = (total + a.target_chunks - 1) / a.target_chunks;
   cp = max(16, (cp + 15) & ~15);
   int chunks = 0;
   for (int bh = lo; bh < hi; ++bh) {
@@ -389,10 +393,24 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   }
 }
 
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 template <int D, int G>
-hipError_t launch(const DecodeArgs& a, hipStream_t st) {
+hipError_t launch(DecodeArgs a, hipStream_t st) {
   const int BH = a.B * a.Hkv;
-  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(kTargetChunks + BH), dim3(kThreads), 0, st, a);
+  const int slots = min(kMaxSlots, cu_count() * kWgPerCu);
+  a.target_chunks = max(slots, kRounds * slots - BH);
+  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(a.target_chunks + BH), dim3(kThreads), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH), dim3(kThreads), 0, st, a);

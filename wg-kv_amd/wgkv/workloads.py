@@ -129,3 +129,53 @@ def shift_gate_bias(weights, logits, frac, logit_threshold):
         b[h] += float(logit_threshold - qv)
     w["g_predictors.conv2.bias"] = b
     return w
+
+
+def visible_pairs(g_mask, local_window_size, bs=64):
+    """Number of (query, key) pairs the sparse prefill evaluates, per KV head.
+
+    Row i of block r sees keys j <= i that are admitted or lie in
+    [r*bs - W + 1, i] (the vertical-slash ideal mask); computed in closed form
+    from the admitted prefix counts.  g_mask (Hkv, S) bool on any device."""
+    m = g_mask.to(torch.int64)
+    H, S = m.shape
+    cum = torch.cumsum(m, dim=1)                       # admitted in [0, j]
+    i = torch.arange(S, device=m.device)
+    start = torch.clamp((i // bs) * bs - local_window_size + 1, min=0)
+    band = i - start + 1
+    before = torch.where(start > 0, cum[:, (start - 1).clamp(min=0)], torch.zeros_like(cum[:, :1]))
+    return (band[None, :] + before).sum(dim=1)        # (H,)
+
+
+@dataclass
+class PrefillWorkload:
+    q: torch.Tensor        # (1, S, Hq, D) bf16
+    k: torch.Tensor        # (1, S, Hkv, D) bf16 (post-RoPE)
+    v: torch.Tensor
+    pre_k: torch.Tensor    # (1, S, Hkv, D) bf16
+    gate: object           # wgkv.gate.GatingPredictor on the device
+    threshold: float
+    local_window: int
+
+
+def prefill_llama(S=32768, Hq=32, Hkv=8, D=128, W=1024, frac=0.2, threshold=0.1, device="cuda", seed=0):
+    """Config-4 shapes: bf16 q/k/v/pre-RoPE k ~ N(0,1) in (B, S, H, D) layout,
+    a gate with the reference's default init whose conv2 bias is shifted per
+    head so ~``frac`` of the prompt scores above ``threshold``."""
+    import math
+    from .gate import GatingPredictor
+    g = torch.Generator(device=device).manual_seed(seed)
+
+    def rn(*shape):
+        return torch.randn(*shape, generator=g, device=device, dtype=torch.float32).to(torch.bfloat16)
+
+    q, k, v, pk = rn(1, S, Hq, D), rn(1, S, Hkv, D), rn(1, S, Hkv, D), rn(1, S, Hkv, D)
+    torch.manual_seed(seed)
+    gate = GatingPredictor(D, Hkv, ["pre_k", "post_k"], "gelu", 4.0, 1e-3, True, True).to(device)
+    scores, _ = gate.scores_and_mask(pk.transpose(1, 2), k.transpose(1, 2), None, 0.5)
+    logit = torch.log(scores.double()) - torch.log1p(-scores.double())
+    with torch.no_grad():
+        for h in range(Hkv):
+            qv = torch.quantile(logit[0, h].float(), 1.0 - frac).item()
+            gate.conv2.bias[h] += math.log(threshold / (1 - threshold)) - qv
+    return PrefillWorkload(q, k, v, pk, gate, threshold, W)
