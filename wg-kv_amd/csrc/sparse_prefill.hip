@@ -47,16 +47,19 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   constexpr int NT = 128 * G;      // threads
   constexpr int KS = D / 32;       // k-steps over head_dim
   constexpr int DT = D / 16;       // 16-wide d tiles
+  constexpr int CH = D / 8;        // 16-byte slices per row
   constexpr int LDK = D + 8;       // K tile row stride (elements)
   constexpr int LDV = kBlk + 8;    // V^T tile row stride (elements)
+  constexpr int KITEMS = kBlk * CH;         // (row, slice) items of a K tile
+  constexpr int VITEMS = (kBlk / 2) * CH;   // (key pair, slice) items of a V tile
   __shared__ __attribute__((aligned(16))) uint16_t sK[kBlk * LDK];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[D * LDV];
-  __shared__ int s_keys[kBlk];
 
   const int r = blockIdx.x;
   const int bh = blockIdx.y;
   const int b = bh / a.Hkv, h = bh - b * a.Hkv;
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int lane = t & 63, wid = t >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int hq = h * G + (wid >> 1);
   const int row0 = r * kBlk + (wid & 1) * 32;  // first query row of this wave
@@ -82,46 +85,105 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   const int nv = a.column_count[((int64_t)b * a.Hkv + h) * a.R + r];
   const int nb = a.block_count[r];
   const int n_vtiles = (nv + kBlk - 1) / kBlk;
+  const int ntiles = n_vtiles + nb;
   const int32_t* cidx = a.column_index + (int64_t)b * a.ci_sb + (int64_t)h * a.ci_sh;
   const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
   const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
 
-  for (int tile = 0; tile < n_vtiles + nb; ++tile) {
+  // Tile loading: K items are (row, 16-byte slice), V items are (key pair,
+  // slice); thread t takes items t, t+NT, ...  The keys of the next tile are
+  // looked up one tile ahead and its rows loaded into registers one tile
+  // ahead, so both latencies overlap the current tile's arithmetic.
+  constexpr int KPT = (KITEMS + NT - 1) / NT;
+  constexpr int VPT = (VITEMS + NT - 1) / NT;
+  int krow[KPT], kcol[KPT], vkp[VPT], vcol[VPT];
+#pragma unroll
+  for (int i = 0; i < KPT; ++i) {
+    const int e = t + i * NT;
+    krow[i] = e < KITEMS ? e / CH : -1;
+    kcol[i] = e % CH;
+  }
+#pragma unroll
+  for (int i = 0; i < VPT; ++i) {
+    const int e = t + i * NT;
+    vkp[i] = e < VITEMS ? e % (kBlk / 2) : -1;
+    vcol[i] = e / (kBlk / 2);
+  }
+  struct Keys {
+    int k[KPT];
+    int v[VPT][2];
+  };
+  struct Regs {
+    u32x4_t k[KPT];
+    u32x4_t v[VPT][2];
+  };
+  auto tile_keys = [&](int tl, Keys& ks) {
+    if (tl < n_vtiles) {
+      const int nval = min(kBlk, nv - tl * kBlk);
+      const int32_t* ci = cidx + tl * kBlk;
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) ks.k[i] = krow[i] >= 0 ? ci[min(krow[i], nval - 1)] : 0;
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) ks.v[i][j] = vkp[i] >= 0 ? ci[min(2 * vkp[i] + j, nval - 1)] : 0;
+    } else {
+      const int b0 = a.block_offset[r * a.bo_width + (tl - n_vtiles)];
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) ks.k[i] = min(b0 + max(krow[i], 0), a.S - 1);
+#pragma unroll
+      for (int i = 0; i < VPT; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) ks.v[i][j] = min(b0 + 2 * max(vkp[i], 0) + j, a.S - 1);
+    }
+  };
+  auto tile_load = [&](const Keys& ks, Regs& rg) {
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      if (krow[i] >= 0) rg.k[i] = *(const u32x4_t*)(kbase + (int64_t)ks.k[i] * a.kv_ss + kcol[i] * 8);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i)
+      if (vkp[i] >= 0)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) rg.v[i][j] = *(const u32x4_t*)(vbase + (int64_t)ks.v[i][j] * a.kv_ss + vcol[i] * 8);
+  };
+
+  Keys keys_next;
+  Regs regs;
+  if (ntiles > 0) {
+    Keys k0;
+    tile_keys(0, k0);
+    tile_load(k0, regs);
+    if (ntiles > 1) tile_keys(1, keys_next);
+  }
+
+  for (int tile = 0; tile < ntiles; ++tile) {
     const bool vert = tile < n_vtiles;
     int band0 = 0, nvalid = kBlk;
-    if (vert) {
-      nvalid = min(kBlk, nv - tile * kBlk);
-    } else {
-      band0 = a.block_offset[r * a.bo_width + (tile - n_vtiles)];
-    }
+    if (vert) nvalid = min(kBlk, nv - tile * kBlk);
+    else band0 = a.block_offset[r * a.bo_width + (tile - n_vtiles)];
+
     __syncthreads();  // the previous tile's LDS reads are done
-    for (int t = threadIdx.x; t < kBlk; t += NT) {
-      int key;
-      if (vert) key = cidx[tile * kBlk + min(t, nvalid - 1)];
-      else key = min(band0 + t, a.S - 1);
-      s_keys[t] = key;
-    }
-    __syncthreads();
-    // K tile, row-major: 16-byte slices, D/8 per row
-    for (int e = threadIdx.x; e < kBlk * (D / 8); e += NT) {
-      const int row = e / (D / 8), c = e - row * (D / 8);
-      const u32x4_t v = *(const u32x4_t*)(kbase + (int64_t)s_keys[row] * a.kv_ss + c * 8);
-      *(u32x4_t*)(&sK[row * LDK + c * 8]) = v;
-    }
-    // V^T tile: a thread takes two keys x 8 dims and writes 8 key pairs
-    for (int e = threadIdx.x; e < (kBlk / 2) * (D / 8); e += NT) {
-      const int kp = e % (kBlk / 2), c = e / (kBlk / 2);
-      const u32x4_t v0 = *(const u32x4_t*)(vbase + (int64_t)s_keys[2 * kp] * a.kv_ss + c * 8);
-      const u32x4_t v1 = *(const u32x4_t*)(vbase + (int64_t)s_keys[2 * kp + 1] * a.kv_ss + c * 8);
+#pragma unroll
+    for (int i = 0; i < KPT; ++i)
+      if (krow[i] >= 0) *(u32x4_t*)(&sK[krow[i] * LDK + kcol[i] * 8]) = regs.k[i];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+      if (vkp[i] < 0) continue;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = (v0[w] & 0xffffu) | (v1[w] << 16);
-        const uint32_t hi = (v0[w] >> 16) | (v1[w] & 0xffff0000u);
-        *(uint32_t*)(&sVt[(c * 8 + 2 * w) * LDV + 2 * kp]) = lo;
-        *(uint32_t*)(&sVt[(c * 8 + 2 * w + 1) * LDV + 2 * kp]) = hi;
+        const uint32_t lo = (regs.v[i][0][w] & 0xffffu) | (regs.v[i][1][w] << 16);
+        const uint32_t hi = (regs.v[i][0][w] >> 16) | (regs.v[i][1][w] & 0xffff0000u);
+        *(uint32_t*)(&sVt[(vcol[i] * 8 + 2 * w) * LDV + 2 * vkp[i]]) = lo;
+        *(uint32_t*)(&sVt[(vcol[i] * 8 + 2 * w + 1) * LDV + 2 * vkp[i]]) = hi;
       }
     }
     __syncthreads();
+    // the next tile's rows stream in under this tile's arithmetic
+    if (tile + 1 < ntiles) {
+      tile_load(keys_next, regs);
+      if (tile + 2 < ntiles) tile_keys(tile + 2, keys_next);
+    }
 
     // ---- S^T = K Q^T: key tiles kt (16 keys) x row tiles rt ------------------
     f32x4_t sc[4][2];
@@ -139,28 +201,39 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
           sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j], qb[rt][j], sc[kt][rt], 0, 0, 0);
       }
     }
-    // ---- mask, online softmax (lane: query row rt*16+n, keys kt*16+4g+i) -------
+    // tiles whose 64 keys are all visible to all 32 rows of the wave skip masking
+    const bool full = vert ? nvalid == kBlk : (band0 + kBlk - 1 <= row0 && band0 + kBlk <= a.S);
+    // ---- online softmax (lane: query row rt*16+n, keys kt*16+4g+i) -------------
     bf16x8_t pb[2][2];  // [rt][k-step of 32 keys]
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       const int qrow = row0 + rt * 16 + n;
       float mx = -INFINITY;
+      if (full) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
+        for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kk = kt * 16 + 4 * g + i;
-          bool ok;
-          if (vert) ok = kk < nvalid;
-          else ok = band0 + kk < a.S && band0 + kk <= qrow;
-          const float x = ok ? sc[kt][rt][i] * a.scale_log2 : -INFINITY;
-          sc[kt][rt][i] = x;
-          mx = fmaxf(mx, x);
-        }
+          for (int i = 0; i < 4; ++i) {
+            sc[kt][rt][i] *= a.scale_log2;
+            mx = fmaxf(mx, sc[kt][rt][i]);
+          }
+      } else {
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kk = kt * 16 + 4 * g + i;
+            const bool ok = vert ? kk < nvalid : (band0 + kk < a.S && band0 + kk <= qrow);
+            const float x = ok ? sc[kt][rt][i] * a.scale_log2 : -INFINITY;
+            sc[kt][rt][i] = x;
+            mx = fmaxf(mx, x);
+          }
+      }
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float mn = fmaxf(m_run[rt], mx);
-      const float alpha = mn == -INFINITY ? 1.f : fast_exp2(m_run[rt] - mn);
+      const float mref = mn == -INFINITY ? 0.f : mn;  // rows with nothing visible yet keep p = 0
+      const float alpha = fast_exp2(m_run[rt] - mref);
       m_run[rt] = mn;
       l_part[rt] *= alpha;
 #pragma unroll
@@ -170,10 +243,10 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
-          const float p0 = mn == -INFINITY ? 0.f : fast_exp2(sc[kt][rt][i] - mn);
-          const float p1 = mn == -INFINITY ? 0.f : fast_exp2(sc[kt][rt][i + 1] - mn);
+          const float p0 = fast_exp2(sc[kt][rt][i] - mref);
+          const float p1 = fast_exp2(sc[kt][rt][i + 1] - mref);
           l_part[rt] += p0 + p1;
-          pw[kt * 2 + i / 2] = (uint32_t)f32_to_bf16(p0) | ((uint32_t)f32_to_bf16(p1) << 16);
+          pw[kt * 2 + i / 2] = pack_bf16x2(p0, p1);
         }
       // k-step s covers key tiles 2s (slots 0-3) and 2s+1 (slots 4-7)
 #pragma unroll
@@ -211,8 +284,8 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
       uint16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint32_t w0 = (uint32_t)f32_to_bf16(o[dt][rt][0] * inv) | ((uint32_t)f32_to_bf16(o[dt][rt][1] * inv) << 16);
-        const uint32_t w1 = (uint32_t)f32_to_bf16(o[dt][rt][2] * inv) | ((uint32_t)f32_to_bf16(o[dt][rt][3] * inv) << 16);
+        const uint32_t w0 = pack_bf16x2(o[dt][rt][0] * inv, o[dt][rt][1] * inv);
+        const uint32_t w1 = pack_bf16x2(o[dt][rt][2] * inv, o[dt][rt][3] * inv);
         *(uint64_t*)(orow + dt * 16 + 4 * g) = (uint64_t)w0 | ((uint64_t)w1 << 32);
       }
     }

@@ -17,6 +17,15 @@ typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
 WGKV_DEVICE float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
 WGKV_DEVICE float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// Two f32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
+WGKV_DEVICE uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+  bf16x2_t r;
+  r[0] = (__bf16)lo;
+  r[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
 // Round-to-nearest-even f32 -> bf16 (NaN kept quiet).
 WGKV_DEVICE uint16_t f32_to_bf16(float f) {
   uint32_t u = __float_as_uint(f);
