@@ -208,6 +208,67 @@ int wgkv_sparse_prefill_attn(
     int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
     int32_t block, float softmax_scale, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Chunked gated prefill (batch 1): the prompt goes in chunks
+ * [chunk_start, chunk_start + chunk_len) and each chunk leaves the dual cache
+ * as a one-shot prefill of the first chunk_start + chunk_len tokens would
+ * (wgkv_prefill_admit; reference prefill_wrapper, src/modeling_layers.py:
+ * 1183-1300), the same logical cache per head -- (position, K, V) in order --
+ * with pages numbered in chunk order.  The reference prefills in one call
+ * (:1197 asserts a single initialisation); these two entry points extend
+ * that call for prompts fed in pieces.  Per chunk and layer:
+ *   1. wgkv_chunk_cache_update(stage 0): admission of positions
+ *      [chunk_start - W, chunk_start + chunk_len - W) -- the previous ring
+ *      (slot i = position chunk_start - W + i, flags in local_is_global)
+ *      then the chunk's own -- appended in position order to each head's
+ *      global pages (bump-allocated in head order); column_count (Hkv, R_c)
+ *      of the chunk's R_c = ceil(chunk_len/64) row blocks = admitted
+ *      positions below max(0, 64 r - W + 1), r the global row block.
+ *   2. wgkv_chunk_prefill_attn: the vertical-slash attention of the
+ *      chunk's queries (the masks of utils/test_sparse_attn.py:34-58 at the
+ *      chunk's rows): admitted columns through the head's block table, band
+ *      keys below chunk_start from the ring, the rest from the chunk.
+ *   3. wgkv_chunk_cache_update(stage 1): ring slot i <- position
+ *      chunk_start + chunk_len - W + i (flags and, with pre_key, the
+ *      deferred-gating pre-RoPE keys).
+ * Both stages of one chunk take the same workspace (stage 0 leaves an abort
+ * flag there that stage 1 reads: a capacity failure sets status =
+ * WGKV_ERR_CAPACITY and the chunk writes nothing).  key/value/pre_key are the
+ * chunk's (Hkv, chunk_len, D) bf16 (strides per head and per position, d
+ * contiguous); g_mask (Hkv, chunk_len) u8.  Requires chunk_start and W
+ * multiples of 64, W a multiple of page_size and, after the first chunk,
+ * chunk_start >= W and chunk_len >= W.
+ * ---------------------------------------------------------------------- */
+size_t wgkv_chunk_admit_workspace_bytes(int32_t num_kv_heads, int32_t chunk_len, int32_t local_window);
+
+int wgkv_chunk_cache_update(
+    int32_t stage,
+    const void* key, const void* value, int64_t kv_stride_h, int64_t kv_stride_s,
+    const void* pre_key, int64_t pk_stride_h, int64_t pk_stride_s,
+    const uint8_t* g_mask, int64_t gm_stride_h,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t chunk_start, int32_t chunk_len, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
+    int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
+    int32_t* next_free_block, int32_t* status, int32_t* column_count,
+    void* workspace, size_t workspace_bytes, void* stream);
+
+/* q (chunk_len, Hq, D) and out with strides q_ss/q_sh, o_ss/o_sh; the
+ * chunk's k/v (chunk_len, Hkv, D) with strides kv_ss/kv_sh; pool_k/pool_v
+ * (pages*page_size, D) and block_table (L, Hkv, max_pages_per_head) of the
+ * cache, column_count (Hkv, R_c) from stage 0.  Supported: D in {64,128},
+ * G in {1,2,4,8}. */
+int wgkv_chunk_prefill_attn(
+    const void* q, int64_t q_ss, int64_t q_sh,
+    const void* k, const void* v, int64_t kv_ss, int64_t kv_sh,
+    void* out, int64_t o_ss, int64_t o_sh,
+    const void* pool_k, const void* pool_v,
+    const int32_t* block_table, int32_t max_pages_per_head,
+    const int32_t* column_count,
+    int32_t layer, int32_t chunk_start, int32_t chunk_len,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, float softmax_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

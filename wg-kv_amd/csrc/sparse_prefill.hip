@@ -40,9 +40,20 @@ struct PrefillArgs {
   int64_t ci_sb, ci_sh;  // column_index strides (batch, head); positions contiguous
   int B, S, Hkv, R;
   float scale_log2;
+  // chunked mode: queries/outputs and the chunk's k/v are chunk-relative rows
+  // of positions c0 .. c0+C-1; S = c0 + C bounds the keys.  Admitted columns
+  // are logical indices into each head's paged global cache (block table row
+  // bt + h*bt_sh, already offset past the local pages), band keys below c0
+  // come from the ring (pool row ring_row0 + h*W + p - (c0 - W)).
+  int c0, W, page;
+  const uint16_t* pool_k;
+  const uint16_t* pool_v;
+  const int32_t* bt;
+  int64_t bt_sh;
+  int64_t ring_row0;
 };
 
-template <int D, int G>
+template <int D, int G, bool CHUNK>
 __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) {
   constexpr int NT = 128 * G;      // threads
   constexpr int KS = D / 32;       // k-steps over head_dim
@@ -62,13 +73,15 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   const int lane = t & 63, wid = t >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int hq = h * G + (wid >> 1);
-  const int row0 = r * kBlk + (wid & 1) * 32;  // first query row of this wave
+  const int lrow0 = r * kBlk + (wid & 1) * 32;   // first query row of this wave (tensor row)
+  const int row0 = (CHUNK ? a.c0 : 0) + lrow0;   // its position
+  const int nrows = a.S - (CHUNK ? a.c0 : 0);    // query rows in the tensors
 
   // queries as the B operand: lane (row n, slice g) of row tile rt, k-step j
   bf16x8_t qb[2][KS];
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    const int s = min(row0 + rt * 16 + n, a.S - 1);
+    const int s = min(lrow0 + rt * 16 + n, nrows - 1);
     const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)s * a.q_ss + (int64_t)hq * a.q_sh;
 #pragma unroll
     for (int j = 0; j < KS; ++j) qb[rt][j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + (j * 4 + g) * 8));
@@ -83,7 +96,15 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     for (int rt = 0; rt < 2; ++rt) o[dt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 
   const int nv = a.column_count[((int64_t)b * a.Hkv + h) * a.R + r];
-  const int nb = a.block_count[r];
+  int nb, band_start = 0;
+  if (CHUNK) {
+    // band of global row block rg: [max(0, rg*64 - W + 1), rg*64 + 64) in 64-key tiles
+    const int rg = a.c0 / kBlk + r;
+    band_start = max(0, rg * kBlk - a.W + 1);
+    nb = (min(rg * kBlk + kBlk, a.S) - band_start + kBlk - 1) / kBlk;
+  } else {
+    nb = a.block_count[r];
+  }
   const int n_vtiles = (nv + kBlk - 1) / kBlk;
   const int ntiles = n_vtiles + nb;
   const int32_t* cidx = a.column_index + (int64_t)b * a.ci_sb + (int64_t)h * a.ci_sh;
@@ -110,42 +131,67 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     vcol[i] = e / (kBlk / 2);
   }
   struct Keys {
-    int k[KPT];
-    int v[VPT][2];
+    const uint16_t* k[KPT];     // start of the K row of each K item
+    const uint16_t* v[VPT][2];  // start of the V rows of each V item
   };
   struct Regs {
     u32x4_t k[KPT];
     u32x4_t v[VPT][2];
   };
+  const int32_t* bt_h = CHUNK ? a.bt + (int64_t)h * a.bt_sh : nullptr;
+  // pool-relative row of the logical global-cache index j (chunked mode)
+  auto global_row = [&](int j) -> int64_t {
+    return (int64_t)bt_h[j / a.page] * a.page + j % a.page;
+  };
+  // K / V row starts of key position p (band keys)
+  auto band_rows = [&](int p, const uint16_t*& kr, const uint16_t*& vr) {
+    if (CHUNK && p < a.c0) {
+      const int64_t row = a.ring_row0 + (int64_t)h * a.W + (p - (a.c0 - a.W));
+      kr = a.pool_k + row * D;
+      vr = a.pool_v + row * D;
+    } else {
+      const int64_t off = (int64_t)(p - (CHUNK ? a.c0 : 0)) * a.kv_ss;
+      kr = kbase + off;
+      vr = vbase + off;
+    }
+  };
   auto tile_keys = [&](int tl, Keys& ks) {
     if (tl < n_vtiles) {
       const int nval = min(kBlk, nv - tl * kBlk);
-      const int32_t* ci = cidx + tl * kBlk;
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) ks.k[i] = krow[i] >= 0 ? ci[min(krow[i], nval - 1)] : 0;
+      for (int i = 0; i < KPT; ++i) {
+        const int e = min(max(krow[i], 0), nval - 1);
+        if (CHUNK) ks.k[i] = a.pool_k + global_row(tl * kBlk + e) * D;
+        else ks.k[i] = kbase + (int64_t)cidx[tl * kBlk + e] * a.kv_ss;
+      }
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) ks.v[i][j] = vkp[i] >= 0 ? ci[min(2 * vkp[i] + j, nval - 1)] : 0;
+        for (int j = 0; j < 2; ++j) {
+          const int e = min(2 * max(vkp[i], 0) + j, nval - 1);
+          if (CHUNK) ks.v[i][j] = a.pool_v + global_row(tl * kBlk + e) * D;
+          else ks.v[i][j] = vbase + (int64_t)cidx[tl * kBlk + e] * a.kv_ss;
+        }
     } else {
-      const int b0 = a.block_offset[r * a.bo_width + (tl - n_vtiles)];
+      const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : a.block_offset[r * a.bo_width + (tl - n_vtiles)];
+      const uint16_t* dummy;
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) ks.k[i] = min(b0 + max(krow[i], 0), a.S - 1);
+      for (int i = 0; i < KPT; ++i) band_rows(min(b0 + max(krow[i], 0), a.S - 1), ks.k[i], dummy);
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) ks.v[i][j] = min(b0 + 2 * max(vkp[i], 0) + j, a.S - 1);
+        for (int j = 0; j < 2; ++j) band_rows(min(b0 + 2 * max(vkp[i], 0) + j, a.S - 1), dummy, ks.v[i][j]);
     }
   };
   auto tile_load = [&](const Keys& ks, Regs& rg) {
 #pragma unroll
     for (int i = 0; i < KPT; ++i)
-      if (krow[i] >= 0) rg.k[i] = *(const u32x4_t*)(kbase + (int64_t)ks.k[i] * a.kv_ss + kcol[i] * 8);
+      if (krow[i] >= 0) rg.k[i] = *(const u32x4_t*)(ks.k[i] + kcol[i] * 8);
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
       if (vkp[i] >= 0)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) rg.v[i][j] = *(const u32x4_t*)(vbase + (int64_t)ks.v[i][j] * a.kv_ss + vcol[i] * 8);
+        for (int j = 0; j < 2; ++j) rg.v[i][j] = *(const u32x4_t*)(ks.v[i][j] + vcol[i] * 8);
   };
 
   Keys keys_next;
@@ -161,7 +207,7 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     const bool vert = tile < n_vtiles;
     int band0 = 0, nvalid = kBlk;
     if (vert) nvalid = min(kBlk, nv - tile * kBlk);
-    else band0 = a.block_offset[r * a.bo_width + (tile - n_vtiles)];
+    else band0 = CHUNK ? band_start + (tile - n_vtiles) * kBlk : a.block_offset[r * a.bo_width + (tile - n_vtiles)];
 
     __syncthreads();  // the previous tile's LDS reads are done
 #pragma unroll
@@ -279,8 +325,8 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     l += __shfl_xor(l, 16);
     l += __shfl_xor(l, 32);
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int s = row0 + rt * 16 + n;
-    if (s < a.S) {
+    const int s = lrow0 + rt * 16 + n;
+    if (s < nrows) {
       uint16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh;
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -293,9 +339,20 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
 }
 
 template <int D, int G>
-hipError_t launch(const PrefillArgs& a, hipStream_t st) {
-  hipLaunchKernelGGL((sparse_prefill_kernel<D, G>), dim3(a.R, a.B * a.Hkv), dim3(128 * G), 0, st, a);
+hipError_t launch(const PrefillArgs& a, hipStream_t st, bool chunked) {
+  if (chunked)
+    hipLaunchKernelGGL((sparse_prefill_kernel<D, G, true>), dim3(a.R, a.B * a.Hkv), dim3(128 * G), 0, st, a);
+  else
+    hipLaunchKernelGGL((sparse_prefill_kernel<D, G, false>), dim3(a.R, a.B * a.Hkv), dim3(128 * G), 0, st, a);
   return hipGetLastError();
+}
+
+hipError_t launch_any(const PrefillArgs& a, hipStream_t st, int head_dim, int G, bool chunked) {
+  if (head_dim == 128)
+    return G == 1 ? launch<128, 1>(a, st, chunked) : G == 2 ? launch<128, 2>(a, st, chunked)
+         : G == 4 ? launch<128, 4>(a, st, chunked) : launch<128, 8>(a, st, chunked);
+  return G == 1 ? launch<64, 1>(a, st, chunked) : G == 2 ? launch<64, 2>(a, st, chunked)
+       : G == 4 ? launch<64, 4>(a, st, chunked) : launch<64, 8>(a, st, chunked);
 }
 
 }  // namespace
@@ -342,12 +399,63 @@ extern "C" int wgkv_sparse_prefill_attn(
   a.Hkv = num_kv_heads;
   a.R = (seq_len + kBlk - 1) / kBlk;
   a.scale_log2 = softmax_scale * kLog2e;
-  hipStream_t st = (hipStream_t)stream;
-  hipError_t e;
-  if (head_dim == 128) {
-    e = G == 1 ? launch<128, 1>(a, st) : G == 2 ? launch<128, 2>(a, st) : G == 4 ? launch<128, 4>(a, st) : launch<128, 8>(a, st);
-  } else {
-    e = G == 1 ? launch<64, 1>(a, st) : G == 2 ? launch<64, 2>(a, st) : G == 4 ? launch<64, 4>(a, st) : launch<64, 8>(a, st);
-  }
+  a.c0 = 0;
+  a.W = 0;
+  a.page = 16;
+  a.pool_k = a.pool_v = nullptr;
+  a.bt = nullptr;
+  a.bt_sh = 0;
+  a.ring_row0 = 0;
+  const hipError_t e = launch_any(a, (hipStream_t)stream, head_dim, G, false);
+  return e == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_chunk_prefill_attn(
+    const void* q, int64_t q_ss, int64_t q_sh,
+    const void* k, const void* v, int64_t kv_ss, int64_t kv_sh,
+    void* out, int64_t o_ss, int64_t o_sh,
+    const void* pool_k, const void* pool_v,
+    const int32_t* block_table, int32_t max_pages_per_head,
+    const int32_t* column_count,
+    int32_t layer, int32_t chunk_start, int32_t chunk_len,
+    int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, float softmax_scale, void* stream) {
+  if (!q || !k || !v || !out || !pool_k || !pool_v || !block_table || !column_count) return WGKV_ERR_ARG;
+  if (chunk_len <= 0 || chunk_start < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return WGKV_ERR_ARG;
+  if (local_window <= 0 || local_window % kBlk || chunk_start % kBlk || page_size <= 0 || local_window % page_size)
+    return WGKV_ERR_ARG;
+  if (chunk_start > 0 && chunk_start < local_window) return WGKV_ERR_ARG;  // the ring must be full
+  const int G = num_q_heads / num_kv_heads;
+  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return WGKV_ERR_UNSUPPORTED;
+  if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)pool_k | (uintptr_t)pool_v) & 15)
+    return WGKV_ERR_UNSUPPORTED;
+  if ((q_ss | q_sh | kv_ss | kv_sh | o_ss | o_sh) & 7) return WGKV_ERR_UNSUPPORTED;
+  PrefillArgs a = {};
+  a.q = (const uint16_t*)q;
+  a.q_ss = q_ss;
+  a.q_sh = q_sh;
+  a.k = (const uint16_t*)k;
+  a.v = (const uint16_t*)v;
+  a.kv_ss = kv_ss;
+  a.kv_sh = kv_sh;
+  a.out = (uint16_t*)out;
+  a.o_ss = o_ss;
+  a.o_sh = o_sh;
+  a.column_count = column_count;
+  a.B = 1;
+  a.S = chunk_start + chunk_len;
+  a.Hkv = num_kv_heads;
+  a.R = (chunk_len + kBlk - 1) / kBlk;
+  a.scale_log2 = softmax_scale * kLog2e;
+  a.c0 = chunk_start;
+  a.W = local_window;
+  a.page = page_size;
+  a.pool_k = (const uint16_t*)pool_k;
+  a.pool_v = (const uint16_t*)pool_v;
+  a.bt = block_table + ((int64_t)layer * num_kv_heads) * max_pages_per_head + local_window / page_size;
+  a.bt_sh = max_pages_per_head;
+  a.ring_row0 = (int64_t)layer * num_kv_heads * local_window;
+  const hipError_t e = launch_any(a, (hipStream_t)stream, head_dim, G, true);
   return e == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

@@ -90,6 +90,28 @@ SIGNATURES = {
         c_ptr, c_ptr, c_i64, c_i64,
         c_i32, c_i32, c_i32, c_i32, c_i32,
         c_i32, c_f32, c_ptr]),
+    "wgkv_chunk_admit_workspace_bytes": (c_size, [c_i32, c_i32, c_i32]),
+    "wgkv_chunk_cache_update": (ctypes.c_int, [
+        c_i32,
+        c_ptr, c_ptr, c_i64, c_i64,
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_i64,
+        c_i32, c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32, c_i64,
+        c_ptr, c_ptr, c_ptr, c_i32,
+        c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr, c_ptr,
+        c_ptr, c_size, c_ptr]),
+    "wgkv_chunk_prefill_attn": (ctypes.c_int, [
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_ptr, c_i64, c_i64,
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_ptr,
+        c_ptr, c_i32,
+        c_ptr,
+        c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_f32, c_ptr]),
 }
 
 _lib = None

@@ -59,6 +59,8 @@ class DualCache:
                               if getattr(config, "g_defer", False) else None)
         self.local_ptr = 0
         self.local_length = 0
+        self.prefill_length = 0  # prompt tokens in the cache (all layers); chunks continue from here
+        self.decode_started = False
         self.next_free_block_dev = torch.full((1,), n_local, **i32)
         self.status = torch.zeros(1, **i32)
         self.cache_seqlens = torch.zeros(L, 1, H, **i32)   # decode lengths, one row per layer

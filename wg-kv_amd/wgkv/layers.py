@@ -97,16 +97,43 @@ def migrate_local_kv_to_global(self, past_key_value, device, local_blocks_per_he
 
 def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
                     batch_size, q_seq_len, device, g_mask, local_blocks_per_head):
-    """src/modeling_layers.py:1183-1376.  Tensors are (B, H, S, D); B = 1."""
+    """src/modeling_layers.py:1183-1376.  Tensors are (B, H, S, D); B = 1.
+
+    The first call initialises the cache and prefills as the reference does.
+    A later call before any decode step continues the prompt as a chunk at
+    position ``cache.prefill_length`` (the reference asserts a single
+    initialisation, :1197): the cache ends as a one-shot prefill of the
+    whole prompt would, up to page numbering, and the chunk's queries attend
+    exactly as that prompt's rows would.  Continuation needs a full ring
+    (prefill_length >= W), chunks of at least W tokens and a prefill_length
+    that is a multiple of 64."""
     c = past_key_value
-    if self.layer_idx == 0:
+    W = self.config.local_window_size
+    if self.layer_idx == 0 and not (c.gated_kv_initialized and c.prefill_length > 0):
         c.initialize(self.config, self.head_dim, key_states.dtype, device)
     defer = c.local_pre_key is not None
+    c0 = c.prefill_length
+    if c0 > 0:
+        if c.decode_started:
+            raise AssertionError("prefill continuation after decode steps is not supported")
+        if c0 < W or q_seq_len < W or c0 % 64:
+            raise AssertionError(f"chunked prefill needs prefill_length >= W, chunk >= W and a 64-aligned start "
+                                 f"(prefill_length={c0}, chunk={q_seq_len}, W={W})")
+        out = ops.chunk_prefill(c, self.layer_idx, query_states[0].transpose(0, 1), key_states[0].transpose(0, 1),
+                                value_states[0].transpose(0, 1), g_mask[0], c0, self.scaling,
+                                pre_key=pre_key[0].transpose(0, 1) if (defer and pre_key is not None) else None)
+        _layer_cache_check(self, c, f"prefill_wrapper chunk at {c0} (layer {self.layer_idx})")
+        c.local_length = min(c0 + q_seq_len, W)
+        if self.layer_idx == self.config.num_hidden_layers - 1:
+            c.prefill_length = c0 + q_seq_len
+        return out.unsqueeze(0)
     ops.prefill_admit(c, self.layer_idx, key_states[0], value_states[0], g_mask[0],
                       pre_key=pre_key[0] if (defer and pre_key is not None) else None)
     _layer_cache_check(self, c, f"prefill_wrapper (layer {self.layer_idx})")
-    c.local_length = min(q_seq_len, self.config.local_window_size)  # :1297
-    meta = ops.generate_sparse_indices(g_mask, self.config.local_window_size, batch_size,
+    c.local_length = min(q_seq_len, W)  # :1297
+    if self.layer_idx == self.config.num_hidden_layers - 1:
+        c.prefill_length = q_seq_len
+    meta = ops.generate_sparse_indices(g_mask, W, batch_size,
                                        self.config.num_key_value_heads, q_seq_len, device)
     return self.prefill_kernel(
         query_states.transpose(1, 2), key_states.transpose(1, 2), value_states.transpose(1, 2),
@@ -118,6 +145,7 @@ def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, valu
     """src/modeling_layers.py:1379-1449.  Tensors are (1, H, 1, D)."""
     c = past_key_value
     W = self.config.local_window_size
+    c.decode_started = True
     insert_pos = c.local_length if c.local_length < W else c.local_ptr
     seqlens = c.cache_seqlens[self.layer_idx]
     ops.decode_append(c, self.layer_idx, key_states[0, :, 0], value_states[0, :, 0],

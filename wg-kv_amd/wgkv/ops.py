@@ -262,3 +262,73 @@ def sparse_attn_func(q, k, v, block_count, block_offset, column_count, column_in
         B, S, Hq, Hkv, D, 64, float(softmax_scale), _lib.stream_handle(q.device))
     _lib.check(st, "wgkv_sparse_prefill_attn")
     return out
+
+
+# ---------------------------------------------------------------------------
+# chunked gated prefill: kernels (1) and (3) for a prompt fed in pieces
+# ---------------------------------------------------------------------------
+def chunk_prefill(cache, layer, q, key, value, g_mask, chunk_start, softmax_scale=None, pre_key=None, out=None):
+    """One layer of one prompt chunk [chunk_start, chunk_start + C) (batch 1):
+    admission into the cache, the chunk's sparse attention, the ring rewrite.
+
+    q (C, Hq, D), key/value (C, Hkv, D) bf16 views (d contiguous; typically
+    ``x[0].transpose(0, 1)`` of the layer's (1, H, C, D) states), g_mask
+    (Hkv, C), pre_key like key (deferred gating).  Returns (C, Hq, D) bf16.
+    Capacity failures are recorded in ``cache.status`` and the chunk's cache
+    writes are skipped.
+    """
+    C, Hq, D = q.shape
+    Hkv = key.shape[1]
+    if key.shape != (C, Hkv, D) or value.shape != key.shape:
+        raise AssertionError("key/value must be (chunk_len, num_kv_heads, head_dim)")
+    if q.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+        raise TypeError("chunked prefill takes bf16 q/k/v")
+    if key.stride() != value.stride():
+        raise ValueError("key and value must share strides")
+    if g_mask.shape != (Hkv, C):
+        raise AssertionError("g_mask must be (num_kv_heads, chunk_len)")
+    _require_cuda(q, key, value, g_mask)
+    if q.stride(2) != 1 or key.stride(2) != 1:
+        raise ValueError("head_dim must be contiguous")
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    m = _u8(g_mask)
+    if m.stride(1) != 1:
+        m = m.contiguous()
+    L = _lib.lib()
+    W = cache.local_window_size
+    R = (C + 63) // 64
+    ws = workspace(key.device, L.wgkv_chunk_admit_workspace_bytes(Hkv, C, W))
+    cc = torch.empty(Hkv, R, dtype=torch.int32, device=key.device)
+    lpk = cache.local_pre_key if (pre_key is not None and cache.local_pre_key is not None) else None
+    stream = _lib.stream_handle(key.device)
+
+    def update(stage):
+        st = L.wgkv_chunk_cache_update(
+            stage,
+            _ptr(key), _ptr(value), key.stride(1), key.stride(0),
+            _ptr(pre_key) if lpk is not None else None,
+            pre_key.stride(1) if lpk is not None else 0, pre_key.stride(0) if lpk is not None else 0,
+            _ptr(m), m.stride(0),
+            layer, cache.num_layers, Hkv, chunk_start, C, D,
+            W, cache.block_size, cache.max_tokens_per_head, cache.total_blocks,
+            _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
+            _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(lpk),
+            _ptr(cache.next_free_block_dev), _ptr(cache.status), _ptr(cc),
+            _ptr(ws), ws.numel(), stream)
+        _lib.check(st, f"wgkv_chunk_cache_update(stage {stage})")
+
+    update(0)
+    if out is None:
+        out = torch.empty(C, Hq, D, dtype=torch.bfloat16, device=q.device)
+    st = L.wgkv_chunk_prefill_attn(
+        _ptr(q), q.stride(0), q.stride(1),
+        _ptr(key), _ptr(value), key.stride(0), key.stride(1),
+        _ptr(out), out.stride(0), out.stride(1),
+        _ptr(cache.block_pool_k), _ptr(cache.block_pool_v),
+        _ptr(cache.block_table), cache.block_table.shape[2],
+        _ptr(cc),
+        layer, chunk_start, C, Hq, Hkv, D, W, cache.block_size, float(softmax_scale), stream)
+    _lib.check(st, "wgkv_chunk_prefill_attn")
+    update(1)
+    return out
