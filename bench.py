@@ -103,70 +103,104 @@ def cpu_baseline(w, budget_s):
 
 
 def prefill_section(dev, steps, warmup):
-    """Config-4 shapes, one-shot over the 32K prompt: every kernel of the
-    gated prefill timed on its own (gate, admission into the dual cache,
-    metadata, sparse attention), with MFMA utilisation of the gate (fp32) and
-    of the attention (bf16, FLOPs = sum over query heads and rows of
-    4*D*|visible keys|).  The chunked per-4096 figure is the one-shot time
-    divided by the 8 chunks (the visible (query, key) set is the same)."""
+    """a 32K-token prompt in 4096-token chunks through one
+    Llama-3.1-8B-shaped layer.  Per chunk: the write gate (fp32 scores and the
+    admission mask), admission into the dual cache (compaction, page scatter,
+    column counts), the chunk's sparse attention over admitted columns plus
+    the local band, and the ring rewrite.  Each phase is bracketed by HIP
+    events on the launch stream; ms/chunk is the whole prompt's time / 8.
+    MFMA utilisation: attention FLOPs = sum over query heads and rows of
+    4*D*|visible keys| (the ideal mask), gate FLOPs = 2*(2D*inner + inner)
+    per token and head, against the dense bf16 / fp32 peaks."""
     import torch
     import wgkv
     from wgkv import ops, workloads
     from wgkv.cache import DualCache
     from wgkv.layers import WGKVConfig
 
-    S, Hq, Hkv, D, W = 32768, 32, 8, 128, 1024
+    S, Hq, Hkv, D, W, CH = 32768, 32, 8, 128, 1024, 4096
     w = workloads.prefill_llama(S=S, Hq=Hq, Hkv=Hkv, D=D, W=W, device=dev)
-    pk, kk, vv = w.pre_k.transpose(1, 2), w.k.transpose(1, 2), w.v.transpose(1, 2)
+    pk, kk, vv = w.pre_k.transpose(1, 2), w.k.transpose(1, 2), w.v.transpose(1, 2)  # (1, H, S, D) views
     mask = torch.empty(1, Hkv, S, dtype=torch.bool, device=dev)
     scores = torch.empty(1, Hkv, S, dtype=torch.float32, device=dev)
-
-    def gate():
-        w.gate.scores_and_mask(pk, kk, None, w.threshold, scores_out=scores, mask_out=mask)
-
-    t_gate = time_op(gate, steps, warmup)
+    out = torch.empty(S, Hq, D, dtype=torch.bfloat16, device=dev)
     cfg = WGKVConfig(num_hidden_layers=1, num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D,
                      hidden_size=Hq * D, local_window_size=W, max_tokens_per_head=S + W,
                      max_total_tokens=Hkv * (S + W) + 4096)
     cache = DualCache()
     cache.initialize(cfg, D, torch.bfloat16, dev)
-    snap = (cache.block_table.clone(), cache.global_lengths.clone(), cache.next_free_block_dev.clone())
+    snap = (cache.block_table.clone(), cache.global_lengths.clone(), cache.next_free_block_dev.clone(),
+            cache.local_is_global.clone())
+    chunks = [(c0, min(CH, S - c0)) for c0 in range(0, S, CH)]
+    phases = ("gate", "admit", "sparse_attn", "ring")
+    acc = {p: 0.0 for p in phases}
+    total = [0.0]
 
-    def admit():
+    def run(timed):
         cache.block_table.copy_(snap[0])
         cache.global_lengths.copy_(snap[1])
         cache.next_free_block_dev.copy_(snap[2])
-        ops.prefill_admit(cache, 0, kk[0], vv[0], mask[0])
+        cache.local_is_global.copy_(snap[3])
+        ev = []
 
-    t_admit = time_op(admit, steps, warmup)
-    meta = [None]
+        def mark():
+            if timed:
+                e = torch.cuda.Event(enable_timing=True)
+                e.record()
+                ev.append(e)
 
-    def build_meta():
-        meta[0] = wgkv.generate_sparse_indices(mask, W, 1, Hkv, S)
+        mark()
+        for c0, C in chunks:
+            sl = slice(c0, c0 + C)
+            w.gate.scores_and_mask(pk[:, :, sl], kk[:, :, sl], None, w.threshold,
+                                   scores_out=scores[:, :, sl], mask_out=mask[:, :, sl])
+            mark()
+            st = ops.ChunkStep(cache, 0, w.q[0, sl], w.k[0, sl], w.v[0, sl], mask[0, :, sl], c0,
+                               softmax_scale=D ** -0.5, out=out[sl])
+            st.admit()
+            mark()
+            st.attend()
+            mark()
+            st.ring()
+            mark()
+        if timed:
+            torch.cuda.synchronize()
+            for n in range(len(chunks)):
+                for k, p in enumerate(phases):
+                    acc[p] += ev[4 * n + k].elapsed_time(ev[4 * n + k + 1])
+            total[0] += ev[0].elapsed_time(ev[-1])
 
-    t_meta = time_op(build_meta, steps, warmup)
-    out = torch.empty_like(w.q)
-
-    def attn():
-        wgkv.sparse_attn_func(w.q, w.k, w.v, *meta[0], out=out)
-
-    t_attn = time_op(attn, steps, warmup)
+    for _ in range(warmup):
+        run(False)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        run(True)
+    if int(cache.status.item()) != 0:
+        raise RuntimeError("config-4 prefill ran out of cache capacity")
+    ms = {p: acc[p] / steps for p in phases}
+    t_total = total[0] / steps
     pairs = workloads.visible_pairs(mask[0], W)
     attn_flop = float((pairs * (Hq // Hkv)).sum().item()) * 4 * D
-    gate_flop = 2.0 * 512 * 256 * S * Hkv
+    inner = 4 * D
+    gate_flop = 2.0 * (2 * D * inner + inner) * S * Hkv
     admitted = mask.float().mean().item()
-    total = t_gate + t_admit + t_meta + t_attn
+    # the one-shot kernel over the whole prompt, for comparison (same visible set)
+    md = wgkv.generate_sparse_indices(mask, W, 1, Hkv, S)
+    out1 = torch.empty_like(w.q)
+    t_one = time_op(lambda: wgkv.sparse_attn_func(w.q, w.k, w.v, *md, out=out1), steps, warmup)
     return {
-        "workload": "prefill_llama_32k (BASELINE config 4 shapes, one-shot over the prompt)",
+        "workload": "prefill_llama_32k_chunked (BASELINE config 4: 32K prompt in 8 chunks of 4096, one layer)",
         "admitted_frac": round(admitted, 4),
-        "ms": {"gate": round(t_gate, 4), "admit": round(t_admit, 4), "meta": round(t_meta, 4),
-               "sparse_attn": round(t_attn, 4), "total": round(total, 4),
-               "per_4096_chunk_equiv": round(total / 8, 4)},
-        "sparse_attn": {"tflop": round(attn_flop / 1e12, 4), "tflops": round(attn_flop / t_attn / 1e9, 1),
-                        "mfma_frac_bf16": round(attn_flop / t_attn / 1e9 / BF16_PEAK_TFLOPS, 4),
+        "ms_per_chunk": round(t_total / len(chunks), 4),
+        "ms_prompt": round(t_total, 4),
+        "ms_per_chunk_by_phase": {p: round(ms[p] / len(chunks), 4) for p in phases},
+        "sparse_attn": {"tflop": round(attn_flop / 1e12, 4), "tflops": round(attn_flop / ms["sparse_attn"] / 1e9, 1),
+                        "mfma_frac_bf16": round(attn_flop / ms["sparse_attn"] / 1e9 / BF16_PEAK_TFLOPS, 4),
+                        "one_shot_ms": round(t_one, 4),
+                        "one_shot_mfma_frac_bf16": round(attn_flop / t_one / 1e9 / BF16_PEAK_TFLOPS, 4),
                         "dense_causal_tflop": round(4.0 * D * Hq * S * (S + 1) / 2 / 1e12, 3)},
-        "gate": {"gflop": round(gate_flop / 1e9, 2), "tflops": round(gate_flop / t_gate / 1e9, 1),
-                 "mfma_frac_fp32": round(gate_flop / t_gate / 1e9 / FP32_PEAK_TFLOPS, 4)},
+        "gate": {"gflop": round(gate_flop / 1e9, 2), "tflops": round(gate_flop / ms["gate"] / 1e9, 1),
+                 "mfma_frac_fp32": round(gate_flop / ms["gate"] / 1e9 / FP32_PEAK_TFLOPS, 4)},
     }
 
 

@@ -267,68 +267,91 @@ def sparse_attn_func(q, k, v, block_count, block_offset, column_count, column_in
 # ---------------------------------------------------------------------------
 # chunked gated prefill: kernels (1) and (3) for a prompt fed in pieces
 # ---------------------------------------------------------------------------
-def chunk_prefill(cache, layer, q, key, value, g_mask, chunk_start, softmax_scale=None, pre_key=None, out=None):
-    """One layer of one prompt chunk [chunk_start, chunk_start + C) (batch 1):
-    admission into the cache, the chunk's sparse attention, the ring rewrite.
+class ChunkStep:
+    """One layer of one prompt chunk [chunk_start, chunk_start + C) (batch 1),
+    in its three device steps: ``admit()`` (admission into the cache and the
+    chunk's column counts), ``attend()`` (the chunk's sparse attention) and
+    ``ring()`` (the ring rewrite), in that order.  ``chunk_prefill`` runs all
+    three.
 
     q (C, Hq, D), key/value (C, Hkv, D) bf16 views (d contiguous; typically
     ``x[0].transpose(0, 1)`` of the layer's (1, H, C, D) states), g_mask
-    (Hkv, C), pre_key like key (deferred gating).  Returns (C, Hq, D) bf16.
-    Capacity failures are recorded in ``cache.status`` and the chunk's cache
-    writes are skipped.
+    (Hkv, C), pre_key like key (deferred gating).  Capacity failures are
+    recorded in ``cache.status`` and the chunk's cache writes are skipped.
     """
-    C, Hq, D = q.shape
-    Hkv = key.shape[1]
-    if key.shape != (C, Hkv, D) or value.shape != key.shape:
-        raise AssertionError("key/value must be (chunk_len, num_kv_heads, head_dim)")
-    if q.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
-        raise TypeError("chunked prefill takes bf16 q/k/v")
-    if key.stride() != value.stride():
-        raise ValueError("key and value must share strides")
-    if g_mask.shape != (Hkv, C):
-        raise AssertionError("g_mask must be (num_kv_heads, chunk_len)")
-    _require_cuda(q, key, value, g_mask)
-    if q.stride(2) != 1 or key.stride(2) != 1:
-        raise ValueError("head_dim must be contiguous")
-    if softmax_scale is None:
-        softmax_scale = D ** -0.5
-    m = _u8(g_mask)
-    if m.stride(1) != 1:
-        m = m.contiguous()
-    L = _lib.lib()
-    W = cache.local_window_size
-    R = (C + 63) // 64
-    ws = workspace(key.device, L.wgkv_chunk_admit_workspace_bytes(Hkv, C, W))
-    cc = torch.empty(Hkv, R, dtype=torch.int32, device=key.device)
-    lpk = cache.local_pre_key if (pre_key is not None and cache.local_pre_key is not None) else None
-    stream = _lib.stream_handle(key.device)
 
-    def update(stage):
-        st = L.wgkv_chunk_cache_update(
+    def __init__(self, cache, layer, q, key, value, g_mask, chunk_start, softmax_scale=None, pre_key=None,
+                 out=None):
+        C, Hq, D = q.shape
+        Hkv = key.shape[1]
+        if key.shape != (C, Hkv, D) or value.shape != key.shape:
+            raise AssertionError("key/value must be (chunk_len, num_kv_heads, head_dim)")
+        if q.dtype != torch.bfloat16 or key.dtype != torch.bfloat16 or value.dtype != torch.bfloat16:
+            raise TypeError("chunked prefill takes bf16 q/k/v")
+        if key.stride() != value.stride():
+            raise ValueError("key and value must share strides")
+        if g_mask.shape != (Hkv, C):
+            raise AssertionError("g_mask must be (num_kv_heads, chunk_len)")
+        _require_cuda(q, key, value, g_mask)
+        if q.stride(2) != 1 or key.stride(2) != 1:
+            raise ValueError("head_dim must be contiguous")
+        m = _u8(g_mask)
+        if m.stride(1) != 1:
+            m = m.contiguous()
+        self.cache, self.layer, self.q, self.key, self.value, self.mask = cache, layer, q, key, value, m
+        self.c0, self.C, self.Hq, self.Hkv, self.D = chunk_start, C, Hq, Hkv, D
+        self.scale = D ** -0.5 if softmax_scale is None else softmax_scale
+        self.lib = _lib.lib()
+        W = cache.local_window_size
+        self.ws = workspace(key.device, self.lib.wgkv_chunk_admit_workspace_bytes(Hkv, C, W))
+        self.column_count = torch.empty(Hkv, (C + 63) // 64, dtype=torch.int32, device=key.device)
+        self.lpk = cache.local_pre_key if (pre_key is not None and cache.local_pre_key is not None) else None
+        self.pre_key = pre_key
+        self.out = out if out is not None else torch.empty(C, Hq, D, dtype=torch.bfloat16, device=q.device)
+        self.stream = _lib.stream_handle(key.device)
+
+    def _update(self, stage):
+        c, k, pk, lpk = self.cache, self.key, self.pre_key, self.lpk
+        st = self.lib.wgkv_chunk_cache_update(
             stage,
-            _ptr(key), _ptr(value), key.stride(1), key.stride(0),
-            _ptr(pre_key) if lpk is not None else None,
-            pre_key.stride(1) if lpk is not None else 0, pre_key.stride(0) if lpk is not None else 0,
-            _ptr(m), m.stride(0),
-            layer, cache.num_layers, Hkv, chunk_start, C, D,
-            W, cache.block_size, cache.max_tokens_per_head, cache.total_blocks,
-            _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
-            _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(lpk),
-            _ptr(cache.next_free_block_dev), _ptr(cache.status), _ptr(cc),
-            _ptr(ws), ws.numel(), stream)
+            _ptr(k), _ptr(self.value), k.stride(1), k.stride(0),
+            _ptr(pk) if lpk is not None else None,
+            pk.stride(1) if lpk is not None else 0, pk.stride(0) if lpk is not None else 0,
+            _ptr(self.mask), self.mask.stride(0),
+            self.layer, c.num_layers, self.Hkv, self.c0, self.C, self.D,
+            c.local_window_size, c.block_size, c.max_tokens_per_head, c.total_blocks,
+            _ptr(c.block_pool_k), _ptr(c.block_pool_v), _ptr(c.block_table), c.block_table.shape[2],
+            _ptr(c.global_lengths), _ptr(c.local_is_global.view(torch.uint8)), _ptr(lpk),
+            _ptr(c.next_free_block_dev), _ptr(c.status), _ptr(self.column_count),
+            _ptr(self.ws), self.ws.numel(), self.stream)
         _lib.check(st, f"wgkv_chunk_cache_update(stage {stage})")
 
-    update(0)
-    if out is None:
-        out = torch.empty(C, Hq, D, dtype=torch.bfloat16, device=q.device)
-    st = L.wgkv_chunk_prefill_attn(
-        _ptr(q), q.stride(0), q.stride(1),
-        _ptr(key), _ptr(value), key.stride(0), key.stride(1),
-        _ptr(out), out.stride(0), out.stride(1),
-        _ptr(cache.block_pool_k), _ptr(cache.block_pool_v),
-        _ptr(cache.block_table), cache.block_table.shape[2],
-        _ptr(cc),
-        layer, chunk_start, C, Hq, Hkv, D, W, cache.block_size, float(softmax_scale), stream)
-    _lib.check(st, "wgkv_chunk_prefill_attn")
-    update(1)
+    def admit(self):
+        self._update(0)
+
+    def attend(self):
+        c, q, k, o = self.cache, self.q, self.key, self.out
+        st = self.lib.wgkv_chunk_prefill_attn(
+            _ptr(q), q.stride(0), q.stride(1),
+            _ptr(k), _ptr(self.value), k.stride(0), k.stride(1),
+            _ptr(o), o.stride(0), o.stride(1),
+            _ptr(c.block_pool_k), _ptr(c.block_pool_v),
+            _ptr(c.block_table), c.block_table.shape[2],
+            _ptr(self.column_count),
+            self.layer, self.c0, self.C, self.Hq, self.Hkv, self.D, c.local_window_size, c.block_size,
+            float(self.scale), self.stream)
+        _lib.check(st, "wgkv_chunk_prefill_attn")
+        return o
+
+    def ring(self):
+        self._update(1)
+
+
+def chunk_prefill(cache, layer, q, key, value, g_mask, chunk_start, softmax_scale=None, pre_key=None, out=None):
+    """Admission, sparse attention and ring rewrite of one layer of one prompt
+    chunk (see ChunkStep).  Returns the chunk's (C, Hq, D) bf16 output."""
+    step = ChunkStep(cache, layer, q, key, value, g_mask, chunk_start, softmax_scale, pre_key, out)
+    step.admit()
+    out = step.attend()
+    step.ring()
     return out
