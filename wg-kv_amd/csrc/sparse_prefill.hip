@@ -23,6 +23,30 @@ namespace {
 
 constexpr int kBlk = 64;     // query rows per block and keys per tile
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.f;  // log2 units a row maximum may grow before O / l are rescaled
+
+// IEEE-754-2019 maximum (v_maximum3_f32): unlike fmaxf it needs no
+// canonicalisation of its operands, and -inf (masked scores) is ordered.
+__device__ __forceinline__ float fmax_ieee(float x, float y) { return __builtin_elementwise_maximum(x, y); }
+
+// max of x over lanes i and i^16 / i^32 (v_permlane16_swap / v_permlane32_swap)
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmax_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmax_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -38,7 +62,7 @@ struct PrefillArgs {
   const int32_t* column_count;
   const int32_t* column_index;
   int64_t ci_sb, ci_sh;  // column_index strides (batch, head); positions contiguous
-  int B, S, Hkv, R;
+  int B, S, Hkv, R, G;
   float scale_log2;
   // chunked mode: queries/outputs and the chunk's k/v are chunk-relative rows
   // of positions c0 .. c0+C-1; S = c0 + C bounds the keys.  Admitted columns
@@ -53,18 +77,18 @@ struct PrefillArgs {
   int64_t ring_row0;
 };
 
-template <int D, int G, bool CHUNK>
-__global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) {
-  constexpr int NT = 128 * G;      // threads
+template <int D, int HPW, bool CHUNK>
+__global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a) {
+  constexpr int NT = 128 * HPW;    // threads
   constexpr int KS = D / 32;       // k-steps over head_dim
   constexpr int DT = D / 16;       // 16-wide d tiles
   constexpr int CH = D / 8;        // 16-byte slices per row
   constexpr int LDK = D + 8;       // K tile row stride (elements)
-  constexpr int LDV = kBlk + 8;    // V^T tile row stride (elements)
+  constexpr int LDV = kBlk + 4;    // V^T tile row stride (elements)
   constexpr int KITEMS = kBlk * CH;         // (row, slice) items of a K tile
   constexpr int VITEMS = (kBlk / 2) * CH;   // (key pair, slice) items of a V tile
-  __shared__ __attribute__((aligned(16))) uint16_t sK[kBlk * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sVt[D * LDV];
+  __shared__ __attribute__((aligned(16))) uint16_t sKb[2][kBlk * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t sVtb[2][D * LDV];
 
   const int r = blockIdx.x;
   const int bh = blockIdx.y;
@@ -72,7 +96,7 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   const int t = threadIdx.x;
   const int lane = t & 63, wid = t >> 6;
   const int n = lane & 15, g = lane >> 4;
-  const int hq = h * G + (wid >> 1);
+  const int hq = h * a.G + blockIdx.z * HPW + (wid >> 1);
   const int lrow0 = r * kBlk + (wid & 1) * 32;   // first query row of this wave (tensor row)
   const int row0 = (CHUNK ? a.c0 : 0) + lrow0;   // its position
   const int nrows = a.S - (CHUNK ? a.c0 : 0);    // query rows in the tensors
@@ -117,6 +141,8 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   // ahead, so both latencies overlap the current tile's arithmetic.
   constexpr int KPT = (KITEMS + NT - 1) / NT;
   constexpr int VPT = (VITEMS + NT - 1) / NT;
+  constexpr bool KFULL = KITEMS % NT == 0;  // every thread has all its K items
+  constexpr bool VFULL = VITEMS % NT == 0;
   int krow[KPT], kcol[KPT], vkp[VPT], vcol[VPT];
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
@@ -128,79 +154,92 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   for (int i = 0; i < VPT; ++i) {
     const int e = t + i * NT;
     vkp[i] = e < VITEMS ? e % (kBlk / 2) : -1;
-    vcol[i] = e / (kBlk / 2);
+    {
+      // slices x and x^1 (the two half-waves) land 2 slices apart: bank-disjoint V^T writes
+      const int x = e / (kBlk / 2);
+      vcol[i] = (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
+    }
   }
-  struct Keys {
-    const uint16_t* k[KPT];     // start of the K row of each K item
-    const uint16_t* v[VPT][2];  // start of the V rows of each V item
+  // A tile's rows are fetched in two stages.  Two tiles ahead, tile_idx
+  // loads the indirections -- the admitted columns' positions or, in chunked
+  // mode, the page ids of the global-cache entries (band rows need none) --
+  // into registers; one tile ahead, tile_load turns them into row addresses
+  // and loads the rows.  Keeping the dependent index loads a tile ahead of
+  // the row loads means no wait for an index also waits for the rows issued
+  // before it (memory counters retire in order).
+  struct Idx {
+    int k[KPT];     // per K item: column position / page id / band position
+    int v[VPT][2];  // per V item (two keys)
   };
   struct Regs {
     u32x4_t k[KPT];
     u32x4_t v[VPT][2];
   };
   const int32_t* bt_h = CHUNK ? a.bt + (int64_t)h * a.bt_sh : nullptr;
-  // pool-relative row of the logical global-cache index j (chunked mode)
-  auto global_row = [&](int j) -> int64_t {
-    return (int64_t)bt_h[j / a.page] * a.page + j % a.page;
-  };
-  // K / V row starts of key position p (band keys)
-  auto band_rows = [&](int p, const uint16_t*& kr, const uint16_t*& vr) {
-    if (CHUNK && p < a.c0) {
-      const int64_t row = a.ring_row0 + (int64_t)h * a.W + (p - (a.c0 - a.W));
-      kr = a.pool_k + row * D;
-      vr = a.pool_v + row * D;
-    } else {
-      const int64_t off = (int64_t)(p - (CHUNK ? a.c0 : 0)) * a.kv_ss;
-      kr = kbase + off;
-      vr = vbase + off;
-    }
-  };
-  auto tile_keys = [&](int tl, Keys& ks) {
+  auto tile_idx = [&](int tl, Idx& ix) {
     if (tl < n_vtiles) {
       const int nval = min(kBlk, nv - tl * kBlk);
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
-        const int e = min(max(krow[i], 0), nval - 1);
-        if (CHUNK) ks.k[i] = a.pool_k + global_row(tl * kBlk + e) * D;
-        else ks.k[i] = kbase + (int64_t)cidx[tl * kBlk + e] * a.kv_ss;
+        const int j = tl * kBlk + min(max(krow[i], 0), nval - 1);
+        ix.k[i] = CHUNK ? bt_h[j / a.page] : cidx[j];
       }
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int e = min(2 * max(vkp[i], 0) + j, nval - 1);
-          if (CHUNK) ks.v[i][j] = a.pool_v + global_row(tl * kBlk + e) * D;
-          else ks.v[i][j] = vbase + (int64_t)cidx[tl * kBlk + e] * a.kv_ss;
+        for (int u = 0; u < 2; ++u) {
+          const int j = tl * kBlk + min(2 * max(vkp[i], 0) + u, nval - 1);
+          ix.v[i][u] = CHUNK ? bt_h[j / a.page] : cidx[j];
         }
     } else {
       const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : a.block_offset[r * a.bo_width + (tl - n_vtiles)];
-      const uint16_t* dummy;
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) band_rows(min(b0 + max(krow[i], 0), a.S - 1), ks.k[i], dummy);
+      for (int i = 0; i < KPT; ++i) ix.k[i] = min(b0 + max(krow[i], 0), a.S - 1);
 #pragma unroll
       for (int i = 0; i < VPT; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) band_rows(min(b0 + 2 * max(vkp[i], 0) + j, a.S - 1), dummy, ks.v[i][j]);
+        for (int u = 0; u < 2; ++u) ix.v[i][u] = min(b0 + 2 * max(vkp[i], 0) + u, a.S - 1);
     }
   };
-  auto tile_load = [&](const Keys& ks, Regs& rg) {
+  // row start of key x of tile tl in the K (or V) source
+  auto row_ptr = [&](int tl, bool vertical, int x, int key_in_tile, const uint16_t* tensor_base,
+                     const uint16_t* pool) -> const uint16_t* {
+    if (vertical) {
+      if (CHUNK) {
+        const int j = tl * kBlk + key_in_tile;
+        return pool + ((int64_t)x * a.page + j % a.page) * D;
+      }
+      return tensor_base + (int64_t)x * a.kv_ss;
+    }
+    if (CHUNK && x < a.c0) return pool + (a.ring_row0 + (int64_t)h * a.W + (x - (a.c0 - a.W))) * D;
+    return tensor_base + (int64_t)(x - (CHUNK ? a.c0 : 0)) * a.kv_ss;
+  };
+  auto tile_load = [&](int tl, const Idx& ix, Regs& rg) {
+    const bool vertical = tl < n_vtiles;
+    const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
 #pragma unroll
     for (int i = 0; i < KPT; ++i)
-      if (krow[i] >= 0) rg.k[i] = *(const u32x4_t*)(ks.k[i] + kcol[i] * 8);
+      if (KFULL || krow[i] >= 0) {
+        const uint16_t* row = row_ptr(tl, vertical, ix.k[i], min(krow[i], nval - 1), kbase, a.pool_k);
+        rg.k[i] = *(const u32x4_t*)(row + kcol[i] * 8);
+      }
 #pragma unroll
     for (int i = 0; i < VPT; ++i)
-      if (vkp[i] >= 0)
+      if (VFULL || vkp[i] >= 0)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) rg.v[i][j] = *(const u32x4_t*)(ks.v[i][j] + vcol[i] * 8);
+        for (int u = 0; u < 2; ++u) {
+          const uint16_t* row = row_ptr(tl, vertical, ix.v[i][u], min(2 * vkp[i] + u, nval - 1), vbase, a.pool_v);
+          rg.v[i][u] = *(const u32x4_t*)(row + vcol[i] * 8);
+        }
   };
 
-  Keys keys_next;
+  Idx idx_next;
   Regs regs;
   if (ntiles > 0) {
-    Keys k0;
-    tile_keys(0, k0);
-    tile_load(k0, regs);
-    if (ntiles > 1) tile_keys(1, keys_next);
+    Idx i0;
+    tile_idx(0, i0);
+    tile_load(0, i0, regs);
+    if (ntiles > 1) tile_idx(1, idx_next);
   }
 
   for (int tile = 0; tile < ntiles; ++tile) {
@@ -209,13 +248,14 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     if (vert) nvalid = min(kBlk, nv - tile * kBlk);
     else band0 = CHUNK ? band_start + (tile - n_vtiles) * kBlk : a.block_offset[r * a.bo_width + (tile - n_vtiles)];
 
-    __syncthreads();  // the previous tile's LDS reads are done
+    uint16_t* sK = sKb[tile & 1];
+    uint16_t* sVt = sVtb[tile & 1];
 #pragma unroll
     for (int i = 0; i < KPT; ++i)
-      if (krow[i] >= 0) *(u32x4_t*)(&sK[krow[i] * LDK + kcol[i] * 8]) = regs.k[i];
+      if (KFULL || krow[i] >= 0) *(u32x4_t*)(&sK[krow[i] * LDK + kcol[i] * 8]) = regs.k[i];
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
-      if (vkp[i] < 0) continue;
+      if (!VFULL && vkp[i] < 0) continue;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const uint32_t lo = (regs.v[i][0][w] & 0xffffu) | (regs.v[i][1][w] << 16);
@@ -227,70 +267,85 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     __syncthreads();
     // the next tile's rows stream in under this tile's arithmetic
     if (tile + 1 < ntiles) {
-      tile_load(keys_next, regs);
-      if (tile + 2 < ntiles) tile_keys(tile + 2, keys_next);
+      tile_load(tile + 1, idx_next, regs);
+      if (tile + 2 < ntiles) tile_idx(tile + 2, idx_next);
     }
 
     // ---- S^T = K Q^T: key tiles kt (16 keys) x row tiles rt ------------------
     f32x4_t sc[4][2];
+    // k-step outer: the 8 accumulators are independent chains, so
+    // consecutive MFMAs never wait on each other
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      bf16x8_t kf[KS];
+    for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
-      for (int j = 0; j < KS; ++j)
-        kf[j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[(kt * 16 + n) * LDK + (j * 4 + g) * 8]));
+      for (int rt = 0; rt < 2; ++rt) sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < KS; ++j) {
+      bf16x8_t kf[4];
 #pragma unroll
-        for (int j = 0; j < KS; ++j)
-          sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j], qb[rt][j], sc[kt][rt], 0, 0, 0);
-      }
+      for (int kt = 0; kt < 4; ++kt)
+        kf[kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[(kt * 16 + n) * LDK + (j * 4 + g) * 8]));
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt)
+          sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt], qb[rt][j], sc[kt][rt], 0, 0, 0);
     }
     // tiles whose 64 keys are all visible to all 32 rows of the wave skip masking
     const bool full = vert ? nvalid == kBlk : (band0 + kBlk - 1 <= row0 && band0 + kBlk <= a.S);
     // ---- online softmax (lane: query row rt*16+n, keys kt*16+4g+i) -------------
-    bf16x8_t pb[2][2];  // [rt][k-step of 32 keys]
+    // Row maxima are taken on the raw scores (the scale is positive) and the
+    // scale is folded into the exponent's FMA.  The reference maximum m_run of
+    // a row moves only when a tile's maximum exceeds it by more than 8 (log2
+    // units), so p <= 2^8 and the O / l rescale runs on few tiles.
+    float mxs[2];
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
-      const int qrow = row0 + rt * 16 + n;
-      float mx = -INFINITY;
-      if (full) {
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            sc[kt][rt][i] *= a.scale_log2;
-            mx = fmaxf(mx, sc[kt][rt][i]);
-          }
-      } else {
+      if (!full) {
+        // visible keys of this row are kk < lim
+        const int qrow = row0 + rt * 16 + n;
+        const int lim = vert ? nvalid : min(a.S - band0, qrow - band0 + 1);
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kk = kt * 16 + 4 * g + i;
-            const bool ok = vert ? kk < nvalid : (band0 + kk < a.S && band0 + kk <= qrow);
-            const float x = ok ? sc[kt][rt][i] * a.scale_log2 : -INFINITY;
-            sc[kt][rt][i] = x;
-            mx = fmaxf(mx, x);
+            sc[kt][rt][i] = kk < lim ? sc[kt][rt][i] : -INFINITY;
           }
       }
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mn = fmaxf(m_run[rt], mx);
-      const float mref = mn == -INFINITY ? 0.f : mn;  // rows with nothing visible yet keep p = 0
-      const float alpha = fast_exp2(m_run[rt] - mref);
-      m_run[rt] = mn;
-      l_part[rt] *= alpha;
+      float mx = -INFINITY;
 #pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
+      for (int kt = 0; kt < 4; ++kt)
+        mx = fmax_ieee(mx, fmax_ieee(fmax_ieee(sc[kt][rt][0], sc[kt][rt][1]), fmax_ieee(sc[kt][rt][2], sc[kt][rt][3])));
+      mx = xor16_max(mx);
+      mx = xor32_max(mx);
+      mxs[rt] = mx * a.scale_log2;
+    }
+    const bool need0 = mxs[0] > m_run[0] + kRescaleSlack;
+    const bool need1 = mxs[1] > m_run[1] + kRescaleSlack;
+    if (__builtin_amdgcn_ballot_w64(need0 || need1) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const bool need = rt == 0 ? need0 : need1;
+        const float mnew = need ? mxs[rt] : m_run[rt];
+        const float alpha = mnew == m_run[rt] ? 1.f : fast_exp2(m_run[rt] - mnew);
+        m_run[rt] = mnew;
+        l_part[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
+      }
+    }
+    bf16x8_t pb[2][2];  // [rt][k-step of 32 keys]
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];  // rows with nothing visible keep p = 0
       uint32_t pw[8];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int i = 0; i < 4; i += 2) {
-          const float p0 = fast_exp2(sc[kt][rt][i] - mref);
-          const float p1 = fast_exp2(sc[kt][rt][i + 1] - mref);
+          const float p0 = fast_exp2(fmaf(sc[kt][rt][i], a.scale_log2, -mref));
+          const float p1 = fast_exp2(fmaf(sc[kt][rt][i + 1], a.scale_log2, -mref));
           l_part[rt] += p0 + p1;
           pw[kt * 2 + i / 2] = pack_bf16x2(p0, p1);
         }
@@ -303,9 +358,9 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
     }
     // ---- O^T += V^T P^T ------------------------------------------------------
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt) {
+    for (int s = 0; s < 2; ++s) {
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+      for (int dt = 0; dt < DT; ++dt) {
         const uint16_t* vt = &sVt[(dt * 16 + n) * LDV + s * 32 + 4 * g];
         const uint64_t lo = *(const uint64_t*)vt;
         const uint64_t hi = *(const uint64_t*)(vt + 16);
@@ -322,8 +377,8 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
     float l = l_part[rt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    l = xor16_sum(l);
+    l = xor32_sum(l);
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int s = lrow0 + rt * 16 + n;
     if (s < nrows) {
@@ -338,21 +393,30 @@ __global__ __launch_bounds__(128 * G) void sparse_prefill_kernel(PrefillArgs a) 
   }
 }
 
-template <int D, int G>
+template <int D, int HPW>
 hipError_t launch(const PrefillArgs& a, hipStream_t st, bool chunked) {
+  const dim3 grid(a.R, a.B * a.Hkv, a.G / HPW);
   if (chunked)
-    hipLaunchKernelGGL((sparse_prefill_kernel<D, G, true>), dim3(a.R, a.B * a.Hkv), dim3(128 * G), 0, st, a);
+    hipLaunchKernelGGL((sparse_prefill_kernel<D, HPW, true>), grid, dim3(128 * HPW), 0, st, a);
   else
-    hipLaunchKernelGGL((sparse_prefill_kernel<D, G, false>), dim3(a.R, a.B * a.Hkv), dim3(128 * G), 0, st, a);
+    hipLaunchKernelGGL((sparse_prefill_kernel<D, HPW, false>), grid, dim3(128 * HPW), 0, st, a);
   return hipGetLastError();
 }
 
-hipError_t launch_any(const PrefillArgs& a, hipStream_t st, int head_dim, int G, bool chunked) {
+// Query heads per workgroup: min(G, kHeadsPerWg)
+#ifndef WGKV_PREFILL_HPW
+#define WGKV_PREFILL_HPW 4
+#endif
+constexpr int kHeadsPerWg = WGKV_PREFILL_HPW;
+
+hipError_t launch_any(PrefillArgs& a, hipStream_t st, int head_dim, int G, bool chunked) {
+  a.G = G;
+  const int hpw = G < kHeadsPerWg ? G : kHeadsPerWg;
   if (head_dim == 128)
-    return G == 1 ? launch<128, 1>(a, st, chunked) : G == 2 ? launch<128, 2>(a, st, chunked)
-         : G == 4 ? launch<128, 4>(a, st, chunked) : launch<128, 8>(a, st, chunked);
-  return G == 1 ? launch<64, 1>(a, st, chunked) : G == 2 ? launch<64, 2>(a, st, chunked)
-       : G == 4 ? launch<64, 4>(a, st, chunked) : launch<64, 8>(a, st, chunked);
+    return hpw == 1 ? launch<128, 1>(a, st, chunked) : hpw == 2 ? launch<128, 2>(a, st, chunked)
+         : hpw == 4 ? launch<128, 4>(a, st, chunked) : launch<128, 8>(a, st, chunked);
+  return hpw == 1 ? launch<64, 1>(a, st, chunked) : hpw == 2 ? launch<64, 2>(a, st, chunked)
+       : hpw == 4 ? launch<64, 4>(a, st, chunked) : launch<64, 8>(a, st, chunked);
 }
 
 }  // namespace
