@@ -19,7 +19,7 @@
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTile = 2048;
+constexpr int kTile = 512;   // virtual positions per scan tile
 constexpr int kBlk = 64;
 
 struct ChunkArgs {
@@ -115,6 +115,12 @@ __global__ __launch_bounds__(kThreads) void chunk_plan_kernel(ChunkArgs a) {
   }
   if (t == 0 && (int64_t)nf + carry > a.total_pages) s_fail = 1;
   __syncthreads();
+  // column counts the scatter does not write: rows whose band starts at
+  // position 0 and, on failure, every row (the chunk then sees no columns)
+  for (int e = t; e < a.H * a.rchunk; e += kThreads) {
+    const int i = e % a.rchunk;
+    if (s_fail || (a.r0 + i) * kBlk - a.W + 1 <= 0) a.column_count[e] = 0;
+  }
   if (s_fail) {
     if (t == 0) {
       *a.status = WGKV_ERR_CAPACITY;
@@ -138,8 +144,11 @@ __global__ __launch_bounds__(kThreads) void chunk_plan_kernel(ChunkArgs a) {
 }
 
 // Stable compaction of the admission range into the heads' global pages, and
-// column_count of the chunk's row blocks.
+// column_count of the chunk's row blocks: the count of row block r is the
+// number of admitted positions below p = 64 r - W + 1, i.e. the inclusive
+// count at virtual index p - 1 - base, which falls in exactly one tile.
 __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(ChunkArgs a) {
+  constexpr int kPer = kTile / kThreads;
   __shared__ int s_tmp[kThreads];
   __shared__ int s_src[kTile];     // virtual index
   __shared__ int64_t s_dst[kTile]; // pool row
@@ -149,24 +158,36 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(ChunkArgs a) {
   const int nr = vring(a);
   const int n_adm = vlen(a) - a.W;
   const int lb = a.W / a.page;
+  const int base = a.c0 > 0 ? a.c0 - a.W : 0;  // global position of virtual index 0
   const int32_t* bt = a.block_table + ((int64_t)a.layer * a.H + h) * a.max_pages + lb;
   const int gl0 = a.gl_before[h];
-  const int v0 = tile * kTile + t * (kTile / kThreads);
+  const int v0 = tile * kTile + t * kPer;
+  bool f[kPer];
   int cnt = 0;
-  for (int k = 0; k < kTile / kThreads; ++k) {
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
     const int v = v0 + k;
-    cnt += (v < n_adm && vflag(a, h, v)) ? 1 : 0;
+    f[k] = v < n_adm && vflag(a, h, v);
+    cnt += f[k] ? 1 : 0;
   }
   int total = 0;
   int o = block_exclusive_scan_256(cnt, s_tmp, &total);
-  const int base = gl0 + a.tile_base[h * a.ntiles + tile];
-  for (int k = 0; k < kTile / kThreads; ++k) {
+  const int before = gl0 + a.tile_base[h * a.ntiles + tile];
+  int32_t* cc = a.column_count + (int64_t)h * a.rchunk;
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) {
     const int v = v0 + k;
-    if (v < n_adm && vflag(a, h, v)) {
-      const int j = base + o;  // logical index in the head's global cache
+    if (f[k]) {
+      const int j = before + o;  // logical index in the head's global cache
       s_src[o] = v;
       s_dst[o] = (int64_t)bt[j / a.page] * a.page + j % a.page;
       ++o;
+    }
+    // o is now the inclusive count at v within the tile
+    const int p = base + v + 1;
+    if (v < n_adm && p > 0 && (p + a.W - 1) % kBlk == 0) {
+      const int r = (p + a.W - 1) / kBlk;
+      if (r >= a.r0 && r < a.r0 + a.rchunk) cc[r - a.r0] = before + o;
     }
   }
   __syncthreads();
@@ -189,53 +210,19 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(ChunkArgs a) {
   }
 }
 
-// column_count[h][r - r0] for the chunk's row blocks: one workgroup per head
-// walks the virtual sequence with a running count.
-__global__ __launch_bounds__(kThreads) void chunk_colcount_kernel(ChunkArgs a) {
-  __shared__ int s_tmp[kThreads];
-  const int h = blockIdx.x;
-  const int t = threadIdx.x;
-  if (*a.abort_flag) {
-    // nothing was admitted: the chunk's attention then sees no columns
-    for (int i = t; i < a.rchunk; i += kThreads) a.column_count[(int64_t)h * a.rchunk + i] = 0;
-    return;
-  }
-  const int base = a.c0 > 0 ? a.c0 - a.W : 0;  // global position of virtual index 0
-  const int gl0 = a.gl_before[h];
-  int32_t* cc = a.column_count + (int64_t)h * a.rchunk;
-  // rows whose band starts at position 0 see no admitted columns
-  for (int i = t; i < a.rchunk; i += kThreads)
-    if ((a.r0 + i) * kBlk - a.W + 1 <= 0) cc[i] = 0;
-  const int len = vlen(a);
-  int carry = 0;
-  for (int v0 = 0; v0 < len; v0 += kThreads) {
-    const int v = v0 + t;
-    const int f = v < len ? (int)vflag(a, h, v) : 0;
-    int total = 0;
-    const int excl = block_exclusive_scan_256(f, s_tmp, &total);
-    // prefix count below position p = base + v + 1 is carry + excl + f; it is
-    // the count of row block r when r*64 - W + 1 == p
-    if (v < len) {
-      const int p = base + v + 1;
-      if ((p + a.W - 1) % kBlk == 0) {
-        const int r = (p + a.W - 1) / kBlk;
-        if (r >= a.r0 && r < a.r0 + a.rchunk && p > 0) cc[r - a.r0] = gl0 + carry + excl + f;
-      }
-    }
-    carry += total;
-  }
-}
-
 // After the chunk's attention: ring slot i <- chunk position C - W + i.
+// Grid (head, 64-slot group).
 __global__ __launch_bounds__(kThreads) void chunk_ring_kernel(ChunkArgs a) {
   if (*a.abort_flag) return;
   const int h = blockIdx.x;
   const int n_loc = min(a.W, a.c0 + a.C);
   const int first = a.C - n_loc;  // chunk row of slot 0
+  const int i0 = blockIdx.y * kBlk, i1 = min(n_loc, i0 + kBlk);
+  if (i0 >= i1) return;
   const int64_t ring_base = ((int64_t)a.layer * a.H + h) * a.W;
   const int chunks = a.D / 8;
-  for (int e = threadIdx.x; e < n_loc * chunks; e += kThreads) {
-    const int i = e / chunks, c = e - i * chunks;
+  for (int e = threadIdx.x; e < (i1 - i0) * chunks; e += kThreads) {
+    const int i = i0 + e / chunks, c = e % chunks;
     const int64_t off = (int64_t)h * a.kv_sh + (int64_t)(first + i) * a.kv_ss + c * 8;
     *(u32x4_t*)(a.pool_k + (ring_base + i) * a.D + c * 8) = *(const u32x4_t*)(a.key + off);
     *(u32x4_t*)(a.pool_v + (ring_base + i) * a.D + c * 8) = *(const u32x4_t*)(a.value + off);
@@ -244,7 +231,7 @@ __global__ __launch_bounds__(kThreads) void chunk_ring_kernel(ChunkArgs a) {
       *(u32x4_t*)(a.local_pre_key + (ring_base + i) * a.D + c * 8) = *(const u32x4_t*)(a.pre_key + po);
     }
   }
-  for (int i = threadIdx.x; i < n_loc; i += kThreads)
+  for (int i = i0 + threadIdx.x; i < i1; i += kThreads)
     a.local_is_global[ring_base + i] = a.mask[(int64_t)h * a.m_sh + first + i] ? 1 : 0;
 }
 
@@ -327,9 +314,9 @@ extern "C" int wgkv_chunk_cache_update(
     hipLaunchKernelGGL(chunk_count_kernel, grid, dim3(kThreads), 0, st, a);
     hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(kThreads), 0, st, a);
     hipLaunchKernelGGL(chunk_scatter_kernel, grid, dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL(chunk_colcount_kernel, dim3(num_kv_heads), dim3(kThreads), 0, st, a);
   } else {
-    hipLaunchKernelGGL(chunk_ring_kernel, dim3(num_kv_heads), dim3(kThreads), 0, st, a);
+    const int groups = (min(local_window, chunk_start + chunk_len) + kBlk - 1) / kBlk;
+    hipLaunchKernelGGL(chunk_ring_kernel, dim3(num_kv_heads, groups), dim3(kThreads), 0, st, a);
   }
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
