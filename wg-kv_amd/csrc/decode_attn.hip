@@ -13,11 +13,11 @@
 //   * K is read in the MFMA B-operand layout (lane n%16 = token row, lane/16
 //     = 16-byte slice of the row) and multiplied with the query heads on
 //     v_mfma_f32_16x16x32_bf16 (query head i replicated in rows 4r+i);
-//   * softmax runs in the log2 domain with one running max per query head,
-//     uniform over the wave, and a per-lane running denominator;
+//   * softmax runs in the log2 domain with one lazily moved running max per
+//     query head, uniform over the wave, and a per-lane running denominator;
 //   * P goes through a 1 KB LDS slot per wave and V is read fully coalesced
-//     (consecutive 16-byte slices of consecutive rows) and accumulated on the
-//     VALU in fp32.
+//     (consecutive 16-byte slices of consecutive rows); P V runs on
+//     v_dot2_f32_bf16 over pairs of rows (P rounded to bf16, fp32 sums).
 // At the end of a chunk the 4 waves merge through LDS; a single-chunk head
 // writes its output directly, otherwise the chunk writes (m, l, acc) partials
 // that wgkv_decode_merge combines with the usual log-sum-exp rule.
@@ -28,11 +28,12 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxBH = 2048;
-constexpr int kWgPerCu = 3;          // resident workgroups per CU at 165 VGPRs
+constexpr int kWgPerCu = 3;          // resident workgroups per CU at 158 VGPRs
 constexpr int kRounds = 1;           // chunks per resident workgroup slot
 constexpr int kMaxSlots = 1024;      // cap on CUs * kWgPerCu (workspace sizing)
 constexpr int kMaxChunks = kRounds * kMaxSlots + kMaxBH;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.f;  // log2 units a running maximum may lag the scores
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -139,8 +140,14 @@ __device__ __forceinline__ void load_v(const DecodeArgs& a, u32x4_t (&vr)[D / 8]
   }
 }
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2_t;
+// c + a.lo * b.lo + a.hi * b.hi for packed bf16 pairs, fp32 accumulation
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
+}
+
 template <int D, int G>
-// 165 registers at D=128, G=4: three waves per SIMD (measured faster than two).
+// 158 registers at D=128, G=4: three waves per SIMD (measured faster than two).
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_split_kernel(
     DecodeArgs a) {
   constexpr int KS = D / 32;       // MFMA k-steps per row
@@ -170,7 +177,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   const int s1 = min(nsub, s0 + cp);
   const int tok_end = min(T, s1 * 16);
 
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  // wid is wave-uniform: the quad bookkeeping, page-table reads and row
+  // addresses then live in scalar registers
+  const int lane = threadIdx.x & 63, wid = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int32_t* bt_row = a.bt + (int64_t)b * a.bt_sb + (int64_t)h * a.bt_sh;
 
@@ -216,6 +225,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
         c[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[j], __builtin_bit_cast(bf16x8_t, kr[p][j]), c[p], 0, 0, 0);
     }
 
+    // Softmax in the log2 domain with a lazy running maximum: m_run of a
+    // head moves only when a score of the quad exceeds it by more than
+    // kRescaleSlack (then to the quad's maximum, rescaling l and acc), so
+    // p <= 2^kRescaleSlack and most quads need neither a maximum nor a
+    // rescale -- one compare and ballot per head.
     const bool ok = (sp0 + g) * 16 + n < tok_end;
     float s[G], pr[4];
 #pragma unroll
@@ -223,50 +237,59 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       const float x = g == 0 ? c[0][i] : g == 1 ? c[1][i] : g == 2 ? c[2][i] : c[3][i];
       s[i] = ok ? x * a.scale_log2 : -INFINITY;
     }
-    bool grew = false;
-    float alpha[G];
+    uint64_t up_any = 0;
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const float mn = fmaxf(m_run[i], wave_max(s[i]));
-      grew |= mn > m_run[i];
-      alpha[i] = fast_exp2(m_run[i] - mn);
-      m_run[i] = mn;
-    }
-    if (grew) {
+    for (int i = 0; i < G; ++i) up_any |= __builtin_amdgcn_ballot_w64(s[i] > m_run[i] + kRescaleSlack);
+    if (up_any) {
 #pragma unroll
       for (int i = 0; i < G; ++i) {
-        l_lane[i] *= alpha[i];
+        if (__builtin_amdgcn_ballot_w64(s[i] > m_run[i] + kRescaleSlack) == 0) continue;
+        const float mn = wave_max(s[i]);  // > m_run[i] + slack
+        const float alpha = fast_exp2(m_run[i] - mn);  // 0 when m_run was -inf
+        m_run[i] = mn;
+        l_lane[i] *= alpha;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[i][e] *= alpha[i];
+        for (int e = 0; e < 8; ++e) acc[i][e] *= alpha;
       }
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) pr[i] = 0.f;
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      pr[i] = fast_exp2(s[i] - m_run[i]);
+      // m_run is -inf only while every score seen is -inf: p = 0 then
+      pr[i] = fast_exp2(s[i] - (m_run[i] == -INFINITY ? 0.f : m_run[i]));
       l_lane[i] += pr[i];
     }
     s_p[wid][g * 16 + n] = (f32x4_t){pr[0], pr[1], pr[2], pr[3]};
     wave_lds_sync();
 
+    // P V on v_dot2_f32_bf16: the lane's rows are paired (load i, load i+1)
+    // so that one instruction adds p_r * v_r + p_r' * v_r' for one d; the
+    // probabilities are rounded to bf16 for the product, as the reference's
+    // kernel does (src/modeling_layers.py:930-931).
     const bool full = sp0 * 16 + 64 <= tok_end;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-      const int r = i * RPI + lane / CH;
-      const f32x4_t pp = s_p[wid][r];
-      u32x4_t v = vr[i];
-      if (!full && sp0 * 16 + r >= tok_end) v = (u32x4_t){0u, 0u, 0u, 0u};
-      float vf[8];
+    for (int i = 0; i < NV; i += 2) {
+      const int r0 = i * RPI + lane / CH, r1 = r0 + RPI;
+      const f32x4_t p0 = s_p[wid][r0];
+      const f32x4_t p1 = s_p[wid][r1];
+      u32x4_t v0 = vr[i], v1 = vr[i + 1];
+      if (!full && sp0 * 16 + r0 >= tok_end) v0 = (u32x4_t){0u, 0u, 0u, 0u};
+      if (!full && sp0 * 16 + r1 >= tok_end) v1 = (u32x4_t){0u, 0u, 0u, 0u};
+      uint32_t pp[G];
+#pragma unroll
+      for (int qi = 0; qi < G; ++qi) pp[qi] = pack_bf16x2(p0[qi], p1[qi]);
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        vf[2 * e] = bf16lo(v[e]);
-        vf[2 * e + 1] = bf16hi(v[e]);
+        // (v0.d, v1.d) for d = 2e (low halves) and d = 2e+1 (high halves)
+        const uint32_t lo = __builtin_amdgcn_perm(v1[e], v0[e], 0x05040100u);
+        const uint32_t hi = __builtin_amdgcn_perm(v1[e], v0[e], 0x07060302u);
+#pragma unroll
+        for (int qi = 0; qi < G; ++qi) {
+          acc[qi][2 * e] = dot2_bf16(lo, pp[qi], acc[qi][2 * e]);
+          acc[qi][2 * e + 1] = dot2_bf16(hi, pp[qi], acc[qi][2 * e + 1]);
+        }
       }
-#pragma unroll
-      for (int qi = 0; qi < G; ++qi)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[qi][e] = fmaf(pp[qi], vf[e], acc[qi][e]);
     }
     wave_lds_sync();
   }
@@ -328,8 +351,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 // comes from the split kernel, which ran before on the same stream.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
-  constexpr int NQ = G * D / 4;          // float4 quads of the output row
-  constexpr int GROUPS = kThreads / NQ;  // chunk groups summed in parallel
+  // one workgroup per (b, h, query head i): the float4 quads of head i's row
+  // are summed by GROUPS thread groups over disjoint chunk subsets
+  constexpr int NQ = D / 4;
+  constexpr int GROUPS = kThreads / NQ;
   __shared__ f32x4_t s_a[kThreads];
   __shared__ float s_m[kThreads], s_l[kThreads];
   const int bh = blockIdx.x;
@@ -340,8 +365,8 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   const float* part_l = a.part + kMaxChunks * 4;
   const float* part_acc = a.part + kMaxChunks * 8;
   const int t = threadIdx.x;
-  const int vq = t % NQ, grp = t / NQ;
-  const int i = (vq * 4) / D;
+  const int i = blockIdx.y;
+  const int vq = i * NQ + t % NQ, grp = t / NQ;
 
   // Chunks are read in batches of kBatch with every load issued before the
   // (branch-free) online update consumes them.
@@ -413,7 +438,7 @@ hipError_t launch(DecodeArgs a, hipStream_t st) {
   hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(a.target_chunks + BH), dim3(kThreads), 0, st, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH, G), dim3(kThreads), 0, st, a);
   return hipGetLastError();
 }
 
