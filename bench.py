@@ -38,7 +38,16 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-layer", action="store_true")
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="run only a 1 GiB torch copy x5 and the config-3 decode x5, for rocprofv3 --pmc "
+                        "FETCH_SIZE / WRITE_SIZE passes (the copy calibrates the counters)")
     return p.parse_args()
+
+
+# HBM bytes per config-3 decode call, from rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE passes over `bench.py --traffic-probe`, each scaled by what the
+# counter reads for a 1 GiB device copy (profiles/decode_attn_traffic_b8_128k.md)
+DECODE_TRAFFIC_BYTES = 1415738794
 
 
 def time_op(fn, steps, warmup):
@@ -304,6 +313,17 @@ def main():
         wgkv.paged_decode_attn(w.q, w.k_cache, w.v_cache, w.cache_seqlens, w.block_table,
                                w.softmax_scale, out=out)
 
+    if args.traffic_probe:
+        src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        for _ in range(5):
+            step()
+        torch.cuda.synchronize()
+        print(json.dumps({"traffic_probe": {"copy_bytes_read": src.numel() * 2, "copy_bytes_written": dst.numel() * 2,
+                                            "decode_algorithmic_bytes": w.algorithmic_bytes()}}), flush=True)
+        return
     ms = time_op(step, args.steps, args.warmup)
     nbytes = w.algorithmic_bytes()
     achieved = nbytes / (ms * 1e-3) / 1e9
@@ -332,7 +352,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": DECODE_TRAFFIC_BYTES,
             "bytes_per_launch": nbytes,
             "launch": "wgkv_paged_decode_attn = decode_split_kernel + decode_merge_kernel",
         },
