@@ -38,6 +38,14 @@ def parse():
     p.add_argument("--no-secondary", action="store_true")
     p.add_argument("--no-prefill", action="store_true")
     p.add_argument("--no-layer", action="store_true")
+    p.add_argument("--e2e", action="store_true",
+                   help="only the BASELINE config-5 end-to-end run: a 32-layer Llama-3.1-8B-shaped model, "
+                        "chunked prefill of --e2e-prompt tokens then --e2e-steps greedy decode steps, "
+                        "gated and all-admitted, on one GPU (several minutes)")
+    p.add_argument("--e2e-prompt", type=int, default=400000)
+    p.add_argument("--e2e-steps", type=int, default=256)
+    p.add_argument("--e2e-layers", type=int, default=32)
+    p.add_argument("--e2e-admit", type=float, default=0.30)
     p.add_argument("--traffic-probe", action="store_true",
                    help="run only a 1 GiB torch copy x5 and the config-3 decode x5, for rocprofv3 --pmc "
                         "FETCH_SIZE / WRITE_SIZE passes (the copy calibrates the counters)")
@@ -293,12 +301,74 @@ def layer_section(dev, cpu_budget):
     }
 
 
+def e2e_section(args):
+    """BASELINE config 5 (the reference's scripts/profiling.py run): a random-
+    initialised bf16 Llama-3.1-8B-shaped model, uniform random token ids, the
+    prompt prefilled in 4096-token chunks, then greedy decode steps; once with
+    the learned gate (bias calibrated to admit ``--e2e-admit`` of the first
+    chunk per head and layer) and once with every token admitted (the
+    reference's use_baseline run).  Prefill time (TTFT), mean decode step
+    (TPOT; each step one replay of a captured HIP graph of the whole model's
+    decode step), tokens/s, cached tokens per (layer, head) and KV memory."""
+    import torch
+    from wgkv import e2e
+
+    dev = torch.device("cuda:0")
+    ec = e2e.E2EConfig(num_hidden_layers=args.e2e_layers)
+    S, steps, W = args.e2e_prompt, args.e2e_steps, ec.local_window_size
+    torch.manual_seed(0)
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    with torch.device(dev):
+        model = e2e.LlamaLite(ec, gated=True, max_tokens_per_head=S + steps + 2 * W,
+                              max_total_tokens=ec.num_hidden_layers * ec.num_key_value_heads * (S + steps + 2 * W))
+    torch.set_default_dtype(prev)
+    model.init_weights(seed=0)
+    ids = torch.randint(0, ec.vocab_size, (1, S), generator=torch.Generator().manual_seed(0)).to(dev)
+
+    def log(msg):
+        print(f"[e2e] {msg}", file=sys.stderr, flush=True)
+
+    out = {"workload": f"e2e_llama8b_{S // 1000}k (BASELINE config 5): {ec.num_hidden_layers} layers, "
+                       f"hidden {ec.hidden_size}, FFN {ec.intermediate_size}, vocab {ec.vocab_size}, "
+                       f"prompt {S} in 4096-token chunks, {steps} greedy decode steps, W {W}",
+           "data": "synthetic: random-init bf16 weights, uniform random token ids"}
+    log("calibrating the gates")
+    e2e.calibrate_gates(model, ids, args.e2e_admit)
+    for name, gated in (("gated", True), ("full", False)):
+        model.cfg.use_baseline = not gated
+        # the gated pool holds the expected admitted share with margin; the full pool every token
+        per_head = S + steps + 2 * W if not gated else int(S * min(1.0, 1.5 * args.e2e_admit)) + steps + 2 * W
+        model.cfg.max_tokens_per_head = S + steps + 2 * W
+        model.cfg.max_total_tokens = ec.num_hidden_layers * ec.num_key_value_heads * per_head
+        log(f"{name}: prefill {S} tokens")
+        r = e2e.run(model, ids, steps, progress=log, graph=True)
+        torch.cuda.empty_cache()
+        dm = sorted(r.decode_ms)
+        tpot = sum(r.decode_ms) / len(r.decode_ms)
+        out[name] = {"prefill_ms": round(r.prefill_ms, 1), "prefill_tokens_per_s": round(S / (r.prefill_ms / 1e3), 1),
+                     "tpot_ms": round(tpot, 3), "tpot_median_ms": round(dm[len(dm) // 2], 3),
+                     "decode_tokens_per_s": round(1000.0 / tpot, 2),
+                     "avg_tokens_per_head_before_decode": round(r.tokens_before),
+                     "avg_tokens_per_head_after_decode": round(r.tokens_after),
+                     "model_gib": round(r.model_mib / 1024, 2), "kv_cache_gib": round(r.kv_mib / 1024, 2),
+                     "first_tokens": r.tokens[:8]}
+        log(f"{name}: {out[name]}")
+    out["gated_vs_full"] = {"prefill_speedup": round(out["full"]["prefill_ms"] / out["gated"]["prefill_ms"], 3),
+                            "decode_speedup": round(out["full"]["tpot_ms"] / out["gated"]["tpot_ms"], 3),
+                            "kv_ratio": round(out["gated"]["kv_cache_gib"] / out["full"]["kv_cache_gib"], 3)}
+    return out
+
+
 def main():
     args = parse()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.e2e:
+        print(json.dumps({"e2e": e2e_section(args)}), flush=True)
+        return
     import torch
     import wgkv
     from wgkv import workloads

@@ -154,6 +154,24 @@ int wgkv_decode_append(
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
     void* stream);
 
+/* wgkv_decode_append with the ring state (local_ptr, local_length) in device
+ * memory (int32[2]) instead of host arguments, for decode steps replayed from
+ * a captured HIP graph: promotion runs only if the device local_length equals
+ * W (the host condition of :1470), and with advance != 0 (the last layer's
+ * call) the kernel advances the ring state as decode_wrapper's host update
+ * does (:1409-1413).  Same arguments otherwise. */
+int wgkv_decode_append_ring(
+    const void* key, const void* value, int64_t kv_stride_h,
+    const void* pre_key, int64_t pk_stride_h,
+    const uint8_t* g_mask,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
+    int32_t* ring_state, int32_t advance, int32_t do_migrate, int32_t do_write,
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
+    int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
+    int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* stream);
+
 /* ------------------------------------------------------------------------
  * Write-gate scores and admission flags.
  *

@@ -197,6 +197,8 @@ struct AppendArgs {
   int layer, L, H, D, W, page, max_tokens_per_head;
   int64_t total_pages;
   int local_ptr, local_length, do_migrate, do_write;
+  int32_t* ring;  // device (local_ptr, local_length), replacing the two above when set
+  int advance;    // with ring: advance it after this layer's write (the last layer's call)
   uint16_t* pool_k;
   uint16_t* pool_v;
   int32_t* block_table;
@@ -219,16 +221,23 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
   const int t = threadIdx.x;
   const int LH = a.L * a.H;
   const int lb = a.W / a.page;
+  int local_ptr = a.local_ptr, local_length = a.local_length, do_migrate = a.do_migrate;
+  if (a.ring) {
+    // ring pointers on the device; promotion only once the ring is full (:1470)
+    local_ptr = a.ring[0];
+    local_length = a.ring[1];
+    do_migrate = do_migrate && local_length == a.W;
+  }
   if (t == 0) s_fail = 0;
   __syncthreads();
-  if (a.do_migrate) {
+  if (do_migrate) {
     // pass 1: checks
     int need_total = 0;
     for (int i0 = 0; i0 < LH; i0 += kThreads) {
       const int i = i0 + t;
       int need = 0;
       if (i < LH) {
-        const bool flag = a.local_is_global[(int64_t)i * a.W + a.local_ptr] != 0;
+        const bool flag = a.local_is_global[(int64_t)i * a.W + local_ptr] != 0;
         const int gl = a.global_lengths[i];
         if (flag && (a.W + gl + 1 > a.max_tokens_per_head || lb + gl / a.page >= a.max_pages)) atomicOr(&s_fail, 1);
         need = (flag && gl % a.page == 0) ? 1 : 0;
@@ -251,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
       bool flag = false;
       int gl = 0, need = 0;
       if (i < LH) {
-        flag = a.local_is_global[(int64_t)i * a.W + a.local_ptr] != 0;
+        flag = a.local_is_global[(int64_t)i * a.W + local_ptr] != 0;
         gl = a.global_lengths[i];
         need = (flag && gl % a.page == 0) ? 1 : 0;
       }
@@ -266,7 +275,7 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
         } else {
           pg = *bt;
         }
-        const int64_t src = (int64_t)i * a.W + a.local_ptr;
+        const int64_t src = (int64_t)i * a.W + local_ptr;
         const int64_t dst = (int64_t)pg * a.page + gl % a.page;
         for (int c = 0; c < a.D / 8; ++c) {
           *(u32x4_t*)(a.pool_k + dst * a.D + c * 8) = *(const u32x4_t*)(a.pool_k + src * a.D + c * 8);
@@ -281,8 +290,8 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
   }
   if (!a.do_write) return;
   // ring write of this layer's new token
-  const int slot = a.local_length < a.W ? a.local_length : a.local_ptr;
-  const int cur = a.local_length < a.W ? a.local_length + 1 : a.W;
+  const int slot = local_length < a.W ? local_length : local_ptr;
+  const int cur = local_length < a.W ? local_length + 1 : a.W;
   const int chunks = a.D / 8;
   for (int e = t; e < a.H * chunks; e += kThreads) {
     const int h = e / chunks, c = e - h * chunks;
@@ -296,6 +305,15 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
     const int64_t row = ((int64_t)a.layer * a.H + h) * a.W + slot;
     if (a.mask) a.local_is_global[row] = a.mask[h] ? 1 : 0;
     if (a.cache_seqlens) a.cache_seqlens[h] = cur + a.global_lengths[a.layer * a.H + h];
+  }
+  if (a.ring && a.advance) {
+    // every thread has read the pointers above; advance them for the next step
+    // (decode_wrapper's host update after the last layer, :1409-1413)
+    __syncthreads();
+    if (t == 0) {
+      if (local_length < a.W) a.ring[1] = local_length + 1;
+      else a.ring[0] = (local_ptr + 1) % a.W;
+    }
   }
 }
 
@@ -375,13 +393,15 @@ extern "C" int wgkv_prefill_admit(
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_decode_append(
+namespace {
+
+int decode_append_launch(
     const void* key, const void* value, int64_t kv_stride_h,
     const void* pre_key, int64_t pk_stride_h,
     const uint8_t* g_mask,
     int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
     int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
-    int32_t local_ptr, int32_t local_length, int32_t do_migrate, int32_t do_write,
+    int32_t local_ptr, int32_t local_length, int32_t* ring_state, int32_t advance, int32_t do_migrate, int32_t do_write,
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
@@ -392,7 +412,8 @@ extern "C" int wgkv_decode_append(
     return WGKV_ERR_ARG;
   if (num_kv_heads <= 0 || layer < 0 || layer >= num_layers) return WGKV_ERR_ARG;
   if (page_size <= 0 || local_window <= 0 || local_window % page_size) return WGKV_ERR_ARG;
-  if (local_ptr < 0 || local_ptr >= local_window || local_length < 0 || local_length > local_window) return WGKV_ERR_ARG;
+  if (!ring_state && (local_ptr < 0 || local_ptr >= local_window || local_length < 0 || local_length > local_window))
+    return WGKV_ERR_ARG;
   if (do_write && !g_mask && (!pre_key || !local_pre_key)) return WGKV_ERR_ARG;  // deferred gating stores pre_key
   if (head_dim % 8 || head_dim <= 0) return WGKV_ERR_UNSUPPORTED;
   if (!aligned16(pool_k) || !aligned16(pool_v)) return WGKV_ERR_UNSUPPORTED;
@@ -415,6 +436,8 @@ extern "C" int wgkv_decode_append(
   a.total_pages = total_pages;
   a.local_ptr = local_ptr;
   a.local_length = local_length;
+  a.ring = ring_state;
+  a.advance = advance;
   a.do_migrate = do_migrate;
   a.do_write = do_write;
   a.pool_k = (uint16_t*)pool_k;
@@ -429,4 +452,43 @@ extern "C" int wgkv_decode_append(
   a.status = status;
   hipLaunchKernelGGL(decode_append_kernel, dim3(1), dim3(kThreads), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int wgkv_decode_append(
+    const void* key, const void* value, int64_t kv_stride_h,
+    const void* pre_key, int64_t pk_stride_h,
+    const uint8_t* g_mask,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
+    int32_t local_ptr, int32_t local_length, int32_t do_migrate, int32_t do_write,
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
+    int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
+    int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* stream) {
+  return decode_append_launch(key, value, kv_stride_h, pre_key, pk_stride_h, g_mask, layer, num_layers, num_kv_heads,
+                              head_dim, local_window, page_size, max_tokens_per_head, total_pages, local_ptr,
+                              local_length, nullptr, 0, do_migrate, do_write, pool_k, pool_v, block_table,
+                              max_pages_per_head, global_lengths, local_is_global, local_pre_key, next_free_block,
+                              cache_seqlens, status, stream);
+}
+
+extern "C" int wgkv_decode_append_ring(
+    const void* key, const void* value, int64_t kv_stride_h,
+    const void* pre_key, int64_t pk_stride_h,
+    const uint8_t* g_mask,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t max_tokens_per_head, int64_t total_pages,
+    int32_t* ring_state, int32_t advance, int32_t do_migrate, int32_t do_write,
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
+    int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
+    int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* stream) {
+  if (!ring_state) return WGKV_ERR_ARG;
+  return decode_append_launch(key, value, kv_stride_h, pre_key, pk_stride_h, g_mask, layer, num_layers, num_kv_heads,
+                              head_dim, local_window, page_size, max_tokens_per_head, total_pages, 0, 0, ring_state,
+                              advance, do_migrate, do_write, pool_k, pool_v, block_table, max_pages_per_head,
+                              global_lengths, local_is_global, local_pre_key, next_free_block, cache_seqlens, status,
+                              stream);
 }

@@ -61,10 +61,31 @@ class DualCache:
         self.local_length = 0
         self.prefill_length = 0  # prompt tokens in the cache (all layers); chunks continue from here
         self.decode_started = False
+        # (local_ptr, local_length) on the device for graph-captured decode steps
+        self.ring_state = torch.zeros(2, **i32)
+        self.device_ring = False
         self.next_free_block_dev = torch.full((1,), n_local, **i32)
         self.status = torch.zeros(1, **i32)
         self.cache_seqlens = torch.zeros(L, 1, H, **i32)   # decode lengths, one row per layer
         self.gated_kv_initialized = True
+
+    def use_device_ring(self, on=True):
+        """Switch decode steps to the device copy of the ring pointers (for
+        HIP-graph capture of a whole decode step); the copy is loaded from the
+        host pointers here.  The host pointers keep being advanced by the
+        Python decode path; a caller replaying a captured step advances them
+        with ``advance_host_ring``."""
+        if on:
+            self.ring_state.copy_(torch.tensor([self.local_ptr, self.local_length], dtype=torch.int32))
+        self.device_ring = on
+
+    def advance_host_ring(self):
+        """The host-side pointer update decode_wrapper makes after the last
+        layer (src/modeling_layers.py:1409-1413)."""
+        if self.local_length < self.local_window_size:
+            self.local_length += 1
+        else:
+            self.local_ptr = (self.local_ptr + 1) % self.local_window_size
 
     @property
     def next_free_block(self):

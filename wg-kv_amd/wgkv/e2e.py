@@ -1,0 +1,287 @@
+"""A minimal Llama decoder stack around the write-gated path, for end-to-end
+runs (the reference's scripts/profiling.py:198-420).
+
+Embedding, RMSNorm, the gated attention layer (``wgkv.attention.LlamaAttention``
+with its swap points), SwiGLU MLP and LM head, random-initialised in bf16 on
+the device; the dense projections are torch GEMMs (hipBLASLt).  The prompt is
+prefilled in chunks through the cache's chunk continuation and then decoded
+greedily, as profiling.py does (argmax of the last logits, :146-147).  The
+"full" run admits every token (``use_baseline``, src/modeling_layers.py:1556),
+so the same kernels compute dense causal attention over the whole prefix.
+
+Reported as profiling.py reports (:395-410): prefill time and throughput,
+average tokens per (layer, head) in the cache before and after decoding
+(next_free_block * block_size / (L * Hkv), :150-153), decode time per token,
+model and KV-cache memory (:165-186).
+"""
+import math
+import time
+from dataclasses import dataclass, field
+from typing import List
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from .attention import LlamaAttention, LlamaRotaryEmbedding
+from .cache import DualCache
+from .layers import WGKVConfig
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, hidden, eps=1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden))
+        self.eps = eps
+
+    def forward(self, x):
+        dt = x.dtype
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return self.weight * xf.to(dt)
+
+
+class MLP(nn.Module):
+    def __init__(self, hidden, inter):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden, inter, bias=False)
+        self.up_proj = nn.Linear(hidden, inter, bias=False)
+        self.down_proj = nn.Linear(inter, hidden, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg, idx, inter, qk_norm=False):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.hidden_size)
+        self.self_attn = LlamaAttention(cfg, idx, qk_norm=qk_norm)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size)
+        self.mlp = MLP(cfg.hidden_size, inter)
+
+    def forward(self, x, pos_emb, cache):
+        h, _, _ = self.self_attn(3, self.input_layernorm(x), pos_emb, None, cache)
+        x = x + h
+        return x + self.mlp(self.post_attention_layernorm(x))
+
+
+@dataclass
+class E2EConfig:
+    """Llama-3.1-8B shapes (hidden 4096, FFN 14336, 32 layers, 32 q / 8 KV
+    heads, vocab 128256, rope_theta 500000) and the run's cache settings."""
+    hidden_size: int = 4096
+    intermediate_size: int = 14336
+    num_hidden_layers: int = 32
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 8
+    vocab_size: int = 128256
+    rope_theta: float = 500000.0
+    local_window_size: int = 1024
+    g_threshold: float = 0.1
+    qk_norm: bool = False
+
+
+class LlamaLite(nn.Module):
+    def __init__(self, ec: E2EConfig, gated: bool, max_tokens_per_head: int, max_total_tokens: int):
+        super().__init__()
+        self.ec = ec
+        self.cfg = WGKVConfig(hidden_size=ec.hidden_size, num_hidden_layers=ec.num_hidden_layers,
+                              num_attention_heads=ec.num_attention_heads, num_key_value_heads=ec.num_key_value_heads,
+                              rope_theta=ec.rope_theta, local_window_size=ec.local_window_size,
+                              g_threshold=ec.g_threshold, use_baseline=not gated,
+                              max_tokens_per_head=max_tokens_per_head, max_total_tokens=max_total_tokens,
+                              check_capacity=False)
+        self.embed_tokens = nn.Embedding(ec.vocab_size, ec.hidden_size)
+        self.layers = nn.ModuleList(DecoderLayer(self.cfg, i, ec.intermediate_size, ec.qk_norm)
+                                    for i in range(ec.num_hidden_layers))
+        self.norm = RMSNorm(ec.hidden_size)
+        self.lm_head = nn.Linear(ec.hidden_size, ec.vocab_size, bias=False)
+        self.rotary_emb = LlamaRotaryEmbedding(self.cfg.head_dim, ec.rope_theta)
+
+    @torch.no_grad()
+    def init_weights(self, seed=0, std=0.02):
+        """N(0, std) projections and embeddings, unit norms; the gates keep
+        the reference's default Conv1d init (src/modeling_layers.py:163-168)."""
+        g = torch.Generator(device=self.lm_head.weight.device).manual_seed(seed)
+        for name, p in self.named_parameters():
+            if "g_predictors" in name or name.endswith("norm.weight"):
+                continue
+            p.normal_(0.0, std, generator=g)
+
+    @torch.no_grad()
+    def forward_tokens(self, ids, start, cache):
+        """ids (1, n) at positions start..start+n-1 -> logits of the last token."""
+        pos = torch.arange(start, start + ids.shape[1], device=ids.device)[None]
+        return self.forward_at(ids, pos, cache)
+
+    @torch.no_grad()
+    def forward_at(self, ids, pos, cache):
+        """ids (1, n) at the positions of the device tensor pos (1, n)."""
+        x = self.embed_tokens(ids)
+        pe = self.rotary_emb(x, pos)
+        for layer in self.layers:
+            x = layer(x, pe, cache)
+        return self.lm_head(self.norm(x[:, -1:]))
+
+
+def greedy_token(logits):
+    """argmax over the vocabulary of logits (1, 1, V) -> (1, 1) int64, in two
+    single-workgroup reductions (rows of V/128, then the 128 row maxima) so
+    that no multi-workgroup reduction (which clears its semaphores with a
+    memset) is recorded into a captured graph.  Ties resolve to the lowest
+    index, as torch.argmax does."""
+    V = logits.shape[-1]
+    flat = logits.reshape(-1)
+    if V % 128:
+        return torch.argmax(flat).view(1, 1)
+    vals, idx = flat.view(128, V // 128).max(dim=1)
+    r = torch.argmax(vals)
+    return (r * (V // 128) + idx[r]).view(1, 1)
+
+
+class GraphDecoder:
+    """One greedy decode step of the whole model (every layer, the LM head
+    and the argmax) captured in a HIP graph and replayed.  The cache runs on
+    its device ring pointers; the token and the position live in device
+    tensors the step itself advances.  The ring must already be full (any
+    prompt of at least W tokens) and gating immediate (deferred gating
+    re-gates on a host condition)."""
+
+    def __init__(self, model, cache, token, pos, warmup=2):
+        dev = token.device
+        self.model, self.cache = model, cache
+        self.tok = token.clone().view(1, 1)
+        self.pos = torch.tensor([[pos]], dtype=torch.int64, device=dev)
+        if cache.local_length != cache.local_window_size:
+            raise AssertionError("graph decode needs a full ring")
+        cache.use_device_ring(True)
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            for _ in range(warmup):  # real decode steps: workspaces and library state before capture
+                self._step()
+        torch.cuda.current_stream(dev).wait_stream(side)
+        self.warm_tokens = warmup
+        host = (cache.local_ptr, cache.local_length)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self._step()
+        cache.local_ptr, cache.local_length = host  # capture ran the host side once, the device side not
+
+    def _step(self):
+        logits = self.model.forward_at(self.tok, self.pos, self.cache)
+        self.tok.copy_(greedy_token(logits))
+        self.pos += 1
+        return logits
+
+    def step(self):
+        """Replay one step; returns the (device) token it produced."""
+        self.graph.replay()
+        self.cache.advance_host_ring()
+        return self.tok
+
+
+def calibrate_gates(model, ids, frac, chunk=4096):
+    """Shift each layer's conv2.bias per head so that about ``frac`` of the
+    first ``chunk`` prompt tokens score above the threshold: logit(tau) minus
+    the (1-frac) quantile of that head's pre-sigmoid logits, taken layer by
+    layer on the activations the earlier (already shifted) layers produce."""
+    tau = model.cfg.g_threshold
+    shift_to = math.log(tau / (1.0 - tau))
+    originals = []
+    for layer in model.layers:
+        gp = layer.self_attn.g_predictors
+        orig = gp.scores_and_mask
+
+        def calibrated(pre_key, post_key, value, threshold, _gp=gp, _orig=orig, **kw):
+            s, _ = _orig(pre_key, post_key, value, 0.5)
+            sd = s[0].double().clamp(1e-12, 1 - 1e-12)
+            logit = torch.log(sd) - torch.log1p(-sd)
+            with torch.no_grad():
+                for h in range(logit.shape[0]):
+                    q = torch.quantile(logit[h].float(), 1.0 - frac).item()
+                    _gp.conv2.bias[h] += shift_to - q
+            return _orig(pre_key, post_key, value, threshold, **kw)
+
+        gp.scores_and_mask = calibrated
+        originals.append((gp, orig))
+    cache = DualCache()
+    model.forward_tokens(ids[:, :chunk], 0, cache)
+    for gp, orig in originals:
+        gp.scores_and_mask = orig
+    del cache
+
+
+@dataclass
+class E2EResult:
+    prompt_length: int
+    prefill_ms: float
+    decode_ms: List[float] = field(default_factory=list)
+    tokens_before: float = 0.0
+    tokens_after: float = 0.0
+    model_mib: float = 0.0
+    kv_mib: float = 0.0
+    tokens: List[int] = field(default_factory=list)
+
+
+def avg_tokens_in_cache(cache, model):
+    """profiling.py:150-153."""
+    return cache.next_free_block * model.cfg.block_size / (model.cfg.num_hidden_layers * model.cfg.num_key_value_heads)
+
+
+def kv_cache_mib(cache):
+    """profiling.py:180-186: the block table plus the used share of the pools."""
+    ratio = cache.next_free_block / cache.total_blocks
+    b = cache.block_table.numel() * 4 + (cache.block_pool_k.numel() + cache.block_pool_v.numel()) * 2 * ratio
+    return b / (1024 * 1024)
+
+
+@torch.no_grad()
+def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=False):
+    """Chunked prefill of ids (1, S), then ``steps`` greedy decode steps, each
+    timed with HIP events on the launch stream after a synchronisation (as
+    profiling.py's measure_time, :113-120); with ``graph`` every step is a
+    replay of a captured HIP graph (GraphDecoder)."""
+    S = ids.shape[1]
+    cache = DualCache()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record()
+    logits = None
+    for c0 in range(0, S, chunk):
+        logits = model.forward_tokens(ids[:, c0:c0 + chunk], c0, cache)
+        if progress is not None and (c0 // chunk) % 16 == 0:
+            progress(f"prefill chunk {c0 // chunk + 1}/{(S + chunk - 1) // chunk}")
+    ev1.record()
+    torch.cuda.synchronize()
+    res = E2EResult(prompt_length=S, prefill_ms=ev0.elapsed_time(ev1))
+    cache.raise_if_failed("prefill")
+    res.tokens_before = avg_tokens_in_cache(cache, model)
+    tok = greedy_token(logits)
+    pos = S
+    gd = None
+    if graph:
+        gd = GraphDecoder(model, cache, tok, pos)
+        warmup_steps = max(0, warmup_steps - gd.warm_tokens)
+    for i in range(warmup_steps + steps):
+        torch.cuda.synchronize()
+        ev0.record()
+        if gd is not None:
+            tok = gd.step()
+        else:
+            logits = model.forward_tokens(tok, pos, cache)
+            tok = greedy_token(logits)
+        ev1.record()
+        torch.cuda.synchronize()
+        if i >= warmup_steps:
+            res.decode_ms.append(ev0.elapsed_time(ev1))
+            res.tokens.append(int(tok.item()))
+        pos += 1
+    cache.raise_if_failed("decode")
+    res.tokens_after = avg_tokens_in_cache(cache, model)
+    res.model_mib = sum(p.numel() * p.element_size() for p in model.parameters()) / (1024 * 1024)
+    res.kv_mib = kv_cache_mib(cache)
+    del cache
+    return res

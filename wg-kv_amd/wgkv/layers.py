@@ -148,17 +148,17 @@ def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, valu
     c.decode_started = True
     insert_pos = c.local_length if c.local_length < W else c.local_ptr
     seqlens = c.cache_seqlens[self.layer_idx]
+    last = self.layer_idx == self.config.num_hidden_layers - 1
     ops.decode_append(c, self.layer_idx, key_states[0, :, 0], value_states[0, :, 0],
                       g_mask=None if g_mask is None else g_mask[0, :, 0],
                       pre_key=pre_key[0, :, 0] if g_mask is None else None,
-                      migrate=False, write=True, cache_seqlens=seqlens[0])
+                      migrate=False, write=True, cache_seqlens=seqlens[0], advance=last)
     if g_mask is None and insert_pos == W - 1:
+        if c.device_ring:
+            raise AssertionError("deferred gating re-gates on a host condition; it cannot run with device_ring")
         refresh_local_is_global(self, c, device)
-    if self.layer_idx == self.config.num_hidden_layers - 1:
-        if c.local_length < W:
-            c.local_length += 1
-        else:
-            c.local_ptr = (c.local_ptr + 1) % W
+    if last:
+        c.advance_host_ring()
     handle = self.decode_kernel_handle(
         query_states.transpose(1, 2), c.k_cache(), c.v_cache(), seqlens,
         c.block_table[self.layer_idx].unsqueeze(0), self.scaling)
@@ -177,7 +177,9 @@ def self_attn_forward_patch_inference(self, past_key_value, input_shape, query_s
     if self.config.local_window_size % self.config.block_size:
         raise AssertionError("local_window_size % block_size != 0")
     lbph = self.config.local_window_size // self.config.block_size
-    if (not is_prefilling) and self.layer_idx == 0 and past_key_value.local_length == self.config.local_window_size:
+    if (not is_prefilling) and self.layer_idx == 0 and (past_key_value.device_ring or
+                                                        past_key_value.local_length == self.config.local_window_size):
+        # with device_ring the ring-full condition is evaluated on the device
         migrate_local_kv_to_global(self, past_key_value, device, lbph)
     if is_prefilling:
         return self.prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,

@@ -193,28 +193,36 @@ def prefill_admit(cache, layer, key, value, g_mask, pre_key=None):
 
 
 def decode_append(cache, layer, key=None, value=None, g_mask=None, pre_key=None, migrate=False, write=True,
-                  cache_seqlens=None):
+                  cache_seqlens=None, advance=False):
     """Decode-step cache update of ``cache``: optional lazy promotion (all
-    layers) and the ring write of ``layer``'s token.  key/value/pre_key (H, D)."""
+    layers) and the ring write of ``layer``'s token.  key/value/pre_key (H, D).
+
+    With ``cache.device_ring`` the ring pointers are read from (and, with
+    ``advance``, advanced in) ``cache.ring_state`` on the device, so the step
+    can be captured in a HIP graph; promotion then runs only if the ring is
+    full, decided on the device."""
     H = cache.num_kv_heads
     D = cache.head_dim
     L = _lib.lib()
     m = None
     if write and g_mask is not None:
         m = _u8(g_mask).reshape(H).contiguous()
-    st = L.wgkv_decode_append(
-        _ptr(key) if write else None, _ptr(value) if write else None, key.stride(0) if write else 0,
-        _ptr(pre_key) if (write and pre_key is not None) else None,
-        pre_key.stride(0) if (write and pre_key is not None) else 0,
-        _ptr(m),
-        layer, cache.num_layers, H, D,
-        cache.local_window_size, cache.block_size, cache.max_tokens_per_head, cache.total_blocks,
-        cache.local_ptr, cache.local_length, int(migrate), int(write),
-        _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
-        _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(cache.local_pre_key),
-        _ptr(cache.next_free_block_dev), _ptr(cache_seqlens), _ptr(cache.status),
-        _lib.stream_handle(cache.block_pool_k.device))
-    _lib.check(st, "wgkv_decode_append")
+    head = (_ptr(key) if write else None, _ptr(value) if write else None, key.stride(0) if write else 0,
+            _ptr(pre_key) if (write and pre_key is not None) else None,
+            pre_key.stride(0) if (write and pre_key is not None) else 0,
+            _ptr(m),
+            layer, cache.num_layers, H, D,
+            cache.local_window_size, cache.block_size, cache.max_tokens_per_head, cache.total_blocks)
+    tail = (_ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
+            _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(cache.local_pre_key),
+            _ptr(cache.next_free_block_dev), _ptr(cache_seqlens), _ptr(cache.status),
+            _lib.stream_handle(cache.block_pool_k.device))
+    if getattr(cache, "device_ring", False):
+        st = L.wgkv_decode_append_ring(*head, _ptr(cache.ring_state), int(advance), int(migrate), int(write), *tail)
+        _lib.check(st, "wgkv_decode_append_ring")
+    else:
+        st = L.wgkv_decode_append(*head, cache.local_ptr, cache.local_length, int(migrate), int(write), *tail)
+        _lib.check(st, "wgkv_decode_append")
 
 
 # ---------------------------------------------------------------------------
