@@ -14,7 +14,7 @@ DEV = torch.device("cuda:0")
 def tiny_model(gated=True, S=1000, steps=8, W=128):
     from wgkv import e2e
     ec = e2e.E2EConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
-                       num_key_value_heads=2, vocab_size=1000, rope_theta=10000.0, local_window_size=W)
+                       num_key_value_heads=2, vocab_size=1024, rope_theta=10000.0, local_window_size=W)
     torch.manual_seed(0)
     prev = torch.get_default_dtype()
     torch.set_default_dtype(torch.bfloat16)

@@ -63,7 +63,8 @@ def test_gate_matches_reference_golden(name, fast):
     compare(scores, mask, ref, thr, f"{name} fast={fast}")
 
 
-@pytest.mark.parametrize("D,g_expand,S,H", [(128, 4.0, 4096, 8), (64, 4.0, 2048, 2), (128, 1.5, 1000, 8), (64, 4.0, 37, 2)])
+@pytest.mark.parametrize("D,g_expand,S,H", [(128, 4.0, 4096, 8), (64, 4.0, 2048, 2), (128, 1.5, 1000, 8), (64, 4.0, 37, 2),
+                                            (128, 4.0, 1, 8), (128, 1.5, 3, 8), (64, 4.0, 4, 2), (128, 4.0, 5, 8)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gate_matches_oracle(D, g_expand, S, H, dtype):
     gen = torch.Generator().manual_seed(S + D)
@@ -94,3 +95,20 @@ def test_gate_forward_returns_scores_and_bf16_params():
     ref16 = ogate.gate_scores(pre_k, post_k, value, p16)
     b = g16(pre_k.cuda(), post_k.cuda(), value.cuda())
     assert (b.cpu() - ref16).abs().max().item() <= 2e-6
+
+
+def test_cached_fp32_weights_follow_in_place_updates():
+    """bf16 gate parameters are widened once and cached; an in-place update
+    (the benchmark's bias calibration) must reach the kernel."""
+    sc = scenarios.GATE_SCENARIOS["llama_cfg1"]
+    params, pre_k, post_k, value = scenarios.gate_inputs(sc)
+    g16 = product_gate(params, sc["H"], sc["D"], sc["g_expand"]).to(torch.bfloat16)
+    first = g16(pre_k.cuda(), post_k.cuda(), value.cuda()).cpu()
+    with torch.no_grad():
+        g16.conv2.bias += 0.5
+    p16 = {k: v.to(torch.bfloat16).float() for k, v in params.items()}
+    p16["conv2.bias"] = g16.conv2.bias.detach().float().cpu()
+    ref = ogate.gate_scores(pre_k, post_k, value, p16)
+    second = g16(pre_k.cuda(), post_k.cuda(), value.cuda()).cpu()
+    assert not torch.equal(first, second)
+    assert (second - ref).abs().max().item() <= 2e-6

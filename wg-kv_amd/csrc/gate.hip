@@ -164,6 +164,131 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
   }
 }
 
+// Few tokens (decode steps): one workgroup per (batch, KV head) and group of
+// up to kSmallTok tokens.  The MFMA tile above would compute 64 token rows to
+// use one and stream W1[h] through a single dependent chain; here the lanes
+// of a wave split the K dimension, so each W1 row is read with one coalesced
+// load per wave, and each wave takes 16 hidden columns at a time (the 4
+// waves interleave in 16-column tiles).  Per column the lane partials are
+// summed over the wave; lane i < 16 then applies bias, activation and w2 for
+// column i.  Column order is fixed, so results are deterministic.
+constexpr int kSmallTok = 4;
+
+template <int K>
+__global__ __launch_bounds__(kThreads) void gate_small_kernel(GateArgs a) {
+  constexpr int KC = K / 4;                 // float4 chunks of an input row
+  constexpr int CPL = (KC + 63) / 64;       // chunks per lane
+  __shared__ __attribute__((aligned(16))) float xs[kSmallTok][K];
+  __shared__ float s_part[4][kSmallTok];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int bh = blockIdx.y;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int s0 = blockIdx.x * kSmallTok;
+  const int nt = min(kSmallTok, a.S - s0);
+  const int D = a.D;
+
+  // normalised inputs -> LDS: wave w handles token w
+  if (wid < nt) {
+    const int s = s0 + wid;
+    for (int i = 0; i < a.n_in; ++i) {
+      float v[2];
+      float sq = 0.f;
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int d = lane + e * 64;
+        v[e] = d < D ? load_in(a, i, b, h, s, d) : 0.f;
+        sq += v[e] * v[e];
+      }
+      float scale = 1.f;
+      if (a.rms) {
+        const float var = wave_sum(sq) / (float)D;
+        scale = 1.0f / sqrtf(var + 1e-6f);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const int d = lane + e * 64;
+        if (d < D) {
+          float y = a.rms ? v[e] * scale : v[e];
+          if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
+          xs[wid][i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // this lane's slices of the inputs
+  f32x4_t xr[kSmallTok][CPL];
+#pragma unroll
+  for (int t = 0; t < kSmallTok; ++t)
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int kc = lane + c * 64;
+      xr[t][c] = (t < nt && kc < KC) ? *(const f32x4_t*)(&xs[t][kc * 4]) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    }
+  const float* w1h = a.w1 + (int64_t)h * a.inner * K;
+  const float* b1h = a.b1 + (int64_t)h * a.inner;
+  const float* w2h = a.w2 + (int64_t)h * a.inner;
+  float logit[kSmallTok];
+#pragma unroll
+  for (int t = 0; t < kSmallTok; ++t) logit[t] = 0.f;
+  for (int c0 = wid * 16; c0 < a.inner; c0 += 64) {
+    float dot[kSmallTok][16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      f32x4_t w[CPL];
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int kc = lane + c * 64;
+        w[c] = kc < KC ? *(const f32x4_t*)(w1h + (int64_t)(c0 + j) * K + kc * 4) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int t = 0; t < kSmallTok; ++t) {
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = fmaf(w[c][e], xr[t][c][e], acc);
+        dot[t][j] = acc;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kSmallTok; ++t) {
+      if (t >= nt) break;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const float z = wave_sum(dot[t][j]) + b1h[c0 + j];
+        if (lane == j) logit[t] = fmaf(w2h[c0 + j], a.act ? silu(z) : gelu_erf(z), logit[t]);
+      }
+    }
+  }
+  // lanes 0..15 of each wave hold partial logits; sum them, then the waves
+#pragma unroll
+  for (int t = 0; t < kSmallTok; ++t) {
+    const float v = row_sum16(lane < 16 ? logit[t] : 0.f);
+    if (lane == 0) s_part[wid][t] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x < nt) {
+    const int t = threadIdx.x;
+    const int s = s0 + t;
+    const float z = ((s_part[0][t] + s_part[1][t]) + (s_part[2][t] + s_part[3][t])) + a.b2[h];
+    float g = 1.0f / (1.0f + expf(-z));
+    if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+    if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
+    if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
+  }
+}
+
+template <int K>
+void launch_gate(const GateArgs& a, hipStream_t st) {
+  if (a.S <= kSmallTok) {
+    hipLaunchKernelGGL(gate_small_kernel<K>, dim3(1, a.B * a.H), dim3(kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(gate_kernel<K>, dim3((a.S + kTok - 1) / kTok, a.B * a.H), dim3(kThreads), 0, st, a);
+  }
+}
+
 }  // namespace
 
 extern "C" int wgkv_gate_scores(
@@ -222,14 +347,13 @@ extern "C" int wgkv_gate_scores(
   a.mk_sh = mk_sh;
   if (((uintptr_t)w1 & 15) != 0) return WGKV_ERR_UNSUPPORTED;
   const int K = n_in * head_dim;
-  dim3 grid((seq_len + kTok - 1) / kTok, batch * num_kv_heads);
   hipStream_t st = (hipStream_t)stream;
   switch (K) {
-    case 64: hipLaunchKernelGGL(gate_kernel<64>, grid, dim3(kThreads), 0, st, a); break;
-    case 128: hipLaunchKernelGGL(gate_kernel<128>, grid, dim3(kThreads), 0, st, a); break;
-    case 192: hipLaunchKernelGGL(gate_kernel<192>, grid, dim3(kThreads), 0, st, a); break;
-    case 256: hipLaunchKernelGGL(gate_kernel<256>, grid, dim3(kThreads), 0, st, a); break;
-    case 384: hipLaunchKernelGGL(gate_kernel<384>, grid, dim3(kThreads), 0, st, a); break;
+    case 64: launch_gate<64>(a, st); break;
+    case 128: launch_gate<128>(a, st); break;
+    case 192: launch_gate<192>(a, st); break;
+    case 256: launch_gate<256>(a, st); break;
+    case 384: launch_gate<384>(a, st); break;
     default: return WGKV_ERR_UNSUPPORTED;
   }
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;

@@ -136,8 +136,8 @@ def greedy_token(logits):
     if V % 128:
         return torch.argmax(flat).view(1, 1)
     vals, idx = flat.view(128, V // 128).max(dim=1)
-    r = torch.argmax(vals)
-    return (r * (V // 128) + idx[r]).view(1, 1)
+    r = torch.argmax(vals).view(1)
+    return (r * (V // 128) + torch.gather(idx, 0, r)).view(1, 1)  # no host read of r
 
 
 class GraphDecoder:

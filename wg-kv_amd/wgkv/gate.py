@@ -52,12 +52,23 @@ class GatingPredictor(nn.Module):
         self.conv1.reset_parameters()
         self.conv2.reset_parameters()
 
-    @staticmethod
-    def _f32(p):
+    def _f32(self, p):
+        """fp32 contiguous copy of a parameter for the kernel.  Copies of
+        non-fp32 parameters are cached per parameter storage and refreshed
+        when the parameter's version changes (in-place updates, loading), so
+        a decode step does not re-convert the weights."""
         if p is None:
             return None
-        p = p.detach()
-        return p if (p.dtype == torch.float32 and p.is_contiguous()) else p.float().contiguous()
+        if p.dtype == torch.float32 and p.is_contiguous():
+            return p.detach()
+        cache = self.__dict__.setdefault("_f32_cache", {})
+        key = (p.data_ptr(), tuple(p.shape))
+        hit = cache.get(key)
+        if hit is not None and hit[0] == p._version:
+            return hit[1]
+        c = p.detach().float().contiguous()
+        cache[key] = (p._version, c)
+        return c
 
     def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True):
         """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S))."""
