@@ -168,18 +168,19 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
 // up to kSmallTok tokens.  The MFMA tile above would compute 64 token rows to
 // use one and stream W1[h] through a single dependent chain; here the lanes
 // of a wave split the K dimension, so each W1 row is read with one coalesced
-// load per wave, and each wave takes 16 hidden columns at a time (the 4
-// waves interleave in 16-column tiles).  Per column the lane partials are
+// load per wave, and each of the 16 waves takes 16 hidden columns at a time
+// (interleaved in 16-column tiles).  Per column the lane partials are
 // summed over the wave; lane i < 16 then applies bias, activation and w2 for
 // column i.  Column order is fixed, so results are deterministic.
 constexpr int kSmallTok = 4;
+constexpr int kSmallWaves = 16;  // 16 waves: W1 rows of 16 x 16 columns in flight at once
 
 template <int K>
-__global__ __launch_bounds__(kThreads) void gate_small_kernel(GateArgs a) {
+__global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a) {
   constexpr int KC = K / 4;                 // float4 chunks of an input row
   constexpr int CPL = (KC + 63) / 64;       // chunks per lane
   __shared__ __attribute__((aligned(16))) float xs[kSmallTok][K];
-  __shared__ float s_part[4][kSmallTok];
+  __shared__ float s_part[kSmallWaves][kSmallTok];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int bh = blockIdx.y;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -232,7 +233,7 @@ __global__ __launch_bounds__(kThreads) void gate_small_kernel(GateArgs a) {
   float logit[kSmallTok];
 #pragma unroll
   for (int t = 0; t < kSmallTok; ++t) logit[t] = 0.f;
-  for (int c0 = wid * 16; c0 < a.inner; c0 += 64) {
+  for (int c0 = wid * 16; c0 < a.inner; c0 += 16 * kSmallWaves) {
     float dot[kSmallTok][16];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
@@ -272,7 +273,10 @@ __global__ __launch_bounds__(kThreads) void gate_small_kernel(GateArgs a) {
   if (threadIdx.x < nt) {
     const int t = threadIdx.x;
     const int s = s0 + t;
-    const float z = ((s_part[0][t] + s_part[1][t]) + (s_part[2][t] + s_part[3][t])) + a.b2[h];
+    float z = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSmallWaves; ++w) z += s_part[w][t];
+    z += a.b2[h];
     float g = 1.0f / (1.0f + expf(-z));
     if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
     if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
@@ -283,7 +287,7 @@ __global__ __launch_bounds__(kThreads) void gate_small_kernel(GateArgs a) {
 template <int K>
 void launch_gate(const GateArgs& a, hipStream_t st) {
   if (a.S <= kSmallTok) {
-    hipLaunchKernelGGL(gate_small_kernel<K>, dim3(1, a.B * a.H), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(gate_small_kernel<K>, dim3(1, a.B * a.H), dim3(64 * kSmallWaves), 0, st, a);
   } else {
     hipLaunchKernelGGL(gate_kernel<K>, dim3((a.S + kTok - 1) / kTok, a.B * a.H), dim3(kThreads), 0, st, a);
   }
