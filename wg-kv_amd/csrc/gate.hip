@@ -115,10 +115,16 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
       const int tj = t0 + 4 * j;
       cols[j] = (tj < ntot ? tj : t0) * 16 + n;  // out-of-range tiles recompute tile t0 and are skipped below
     }
-    for (int k0 = 0; k0 < K; k0 += 16) {
-      f32x4_t bw[4], ax[4];
+    // W1 slices of the next k-step are loaded while this step's MFMAs run
+    f32x4_t bw[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bw[j] = *(const f32x4_t*)(w1h + (int64_t)cols[j] * K + k0 + 4 * kq);
+    for (int j = 0; j < 4; ++j) bw[j] = *(const f32x4_t*)(w1h + (int64_t)cols[j] * K + 4 * kq);
+#pragma unroll 1
+    for (int k0 = 0; k0 < K; k0 += 16) {
+      f32x4_t bwn[4], ax[4];
+      if (k0 + 16 < K)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bwn[j] = *(const f32x4_t*)(w1h + (int64_t)cols[j] * K + k0 + 16 + 4 * kq);
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt) ax[mt] = *(const f32x4_t*)(&xs[(mt * 16 + n) * LDX + k0 + 4 * kq]);
 #pragma unroll
@@ -128,6 +134,9 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
 #pragma unroll
           for (int j = 0; j < 4; ++j)
             c[mt][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(ax[mt][e], bw[j][e], c[mt][j], 0, 0, 0);
+      if (k0 + 16 < K)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bw[j] = bwn[j];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
