@@ -46,6 +46,7 @@ def parse():
     p.add_argument("--e2e-steps", type=int, default=256)
     p.add_argument("--e2e-layers", type=int, default=32)
     p.add_argument("--e2e-admit", type=float, default=0.30)
+    p.add_argument("--e2e-model", choices=["llama3-8b", "qwen3-8b"], default="llama3-8b")
     p.add_argument("--traffic-probe", action="store_true",
                    help="run only a 1 GiB torch copy x5 and the config-3 decode x5, for rocprofv3 --pmc "
                         "FETCH_SIZE / WRITE_SIZE passes (the copy calibrates the counters)")
@@ -314,7 +315,10 @@ def e2e_section(args):
     from wgkv import e2e
 
     dev = torch.device("cuda:0")
-    ec = e2e.E2EConfig(num_hidden_layers=args.e2e_layers)
+    if args.e2e_model == "qwen3-8b":
+        ec = e2e.E2EConfig.qwen3_8b(**({} if args.e2e_layers == 32 else {"num_hidden_layers": args.e2e_layers}))
+    else:
+        ec = e2e.E2EConfig(num_hidden_layers=args.e2e_layers)
     S, steps, W = args.e2e_prompt, args.e2e_steps, ec.local_window_size
     torch.manual_seed(0)
     prev = torch.get_default_dtype()
@@ -329,7 +333,8 @@ def e2e_section(args):
     def log(msg):
         print(f"[e2e] {msg}", file=sys.stderr, flush=True)
 
-    out = {"workload": f"e2e_llama8b_{S // 1000}k (BASELINE config 5): {ec.num_hidden_layers} layers, "
+    tag = "qwen3_8b" if args.e2e_model == "qwen3-8b" else "llama8b"
+    out = {"workload": f"e2e_{tag}_{S // 1000}k (BASELINE config 5): {ec.num_hidden_layers} layers, "
                        f"hidden {ec.hidden_size}, FFN {ec.intermediate_size}, vocab {ec.vocab_size}, "
                        f"prompt {S} in 4096-token chunks, {steps} greedy decode steps, W {W}",
            "data": "synthetic: random-init bf16 weights, uniform random token ids"}

@@ -186,7 +186,7 @@ int wgkv_decode_append_ring(
  * dtype, times its norm weight.  act 0 = exact-erf GELU, 1 = SiLU.
  * clamp_min > 0 applies the conv path's clamp (:205).  Outputs (may be NULL,
  * not both): scores f32 (B,H,S), mask u8 (B,H,S) = scores > threshold.
- * Supported: D in {64,128}, inner a multiple of 64, n_in*D <= 384.
+ * Supported: D in {64,128}, inner a multiple of 16, n_in*D <= 384.
  * ---------------------------------------------------------------------- */
 int wgkv_gate_scores(
     const void* pre_key, int64_t pk_sb, int64_t pk_sh, int64_t pk_ss,

@@ -4,7 +4,9 @@ TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``.
 
 Restates, in float32 on the CPU:
 * LlamaAttention.forward for gating_mode 3 -- src/modeling_llama.py:252-287
-  (projections, pre-RoPE key, RoPE :81-146, o_proj);
+  (projections, pre-RoPE key, RoPE :81-146, o_proj), and Qwen3's variant
+  with per-head q/k norms before the pre-RoPE key (src/modeling_qwen3.py:
+  235-239; ``qk_norm=True``);
 * self_attn_forward_patch / _inference -- src/modeling_layers.py:1534-1629,
   :1452-1509 (gate, threshold, migration trigger, prefill/decode dispatch);
 * the cache through ``oracle.dualcache``, the gate through ``oracle.gate``,
@@ -32,6 +34,16 @@ def rope_cos_sin(positions, head_dim, theta=10000.0):
     return emb.cos(), emb.sin()
 
 
+def head_rms_norm(x, weight, eps=1e-6):
+    """Qwen3RMSNorm over the last dimension (src/modeling_qwen3.py:62-76):
+    fp32 normalisation, cast back to the input dtype, then the weight; applied
+    per head to q and k (:235-236)."""
+    dt = x.dtype
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * xf.to(dt)
+
+
 def rotate_half(x):
     h = x.shape[-1] // 2
     return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
@@ -39,7 +51,7 @@ def rotate_half(x):
 
 class OracleLayer:
     def __init__(self, weights, hidden, Hq, Hkv, D, W, max_tokens_per_head, threshold=0.1, g_defer=False,
-                 theta=10000.0, page=16, kv_dtype=torch.float32):
+                 theta=10000.0, page=16, kv_dtype=torch.float32, qk_norm=False):
         self.w = {k: v.float() for k, v in weights.items()}
         self.gp = {k[len("g_predictors."):]: v for k, v in self.w.items() if k.startswith("g_predictors.")}
         self.hidden, self.Hq, self.Hkv, self.D, self.W = hidden, Hq, Hkv, D, W
@@ -48,13 +60,18 @@ class OracleLayer:
         self.g_defer = g_defer
         self.theta = theta
         self.kv_dtype = kv_dtype
+        self.qk_norm = qk_norm
         self.cache = DualCacheOracle(1, Hkv, D, W, Hkv * max_tokens_per_head, max_tokens_per_head,
                                      block_size=page, g_defer=g_defer, dtype=kv_dtype)
 
     def _project(self, x, positions):
         S = x.shape[1]
-        q = (x @ self.w["q_proj.weight"].T).view(1, S, self.Hq, self.D).transpose(1, 2)
-        k = (x @ self.w["k_proj.weight"].T).view(1, S, self.Hkv, self.D).transpose(1, 2)
+        q = (x @ self.w["q_proj.weight"].T).view(1, S, self.Hq, self.D)
+        k = (x @ self.w["k_proj.weight"].T).view(1, S, self.Hkv, self.D)
+        if self.qk_norm:  # Qwen3: per-head norms before the pre-RoPE key is taken
+            q = head_rms_norm(q, self.w["q_norm.weight"])
+            k = head_rms_norm(k, self.w["k_norm.weight"])
+        q, k = q.transpose(1, 2), k.transpose(1, 2)
         v = (x @ self.w["v_proj.weight"].T).view(1, S, self.Hkv, self.D).transpose(1, 2)
         pre_k = k
         cos, sin = rope_cos_sin(positions, self.D, self.theta)

@@ -64,7 +64,8 @@ def test_gate_matches_reference_golden(name, fast):
 
 
 @pytest.mark.parametrize("D,g_expand,S,H", [(128, 4.0, 4096, 8), (64, 4.0, 2048, 2), (128, 1.5, 1000, 8), (64, 4.0, 37, 2),
-                                            (128, 4.0, 1, 8), (128, 1.5, 3, 8), (64, 4.0, 4, 2), (128, 4.0, 5, 8)])
+                                            (128, 4.0, 1, 8), (128, 1.5, 3, 8), (64, 4.0, 4, 2), (128, 4.0, 5, 8),
+                                            (64, 1.5, 300, 2), (64, 1.5, 1, 2)])  # inner 96: Qwen3 width at D 64
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_gate_matches_oracle(D, g_expand, S, H, dtype):
     gen = torch.Generator().manual_seed(S + D)

@@ -17,22 +17,22 @@ from oracle.llama_layer import OracleLayer
 pytestmark = pytest.mark.gpu
 
 
-def build(g_defer):
+def build(g_defer, qk_norm=False, g_expand=4.0):
     from wgkv import workloads
-    cfg, w, x, xs = workloads.config1_layer(g_defer=g_defer)
+    cfg, w, x, xs = workloads.config1_layer(g_defer=g_defer, qk_norm=qk_norm, g_expand=g_expand)
     # place the threshold so ~20 % of the prompt is admitted (config-1 recipe)
-    probe = OracleLayer(w, 512, 8, 2, 64, 128, cfg["max_tokens_per_head"])
+    probe = OracleLayer(w, 512, 8, 2, 64, 128, cfg["max_tokens_per_head"], qk_norm=qk_norm)
     q, pre_k, k, v = probe._project(x, torch.arange(x.shape[1]))
     logits = ogate.gate_logits(pre_k, k, v, probe.gp)[0]
     w = workloads.shift_gate_bias(w, logits, cfg["_frac"], cfg["_logit_threshold"])
     return cfg, w, x, xs
 
 
-def product_layer(cfg, w):
+def product_layer(cfg, w, qk_norm=False):
     from wgkv.attention import LlamaAttention, LlamaRotaryEmbedding
     from wgkv.layers import WGKVConfig
     c = WGKVConfig(**{k: v for k, v in cfg.items() if not k.startswith("_")})
-    layer = LlamaAttention(c, 0)
+    layer = LlamaAttention(c, 0, qk_norm=qk_norm)
     layer.load_state_dict({k: v.clone() for k, v in w.items()}, strict=True)
     return layer.cuda(), LlamaRotaryEmbedding(64, 10000.0).cuda()
 
@@ -52,17 +52,22 @@ def assert_same_state(a, b, label):
         assert np.array_equal(np.asarray(x), np.asarray(y)), f"{label}: {name} differs"
 
 
-@pytest.mark.parametrize("g_defer", [False, True])
-def test_config1_layer_end_to_end(g_defer):
+@pytest.mark.parametrize("g_defer,qwen3", [(False, False), (True, False), (False, True), (True, True)])
+def test_config1_layer_end_to_end(g_defer, qwen3):
+    """qwen3: Qwen3's layer variant (per-head q/k norms before the pre-RoPE
+    key, src/modeling_qwen3.py:235-239) with its gate width g_expand = 1.5
+    (src/configuration_qwen3.py:183), at the config-1 shapes."""
     from wgkv.cache import DualCache
-    print(f"[layer e2e] config 1 g_defer={g_defer}", flush=True)
-    cfg, w, x, xs = build(g_defer)
+    print(f"[layer e2e] config 1 g_defer={g_defer} qwen3={qwen3}", flush=True)
+    g_expand = 1.5 if qwen3 else 4.0
+    cfg, w, x, xs = build(g_defer, qk_norm=qwen3, g_expand=g_expand)
     S = x.shape[1]
-    orc = OracleLayer(w, 512, 8, 2, 64, 128, cfg["max_tokens_per_head"], g_defer=g_defer, kv_dtype=torch.bfloat16)
+    orc = OracleLayer(w, 512, 8, 2, 64, 128, cfg["max_tokens_per_head"], g_defer=g_defer, kv_dtype=torch.bfloat16,
+                      qk_norm=qwen3)
     o_out, o_mask, o_g = orc.prefill(x, torch.arange(S))
     near = int((o_g - 0.1).abs().lt(1e-6).sum())
     admitted = o_mask.float().mean().item()
-    layer, rope = product_layer(cfg, w)
+    layer, rope = product_layer(cfg, w, qk_norm=qwen3)
     cache = DualCache()
     xg = x.cuda()
     pos = torch.arange(S, device="cuda")[None]

@@ -319,7 +319,7 @@ extern "C" int wgkv_gate_scores(
   if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0) return WGKV_ERR_ARG;
   if (!w1 || !b1 || !w2 || !b2 || (!scores && !mask)) return WGKV_ERR_ARG;
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
-  if (inner <= 0 || inner % 64) return WGKV_ERR_UNSUPPORTED;
+  if (inner <= 0 || inner % 16) return WGKV_ERR_UNSUPPORTED;  // 16-column tiles
   if (in_dtype != 0 && in_dtype != 1) return WGKV_ERR_UNSUPPORTED;
   GateArgs a = {};
   const void* srcs[3] = {pre_key, post_key, value};

@@ -80,6 +80,17 @@ class E2EConfig:
     local_window_size: int = 1024
     g_threshold: float = 0.1
     qk_norm: bool = False
+    g_expand: float = 4.0
+
+    @staticmethod
+    def qwen3_8b(**kw):
+        """Qwen3-8B shapes: 36 layers, FFN 12288, vocab 151936, rope_theta 1e6,
+        per-head q/k norms and gate width g_expand = 1.5
+        (src/configuration_qwen3.py:183)."""
+        base = dict(intermediate_size=12288, num_hidden_layers=36, vocab_size=151936, rope_theta=1000000.0,
+                    qk_norm=True, g_expand=1.5)
+        base.update(kw)
+        return E2EConfig(**base)
 
 
 class LlamaLite(nn.Module):
@@ -89,7 +100,7 @@ class LlamaLite(nn.Module):
         self.cfg = WGKVConfig(hidden_size=ec.hidden_size, num_hidden_layers=ec.num_hidden_layers,
                               num_attention_heads=ec.num_attention_heads, num_key_value_heads=ec.num_key_value_heads,
                               rope_theta=ec.rope_theta, local_window_size=ec.local_window_size,
-                              g_threshold=ec.g_threshold, use_baseline=not gated,
+                              g_threshold=ec.g_threshold, g_expand=ec.g_expand, use_baseline=not gated,
                               max_tokens_per_head=max_tokens_per_head, max_total_tokens=max_total_tokens,
                               check_capacity=False)
         self.embed_tokens = nn.Embedding(ec.vocab_size, ec.hidden_size)

@@ -79,7 +79,7 @@ def decode_ragged(ctx=131072, batch=8, Hq=32, Hkv=8, D=128, window=1024, page=16
 
 
 def config1_layer(seed=0, hidden=512, Hq=8, Hkv=2, D=64, S=2048, steps=32, W=128, frac=0.2, threshold=0.1,
-                  g_defer=False):
+                  g_defer=False, qk_norm=False, g_expand=4.0):
     """BASELINE config 1 on the host (CPU tensors): weights, prompt, decode inputs.
 
     torch.manual_seed(seed); q/k/v/o ~ N(0, 0.02); gate with the reference's
@@ -93,13 +93,16 @@ def config1_layer(seed=0, hidden=512, Hq=8, Hkv=2, D=64, S=2048, steps=32, W=128
     """
     import math
     torch.manual_seed(seed)
-    inner = 4 * D
+    inner = int(D * g_expand)
     w = {
         "q_proj.weight": torch.randn(Hq * D, hidden) * 0.02,
         "k_proj.weight": torch.randn(Hkv * D, hidden) * 0.02,
         "v_proj.weight": torch.randn(Hkv * D, hidden) * 0.02,
         "o_proj.weight": torch.randn(hidden, Hq * D) * 0.02,
     }
+    if qk_norm:  # Qwen3's per-head norms, weights near 1 so that they matter
+        w["q_norm.weight"] = 1.0 + 0.1 * torch.randn(D)
+        w["k_norm.weight"] = 1.0 + 0.1 * torch.randn(D)
     conv1 = torch.nn.Conv1d(Hkv * 2 * D, Hkv * inner, 1, groups=Hkv)
     conv2 = torch.nn.Conv1d(Hkv * inner, Hkv, 1, groups=Hkv)
     w["g_predictors.pre_key_norm.weight"] = torch.ones(D)
@@ -113,7 +116,7 @@ def config1_layer(seed=0, hidden=512, Hq=8, Hkv=2, D=64, S=2048, steps=32, W=128
     cfg = dict(hidden_size=hidden, num_hidden_layers=1, num_attention_heads=Hq, num_key_value_heads=Hkv,
                head_dim=D, local_window_size=W, block_size=16, max_tokens_per_head=S + steps + 2 * W,
                max_total_tokens=Hkv * (S + steps + 2 * W), g_threshold=threshold, g_defer=g_defer,
-               g_fast_path=True, rope_theta=10000.0)
+               g_fast_path=True, rope_theta=10000.0, g_expand=g_expand)
     cfg["_frac"] = frac
     cfg["_logit_threshold"] = math.log(threshold / (1 - threshold))
     return cfg, w, x, xs
