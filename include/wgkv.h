@@ -141,7 +141,10 @@ int wgkv_prefill_admit(
  *   if g_mask is NULL (deferred gating), pre_key (H, D) is stored in
  *   local_pre_key; cache_seqlens i32 (H) (may be NULL) receives
  *   min(local_length+1, W) + global_lengths[layer] (:1429-1432).
- * local_ptr / local_length are the host-side ring state before this step. */
+ * local_ptr / local_length are the host-side ring state before this step.
+ * quest_key_min / quest_key_max: the QUEST page key bounds, bf16
+ * (total_pages, D), or both NULL; a promoted token starts its page's bounds
+ * (first row) or widens them (src/modeling_layers.py:744-761). */
 int wgkv_decode_append(
     const void* key, const void* value, int64_t kv_stride_h,
     const void* pre_key, int64_t pk_stride_h,
@@ -152,6 +155,7 @@ int wgkv_decode_append(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* quest_key_min, void* quest_key_max,
     void* stream);
 
 /* wgkv_decode_append with the ring state (local_ptr, local_length) in device
@@ -170,6 +174,7 @@ int wgkv_decode_append_ring(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* quest_key_min, void* quest_key_max,
     void* stream);
 
 /* ------------------------------------------------------------------------
@@ -286,6 +291,48 @@ int wgkv_chunk_prefill_attn(
     int32_t layer, int32_t chunk_start, int32_t chunk_len,
     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
     int32_t local_window, int32_t page_size, float softmax_scale, void* stream);
+
+/* ------------------------------------------------------------------------
+ * QUEST page selection over the dual cache (the reference's comparison
+ * baseline, src/modeling_layers.py:452-576; bounds kept at :1333-1347 and
+ * :744-761).  key_min / key_max: bf16 (total_pages, D), one row per pool page.
+ *
+ * wgkv_quest_update_bounds: for every head of `layer`, recompute the bounds
+ * of the logical global pages [from/page, ceil(len/page)) -- from =
+ * from_lengths[h] (i32 (H), the global lengths before the update) or 0 when
+ * from_lengths is NULL -- as the elementwise min / max of the page's valid
+ * key rows (what the reference's prefill writes and its decode-time updates
+ * accumulate).  Call after wgkv_prefill_admit (from NULL) or after a chunk's
+ * admission (from = the lengths before it).
+ *
+ * wgkv_quest_select: the selection of quest_select_blocks for one decode
+ * step of `layer`: q bf16 (Hq, D) (stride q_stride_h) of the step's token;
+ * each KV head scores its full global pages by max over its G query heads of
+ * sum_d q_d * (q_d >= 0 ? key_max_d : key_min_d) (fp32), keeps the top
+ * k = min(ceil(max(budget - local_tokens, 0)/page), global pages) - (1 if a
+ * partial page exists) full pages (equal scores at the cut: lowest page
+ * first) and the partial page, and writes sel_block_table i32 (H, sel_cap):
+ * the head's first ceil(local_tokens/page) local pages, the kept full pages
+ * in page order, then the partial page; sel_seqlens i32 (H) = local_tokens +
+ * the kept tokens.  These feed wgkv_paged_decode_attn (batch 1).  sel_cap >=
+ * ceil(local_tokens/page) + ceil(max(budget - local_tokens, 0)/page).
+ * ---------------------------------------------------------------------- */
+int wgkv_quest_update_bounds(
+    const void* pool_k, const int32_t* block_table, int32_t max_pages_per_head,
+    const int32_t* global_lengths, const int32_t* from_lengths,
+    int32_t layer, int32_t num_layers, int32_t num_kv_heads, int32_t local_window, int32_t page_size,
+    int32_t head_dim, void* key_min, void* key_max, void* stream);
+
+size_t wgkv_quest_select_workspace_bytes(int32_t num_kv_heads, int32_t max_pages_per_head);
+
+int wgkv_quest_select(
+    const void* q, int64_t q_stride_h,
+    const int32_t* block_table, int32_t max_pages_per_head, const int32_t* global_lengths,
+    const void* key_min, const void* key_max,
+    int32_t layer, int32_t num_layers, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    int32_t local_window, int32_t page_size, int32_t local_tokens, int32_t token_budget,
+    int32_t* sel_block_table, int32_t sel_cap, int32_t* sel_seqlens,
+    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -198,6 +198,8 @@ struct AppendArgs {
   int64_t total_pages;
   int local_ptr, local_length, do_migrate, do_write;
   int32_t* ring;  // device (local_ptr, local_length), replacing the two above when set
+  uint16_t* qmin;  // QUEST page key bounds (total_pages, D) or NULL
+  uint16_t* qmax;
   int advance;    // with ring: advance it after this layer's write (the last layer's call)
   uint16_t* pool_k;
   uint16_t* pool_v;
@@ -278,8 +280,36 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
         const int64_t src = (int64_t)i * a.W + local_ptr;
         const int64_t dst = (int64_t)pg * a.page + gl % a.page;
         for (int c = 0; c < a.D / 8; ++c) {
-          *(u32x4_t*)(a.pool_k + dst * a.D + c * 8) = *(const u32x4_t*)(a.pool_k + src * a.D + c * 8);
+          const u32x4_t kv = *(const u32x4_t*)(a.pool_k + src * a.D + c * 8);
+          *(u32x4_t*)(a.pool_k + dst * a.D + c * 8) = kv;
           *(u32x4_t*)(a.pool_v + dst * a.D + c * 8) = *(const u32x4_t*)(a.pool_v + src * a.D + c * 8);
+          if (a.qmin) {
+            // QUEST page bounds (:744-761): a new page starts at the key, else min / max with it
+            u32x4_t* mn = (u32x4_t*)(a.qmin + (int64_t)pg * a.D + c * 8);
+            u32x4_t* mx = (u32x4_t*)(a.qmax + (int64_t)pg * a.D + c * 8);
+            if (gl % a.page == 0) {
+              *mn = kv;
+              *mx = kv;
+            } else {
+              u32x4_t lo = *mn, hi = *mx;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                uint32_t l = lo[e], hh = hi[e];
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                  const uint32_t sh = 16u * half;
+                  const uint32_t x = (kv[e] >> sh) & 0xffffu;
+                  const float xf = __uint_as_float(x << 16);
+                  if (xf < __uint_as_float(((l >> sh) & 0xffffu) << 16)) l = (l & ~(0xffffu << sh)) | (x << sh);
+                  if (xf > __uint_as_float(((hh >> sh) & 0xffffu) << 16)) hh = (hh & ~(0xffffu << sh)) | (x << sh);
+                }
+                lo[e] = l;
+                hi[e] = hh;
+              }
+              *mn = lo;
+              *mx = hi;
+            }
+          }
         }
         a.global_lengths[i] = gl + 1;
       }
@@ -405,6 +435,7 @@ int decode_append_launch(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* quest_key_min, void* quest_key_max,
     void* stream) {
   if (do_write && (!key || !value)) return WGKV_ERR_ARG;
   if (!pool_k || !pool_v || !block_table || !global_lengths || !local_is_global ||
@@ -438,6 +469,10 @@ int decode_append_launch(
   a.local_length = local_length;
   a.ring = ring_state;
   a.advance = advance;
+  if ((quest_key_min == nullptr) != (quest_key_max == nullptr)) return WGKV_ERR_ARG;
+  if (((uintptr_t)quest_key_min | (uintptr_t)quest_key_max) & 15) return WGKV_ERR_UNSUPPORTED;
+  a.qmin = (uint16_t*)quest_key_min;
+  a.qmax = (uint16_t*)quest_key_max;
   a.do_migrate = do_migrate;
   a.do_write = do_write;
   a.pool_k = (uint16_t*)pool_k;
@@ -466,12 +501,13 @@ extern "C" int wgkv_decode_append(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* quest_key_min, void* quest_key_max,
     void* stream) {
   return decode_append_launch(key, value, kv_stride_h, pre_key, pk_stride_h, g_mask, layer, num_layers, num_kv_heads,
                               head_dim, local_window, page_size, max_tokens_per_head, total_pages, local_ptr,
                               local_length, nullptr, 0, do_migrate, do_write, pool_k, pool_v, block_table,
                               max_pages_per_head, global_lengths, local_is_global, local_pre_key, next_free_block,
-                              cache_seqlens, status, stream);
+                              cache_seqlens, status, quest_key_min, quest_key_max, stream);
 }
 
 extern "C" int wgkv_decode_append_ring(
@@ -484,11 +520,12 @@ extern "C" int wgkv_decode_append_ring(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
+    void* quest_key_min, void* quest_key_max,
     void* stream) {
   if (!ring_state) return WGKV_ERR_ARG;
   return decode_append_launch(key, value, kv_stride_h, pre_key, pk_stride_h, g_mask, layer, num_layers, num_kv_heads,
                               head_dim, local_window, page_size, max_tokens_per_head, total_pages, 0, 0, ring_state,
                               advance, do_migrate, do_write, pool_k, pool_v, block_table, max_pages_per_head,
                               global_lengths, local_is_global, local_pre_key, next_free_block, cache_seqlens, status,
-                              stream);
+                              quest_key_min, quest_key_max, stream);
 }

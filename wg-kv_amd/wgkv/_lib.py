@@ -69,6 +69,7 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr, c_i32,
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr,
         c_ptr]),
     "wgkv_decode_append_ring": (ctypes.c_int, [
         c_ptr, c_ptr, c_i64,
@@ -80,6 +81,7 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr, c_i32,
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr,
         c_ptr]),
     "wgkv_gate_scores": (ctypes.c_int, [
         c_ptr, c_i64, c_i64, c_i64,
@@ -101,6 +103,20 @@ SIGNATURES = {
         c_ptr, c_ptr, c_i64, c_i64,
         c_i32, c_i32, c_i32, c_i32, c_i32,
         c_i32, c_f32, c_ptr]),
+    "wgkv_quest_update_bounds": (ctypes.c_int, [
+        c_ptr, c_ptr, c_i32,
+        c_ptr, c_ptr,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_ptr, c_ptr, c_ptr]),
+    "wgkv_quest_select_workspace_bytes": (c_size, [c_i32, c_i32]),
+    "wgkv_quest_select": (ctypes.c_int, [
+        c_ptr, c_i64,
+        c_ptr, c_i32, c_ptr,
+        c_ptr, c_ptr,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32, c_i32,
+        c_ptr, c_i32, c_ptr,
+        c_ptr, c_size, c_ptr]),
     "wgkv_chunk_admit_workspace_bytes": (c_size, [c_i32, c_i32, c_i32]),
     "wgkv_chunk_cache_update": (ctypes.c_int, [
         c_i32,

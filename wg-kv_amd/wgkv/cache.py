@@ -57,6 +57,9 @@ class DualCache:
         self.local_region_starts = ((torch.arange(L, **i32)[:, None] * H + torch.arange(H, **i32)[None, :]) * W)
         self.local_pre_key = (torch.empty(L, H, W, head_dim, dtype=dtype, device=device)
                               if getattr(config, "g_defer", False) else None)
+        if getattr(config, "use_quest", False):  # page key bounds (reference :1232-1240)
+            self.quest_block_key_min = torch.empty(self.total_blocks, head_dim, dtype=dtype, device=device)
+            self.quest_block_key_max = torch.empty(self.total_blocks, head_dim, dtype=dtype, device=device)
         self.local_ptr = 0
         self.local_length = 0
         self.prefill_length = 0  # prompt tokens in the cache (all layers); chunks continue from here

@@ -9,9 +9,10 @@ HIP library (kernels (1)-(4)).  ``self`` needs ``config``, ``layer_idx``,
 ``head_dim``, ``scaling``, ``num_key_value_groups`` and the attributes above
 (and ``g_predictors`` when the gate is learned).
 
-Only inference (gating_mode 3) is on the hot path; the training modes and the
-comparison baselines (DuoAttention, AdaEA, QUEST, SnapKV) are outside it and
-raise NotImplementedError.
+Only inference (gating_mode 3) is on the hot path.  Of the comparison
+baselines, QUEST page selection (``use_quest``) runs on the same page tables
+and decode kernel; the training modes, DuoAttention, AdaEA and SnapKV are
+outside it and raise NotImplementedError.
 """
 from dataclasses import dataclass, field
 from typing import List, Optional
@@ -52,6 +53,7 @@ class WGKVConfig:
     use_duo_attn: bool = False
     use_adaea: bool = False
     use_quest: bool = False
+    quest_token_budget: Optional[int] = None
     snapkv_enabled: bool = False
     check_capacity: bool = True  # read the device status after cache writes (a host sync)
 
@@ -119,10 +121,13 @@ def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, val
         if c0 < W or q_seq_len < W or c0 % 64:
             raise AssertionError(f"chunked prefill needs prefill_length >= W, chunk >= W and a 64-aligned start "
                                  f"(prefill_length={c0}, chunk={q_seq_len}, W={W})")
+        before = c.global_lengths[self.layer_idx].clone() if self.config.use_quest else None
         out = ops.chunk_prefill(c, self.layer_idx, query_states[0].transpose(0, 1), key_states[0].transpose(0, 1),
                                 value_states[0].transpose(0, 1), g_mask[0], c0, self.scaling,
                                 pre_key=pre_key[0].transpose(0, 1) if (defer and pre_key is not None) else None)
         _layer_cache_check(self, c, f"prefill_wrapper chunk at {c0} (layer {self.layer_idx})")
+        if self.config.use_quest:
+            ops.quest_update_bounds(c, self.layer_idx, from_lengths=before)
         c.local_length = min(c0 + q_seq_len, W)
         if self.layer_idx == self.config.num_hidden_layers - 1:
             c.prefill_length = c0 + q_seq_len
@@ -130,6 +135,8 @@ def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, val
     ops.prefill_admit(c, self.layer_idx, key_states[0], value_states[0], g_mask[0],
                       pre_key=pre_key[0] if (defer and pre_key is not None) else None)
     _layer_cache_check(self, c, f"prefill_wrapper (layer {self.layer_idx})")
+    if self.config.use_quest:  # :1333-1347
+        ops.quest_update_bounds(c, self.layer_idx)
     c.local_length = min(q_seq_len, W)  # :1297
     if self.layer_idx == self.config.num_hidden_layers - 1:
         c.prefill_length = q_seq_len
@@ -157,11 +164,20 @@ def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, valu
         if c.device_ring:
             raise AssertionError("deferred gating re-gates on a host condition; it cannot run with device_ring")
         refresh_local_is_global(self, c, device)
+    if self.config.use_quest:  # :1419-1427
+        if c.device_ring:
+            raise AssertionError("QUEST selection takes the host ring length; it cannot run with device_ring")
+        if self.config.quest_token_budget is None:
+            raise AssertionError("use_quest needs quest_token_budget")
+        local_tokens = min(c.local_length + 1, W)
+        seqlens, table = ops.quest_select(c, self.layer_idx, query_states[0, :, 0], local_tokens,
+                                          self.config.quest_token_budget)
+    else:
+        table = c.block_table[self.layer_idx].unsqueeze(0)
     if last:
         c.advance_host_ring()
     handle = self.decode_kernel_handle(
-        query_states.transpose(1, 2), c.k_cache(), c.v_cache(), seqlens,
-        c.block_table[self.layer_idx].unsqueeze(0), self.scaling)
+        query_states.transpose(1, 2), c.k_cache(), c.v_cache(), seqlens, table, self.scaling)
     return self.decode_kernel_executor(handle)
 
 
@@ -198,6 +214,8 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
         raise NotImplementedError("only inference (gating_mode 3) is on the MI355X path")
     if cfg.use_duo_attn or cfg.use_adaea:
         raise NotImplementedError("DuoAttention / AdaEA baselines are outside the hot path")
+    if cfg.snapkv_enabled:
+        raise NotImplementedError("SnapKV eviction is not built on the MI355X path")
     kv_seq_len = key_states.size(2)
     g_scores = None
     g_mask = None

@@ -216,6 +216,7 @@ def decode_append(cache, layer, key=None, value=None, g_mask=None, pre_key=None,
     tail = (_ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), cache.block_table.shape[2],
             _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(cache.local_pre_key),
             _ptr(cache.next_free_block_dev), _ptr(cache_seqlens), _ptr(cache.status),
+            _ptr(getattr(cache, "quest_block_key_min", None)), _ptr(getattr(cache, "quest_block_key_max", None)),
             _lib.stream_handle(cache.block_pool_k.device))
     if getattr(cache, "device_ring", False):
         st = L.wgkv_decode_append_ring(*head, _ptr(cache.ring_state), int(advance), int(migrate), int(write), *tail)
@@ -363,3 +364,46 @@ def chunk_prefill(cache, layer, q, key, value, g_mask, chunk_start, softmax_scal
     out = step.attend()
     step.ring()
     return out
+
+
+# ---------------------------------------------------------------------------
+# QUEST page selection (the reference's comparison baseline) over kernel (2)
+# ---------------------------------------------------------------------------
+def quest_update_bounds(cache, layer, from_lengths=None):
+    """Recompute the page key bounds of ``layer``'s global pages from
+    ``from_lengths`` (H,) (the global lengths before an admission; None: from
+    the first page)."""
+    st = _lib.lib().wgkv_quest_update_bounds(
+        _ptr(cache.block_pool_k), _ptr(cache.block_table), cache.block_table.shape[2],
+        _ptr(cache.global_lengths), _ptr(from_lengths),
+        layer, cache.num_layers, cache.num_kv_heads, cache.local_window_size, cache.block_size,
+        cache.head_dim, _ptr(cache.quest_block_key_min), _ptr(cache.quest_block_key_max),
+        _lib.stream_handle(cache.block_pool_k.device))
+    _lib.check(st, "wgkv_quest_update_bounds")
+
+
+def quest_select(cache, layer, q, local_tokens, token_budget):
+    """quest_select_blocks (src/modeling_layers.py:452-576) for one decode
+    step of ``layer``: q (Hq, D) bf16.  Returns (cache_seqlens (1, H),
+    block_table (1, H, cap)) for paged_decode_attn."""
+    H, D = cache.num_kv_heads, cache.head_dim
+    P = cache.block_size
+    cap = (local_tokens + P - 1) // P + (max(token_budget - local_tokens, 0) + P - 1) // P + 1
+    dev = q.device
+    key = ("quest_sel", H, cap)
+    bufs = cache.__dict__.setdefault("_quest_bufs", {})
+    if key not in bufs:  # stable buffers (a captured decode step reuses them)
+        bufs[key] = (torch.zeros(1, H, cap, dtype=torch.int32, device=dev), torch.zeros(1, H, dtype=torch.int32, device=dev))
+    sel_bt, sel_len = bufs[key]
+    L = _lib.lib()
+    ws = workspace(dev, L.wgkv_quest_select_workspace_bytes(H, cache.block_table.shape[2]))
+    st = L.wgkv_quest_select(
+        _ptr(q), q.stride(0),
+        _ptr(cache.block_table), cache.block_table.shape[2], _ptr(cache.global_lengths),
+        _ptr(cache.quest_block_key_min), _ptr(cache.quest_block_key_max),
+        layer, cache.num_layers, q.shape[0], H, D,
+        cache.local_window_size, P, int(local_tokens), int(token_budget),
+        _ptr(sel_bt), cap, _ptr(sel_len),
+        _ptr(ws), ws.numel(), _lib.stream_handle(dev))
+    _lib.check(st, "wgkv_quest_select")
+    return sel_len, sel_bt
