@@ -222,6 +222,56 @@ def prefill_section(dev, steps, warmup):
     }
 
 
+def quest_section(dev, steps, warmup):
+    """QUEST page selection (the reference's comparison baseline) at Llama-8B
+    decode shapes: one layer, batch 1, a 128K prompt with 20 % admitted
+    (~27K cached tokens per KV head), token budget 4096.  Per decode step:
+    the selection (page scores + top-k, one launch) and the decode attention
+    over the selected pages, beside the attention over the whole cache."""
+    import torch
+    from wgkv import ops
+    from wgkv.cache import DualCache
+    from wgkv.layers import WGKVConfig
+
+    S, H, G, D, W, budget = 131072, 8, 4, 128, 1024, 4096
+    cfg = WGKVConfig(num_hidden_layers=1, num_attention_heads=H * G, num_key_value_heads=H, head_dim=D,
+                     hidden_size=H * G * D, local_window_size=W, max_tokens_per_head=S + W,
+                     max_total_tokens=H * (S + W), use_quest=True, quest_token_budget=budget)
+    c = DualCache()
+    c.initialize(cfg, D, torch.bfloat16, dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    k = torch.randn(H, S, D, generator=g, device=dev).to(torch.bfloat16)
+    v = torch.randn(H, S, D, generator=g, device=dev).to(torch.bfloat16)
+    m = torch.rand(H, S, generator=g, device=dev) < 0.2
+    ops.prefill_admit(c, 0, k, v, m)
+    ops.quest_update_bounds(c, 0)
+    del k, v
+    c.local_length = W
+    seqlens = (W + c.global_lengths[0]).view(1, H).contiguous()
+    q = torch.randn(1, 1, H * G, D, generator=g, device=dev).to(torch.bfloat16)  # (batch, 1, Hq, D)
+    out = torch.empty_like(q)
+    sel = {}
+
+    def select():
+        sel["r"] = ops.quest_select(c, 0, q[0, 0], W, budget)
+
+    t_sel = time_op(select, steps, warmup)
+    sl, bt = sel["r"]
+    t_att_sel = time_op(lambda: ops.paged_decode_attn(q, c.k_cache(), c.v_cache(), sl, bt, D ** -0.5, out=out),
+                        steps, warmup)
+    t_att_full = time_op(lambda: ops.paged_decode_attn(q, c.k_cache(), c.v_cache(), seqlens,
+                                                       c.block_table[0].unsqueeze(0), D ** -0.5, out=out),
+                         steps, warmup)
+    torch.cuda.synchronize()
+    tok_full = int(seqlens.sum())
+    tok_sel = int(sl.sum())
+    return {"workload": "quest_b1_128k (one layer, 20 % admitted, budget 4096 tokens per head)",
+            "cached_tokens": tok_full, "selected_tokens": tok_sel,
+            "us": {"select": round(t_sel * 1e3, 1), "attention_selected": round(t_att_sel * 1e3, 1),
+                   "attention_full_cache": round(t_att_full * 1e3, 1)},
+            "bounds_bytes_read_per_step": int((c.global_lengths[0] // 16).sum()) * D * 2 * 2}
+
+
 def layer_section(dev, cpu_budget):
     """the write-gated layer (2048 prefill + 32 decode
     steps) on the GPU through the HIP path, and the same layer as the CPU
@@ -452,6 +502,9 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_prefill:
         result["prefill"] = prefill_section(dev, max(5, args.steps // 5), max(2, args.warmup // 5))
+        torch.cuda.empty_cache()
+    if not args.no_secondary:
+        result["quest"] = quest_section(dev, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if not args.no_layer:
         result["layer_config1"] = layer_section(dev, args.cpu_seconds)

@@ -11,8 +11,9 @@
 //   * quest_bounds_kernel: recompute the bounds of a head's logical global
 //     pages [from/page, ceil(len/page)) from the pool (the min / max over the
 //     page's valid rows, which equals the reference's incremental updates);
-//   * quest_select_kernel: one workgroup per head -- scores into the
-//     workspace, a 4-pass radix select of the k-th largest score, then a
+//   * quest_scores_kernel: the page scores of every head into the workspace;
+//   * quest_select_kernel: one workgroup per head -- a 4-pass radix select
+//     of the k-th largest score, then a
 //     stable compaction that writes local pages, the kept full pages in page
 //     order and the partial page, and the head's token count.
 // Scores are fp32 (the reference's are bf16 products summed by torch);
@@ -76,6 +77,48 @@ struct SelectArgs {
   float* scores;       // workspace (H, max_pages)
 };
 
+// Page scores, grid (64, H): 16 lanes per page (8 d-values each, 16-byte
+// loads of the bounds), the lane partials summed with a 16-lane row
+// reduction; workgroups stride over the head's full pages.
+__global__ __launch_bounds__(kThreads) void quest_scores_kernel(SelectArgs a) {
+  __shared__ float s_q[8][256];
+  const int h = blockIdx.y, t = threadIdx.x;
+  const int full = a.len[h] / a.page;
+  for (int e = t; e < a.G * a.D; e += kThreads) {
+    const int g = e / a.D, d = e - g * a.D;
+    s_q[g][d] = bf(a.q[(int64_t)(h * a.G + g) * a.q_sh + d]);
+  }
+  __syncthreads();
+  const int32_t* bt = a.bt + (int64_t)h * a.max_pages + a.lb;
+  float* sc = a.scores + (int64_t)h * a.max_pages;
+  const int lane16 = t & 15, slot = t >> 4;  // 16 pages per pass
+  const int nch = a.D / 8;                   // 8-value chunks per row (<= 32)
+  for (int p0 = blockIdx.x * 16; p0 < full; p0 += gridDim.x * 16) {
+    const int p = p0 + slot;
+    const bool ok = p < full;
+    const int64_t pg = ok ? bt[p] : 0;
+    float s[8];
+#pragma unroll
+    for (int g = 0; g < 8; ++g) s[g] = 0.f;
+    for (int c = lane16; c < nch; c += 16) {
+      const u32x4_t lo = ok ? *(const u32x4_t*)(a.kmin + pg * a.D + c * 8) : (u32x4_t){0u, 0u, 0u, 0u};
+      const u32x4_t hi = ok ? *(const u32x4_t*)(a.kmax + pg * a.D + c * 8) : (u32x4_t){0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float l = (e & 1) ? bf16hi(lo[e >> 1]) : bf16lo(lo[e >> 1]);
+        const float u = (e & 1) ? bf16hi(hi[e >> 1]) : bf16lo(hi[e >> 1]);
+        for (int g = 0; g < a.G; ++g) {
+          const float qd = s_q[g][c * 8 + e];
+          s[g] = fmaf(qd, qd >= 0.f ? u : l, s[g]);
+        }
+      }
+    }
+    float best = -INFINITY;
+    for (int g = 0; g < a.G; ++g) best = fmaxf(best, row_sum16(s[g]));
+    if (ok && lane16 == 0) sc[p] = best;
+  }
+}
+
 // order-preserving map of an fp32 to uint32 (larger float -> larger key)
 __device__ __forceinline__ uint32_t fkey(float f) {
   const uint32_t u = __float_as_uint(f);
@@ -83,7 +126,6 @@ __device__ __forceinline__ uint32_t fkey(float f) {
 }
 
 __global__ __launch_bounds__(kThreads) void quest_select_kernel(SelectArgs a) {
-  __shared__ float s_q[8][256];
   __shared__ int s_hist[256];
   __shared__ int s_tmp[kThreads];
   __shared__ uint32_t s_prefix;
@@ -106,42 +148,7 @@ __global__ __launch_bounds__(kThreads) void quest_select_kernel(SelectArgs a) {
   const int keep = k <= 0 ? 0 : (all ? full : k);
 
   if (keep > 0 && !all) {
-    // scores of the full pages
-    for (int e = t; e < a.G * a.D; e += kThreads) {
-      const int g = e / a.D, d = e - g * a.D;
-      s_q[g][d] = bf(a.q[(int64_t)(h * a.G + g) * a.q_sh + d]);
-    }
-    __syncthreads();
-    for (int p = t; p < full; p += kThreads) {
-      const int64_t pg = bt[a.lb + p];
-      const uint16_t* mn = a.kmin + pg * a.D;
-      const uint16_t* mx = a.kmax + pg * a.D;
-      float s[8];
-      for (int g = 0; g < 8; ++g) s[g] = 0.f;
-      for (int d0 = 0; d0 < a.D; d0 += 8) {  // 16-byte loads of the page's bounds
-        const u32x4_t lo = *(const u32x4_t*)(mn + d0);
-        const u32x4_t hi = *(const u32x4_t*)(mx + d0);
-        float l8[8], h8[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          l8[2 * e] = bf16lo(lo[e]);
-          l8[2 * e + 1] = bf16hi(lo[e]);
-          h8[2 * e] = bf16lo(hi[e]);
-          h8[2 * e + 1] = bf16hi(hi[e]);
-        }
-        for (int g = 0; g < a.G; ++g)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float qd = s_q[g][d0 + e];
-            s[g] = fmaf(qd, qd >= 0.f ? h8[e] : l8[e], s[g]);
-          }
-      }
-      float best = s[0];
-      for (int g = 1; g < a.G; ++g) best = fmaxf(best, s[g]);
-      sc[p] = best;
-    }
-    __syncthreads();
-    // radix select: the key of the keep-th largest score
+    // radix select of the key of the keep-th largest score
     if (t == 0) {
       s_prefix = 0;
       s_need = keep;
@@ -151,37 +158,49 @@ __global__ __launch_bounds__(kThreads) void quest_select_kernel(SelectArgs a) {
       s_hist[t] = 0;
       __syncthreads();
       const uint32_t hi_mask = shift == 24 ? 0u : (0xffffffffu << (shift + 8));
+      const uint32_t prefix = s_prefix;
       for (int p = t; p < full; p += kThreads) {
         const uint32_t key = fkey(sc[p]);
-        if ((key & hi_mask) == (s_prefix & hi_mask)) atomicAdd(&s_hist[(key >> shift) & 255], 1);
+        if ((key & hi_mask) == (prefix & hi_mask)) atomicAdd(&s_hist[(key >> shift) & 255], 1);
       }
       __syncthreads();
-      if (t == 0) {
-        int need = s_need, b = 255;
-        for (; b > 0; --b) {
-          if (s_hist[b] >= need) break;
-          need -= s_hist[b];
-        }
-        s_prefix |= (uint32_t)b << shift;
-        s_need = need;
+      // counts from the top bin down: thread t holds bin 255 - t
+      const int c = s_hist[255 - t];
+      int total = 0;
+      const int above = block_exclusive_scan_256(c, s_tmp, &total);  // keys in higher bins
+      const int need = s_need;
+      __syncthreads();
+      if (above < need && need <= above + c) {  // the bin holding the need-th key
+        s_prefix = prefix | ((uint32_t)(255 - t) << shift);
+        s_need = need - above;
       }
       __syncthreads();
     }
-    // kept: key > T, plus the first s_need pages (in page order) with key == T
+    // kept: key > T, plus the first s_need pages (in page order) with key == T;
+    // thread t owns the contiguous pages [t*per, (t+1)*per)
     const uint32_t T = s_prefix;
-    int eq_before = 0, kept_before = 0;
-    for (int p0 = 0; p0 < full; p0 += kThreads) {
-      const int p = p0 + t;
-      const uint32_t key = p < full ? fkey(sc[p]) : 0u;
-      const int eq = (p < full && key == T) ? 1 : 0;
-      int eq_tot = 0;
-      const int eq_rank = eq_before + block_exclusive_scan_256(eq, s_tmp, &eq_tot);
-      const int take = (p < full && (key > T || (eq && eq_rank < s_need))) ? 1 : 0;
-      int take_tot = 0;
-      const int pos = kept_before + block_exclusive_scan_256(take, s_tmp, &take_tot);
-      if (take) out[local_blocks + pos] = bt[a.lb + p];
-      eq_before += eq_tot;
-      kept_before += take_tot;
+    const int need_eq = s_need;
+    const int per = (full + kThreads - 1) / kThreads;
+    const int p0 = min(full, t * per), p1 = min(full, p0 + per);
+    int n_eq = 0;
+    for (int p = p0; p < p1; ++p) n_eq += fkey(sc[p]) == T ? 1 : 0;
+    int tot = 0;
+    int eq_rank = block_exclusive_scan_256(n_eq, s_tmp, &tot);
+    int n_take = 0;
+    {
+      int r = eq_rank;
+      for (int p = p0; p < p1; ++p) {
+        const uint32_t key = fkey(sc[p]);
+        if (key > T) ++n_take;
+        else if (key == T) n_take += (r++ < need_eq) ? 1 : 0;
+      }
+    }
+    int pos = local_blocks + block_exclusive_scan_256(n_take, s_tmp, &tot);
+    for (int p = p0; p < p1; ++p) {
+      const uint32_t key = fkey(sc[p]);
+      bool take = key > T;
+      if (key == T) take = eq_rank++ < need_eq;
+      if (take) out[pos++] = bt[a.lb + p];
     }
   } else if (keep > 0) {
     for (int p = t; p < keep; p += kThreads) out[local_blocks + p] = bt[a.lb + p];
@@ -262,6 +281,8 @@ extern "C" int wgkv_quest_select(
   a.sel_cap = sel_cap;
   a.sel_len = sel_seqlens;
   a.scores = (float*)workspace;
-  hipLaunchKernelGGL(quest_select_kernel, dim3(num_kv_heads), dim3(kThreads), 0, (hipStream_t)stream, a);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(quest_scores_kernel, dim3(64, num_kv_heads), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL(quest_select_kernel, dim3(num_kv_heads), dim3(kThreads), 0, st, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
