@@ -144,7 +144,11 @@ int wgkv_prefill_admit(
  * local_ptr / local_length are the host-side ring state before this step.
  * quest_key_min / quest_key_max: the QUEST page key bounds, bf16
  * (total_pages, D), or both NULL; a promoted token starts its page's bounds
- * (first row) or widens them (src/modeling_layers.py:744-761). */
+ * (first row) or widens them (src/modeling_layers.py:744-761).
+ * free_ids / free_count: SnapKV's list of released pages (i32, ids in
+ * release order, and its device length) or both NULL; pages for promotion
+ * come from the last entries of the list first, in list order, then from
+ * next_free_block (:694-712). */
 int wgkv_decode_append(
     const void* key, const void* value, int64_t kv_stride_h,
     const void* pre_key, int64_t pk_stride_h,
@@ -155,7 +159,7 @@ int wgkv_decode_append(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
-    void* quest_key_min, void* quest_key_max,
+    void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream);
 
 /* wgkv_decode_append with the ring state (local_ptr, local_length) in device
@@ -174,7 +178,7 @@ int wgkv_decode_append_ring(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
-    void* quest_key_min, void* quest_key_max,
+    void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream);
 
 /* ------------------------------------------------------------------------

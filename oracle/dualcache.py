@@ -111,15 +111,23 @@ class DualCacheOracle:
                 raise CapacityError("Tokens exceed max_tokens_per_head")
             if gl % P == 0:
                 new_pages += 1
-        if self.next_free_block + new_pages > self.total_blocks:
+        free = getattr(self, "free_block_ids", None)  # SnapKV: released pages, reused first (:694-712)
+        from_free = min(new_pages, len(free)) if free is not None else 0
+        if self.next_free_block + new_pages - from_free > self.total_blocks:
             raise CapacityError("Allocation exceeds total_blocks")
+        reuse = free[len(free) - from_free:] if from_free else []
+        if from_free:
+            del free[len(free) - from_free:]
         nxt = self.next_free_block
         for l, h in items:
             gl = int(self.global_lengths[l, h])
             logical = lb + gl // P
             if gl % P == 0:
-                self.block_table[l, h, logical] = nxt
-                nxt += 1
+                if reuse:
+                    self.block_table[l, h, logical] = reuse.pop(0)
+                else:
+                    self.block_table[l, h, logical] = nxt
+                    nxt += 1
             src = int(self.local_region_starts[l, h]) + slot
             dst = int(self.block_table[l, h, logical]) * P + gl % P
             self.block_pool_k[dst] = self.block_pool_k[src]

@@ -200,6 +200,8 @@ struct AppendArgs {
   int32_t* ring;  // device (local_ptr, local_length), replacing the two above when set
   uint16_t* qmin;  // QUEST page key bounds (total_pages, D) or NULL
   uint16_t* qmax;
+  int32_t* free_ids;    // SnapKV free page list (ids in release order) or NULL
+  int32_t* free_count;  // its length (device)
   int advance;    // with ring: advance it after this layer's write (the last layer's call)
   uint16_t* pool_k;
   uint16_t* pool_v;
@@ -249,7 +251,11 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
       need_total += total;
     }
     const int nf = *a.next_free;
-    if (t == 0 && (int64_t)nf + need_total > a.total_pages) s_fail = 1;
+    // freed pages are reused first: the last from_free entries of the list, in
+    // list order, go to the first heads that need a page (:694-712)
+    const int n_free = a.free_ids ? *a.free_count : 0;
+    const int from_free = min(need_total, n_free);
+    if (t == 0 && (int64_t)nf + (need_total - from_free) > a.total_pages) s_fail = 1;
     __syncthreads();
     if (s_fail) {
       if (t == 0) *a.status = WGKV_ERR_CAPACITY;
@@ -272,7 +278,8 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
         int32_t* bt = a.block_table + (int64_t)i * a.max_pages + lb + gl / a.page;
         int pg;
         if (need) {
-          pg = nf + carry + excl;
+          const int rank = carry + excl;
+          pg = rank < from_free ? a.free_ids[n_free - from_free + rank] : nf + (rank - from_free);
           *bt = pg;
         } else {
           pg = *bt;
@@ -315,7 +322,10 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
       }
       carry += total;
     }
-    if (t == 0) *a.next_free = nf + carry;
+    if (t == 0) {
+      *a.next_free = nf + carry - from_free;
+      if (a.free_ids) *a.free_count = n_free - from_free;
+    }
     __syncthreads();
   }
   if (!a.do_write) return;
@@ -435,9 +445,10 @@ int decode_append_launch(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
-    void* quest_key_min, void* quest_key_max,
+    void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream) {
   if (do_write && (!key || !value)) return WGKV_ERR_ARG;
+  if ((free_ids == nullptr) != (free_count == nullptr)) return WGKV_ERR_ARG;
   if (!pool_k || !pool_v || !block_table || !global_lengths || !local_is_global ||
       !next_free_block || !status)
     return WGKV_ERR_ARG;
@@ -473,6 +484,8 @@ int decode_append_launch(
   if (((uintptr_t)quest_key_min | (uintptr_t)quest_key_max) & 15) return WGKV_ERR_UNSUPPORTED;
   a.qmin = (uint16_t*)quest_key_min;
   a.qmax = (uint16_t*)quest_key_max;
+  a.free_ids = free_ids;
+  a.free_count = free_count;
   a.do_migrate = do_migrate;
   a.do_write = do_write;
   a.pool_k = (uint16_t*)pool_k;
@@ -501,13 +514,13 @@ extern "C" int wgkv_decode_append(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
-    void* quest_key_min, void* quest_key_max,
+    void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream) {
   return decode_append_launch(key, value, kv_stride_h, pre_key, pk_stride_h, g_mask, layer, num_layers, num_kv_heads,
                               head_dim, local_window, page_size, max_tokens_per_head, total_pages, local_ptr,
                               local_length, nullptr, 0, do_migrate, do_write, pool_k, pool_v, block_table,
                               max_pages_per_head, global_lengths, local_is_global, local_pre_key, next_free_block,
-                              cache_seqlens, status, quest_key_min, quest_key_max, stream);
+                              cache_seqlens, status, quest_key_min, quest_key_max, free_ids, free_count, stream);
 }
 
 extern "C" int wgkv_decode_append_ring(
@@ -520,12 +533,12 @@ extern "C" int wgkv_decode_append_ring(
     void* pool_k, void* pool_v, int32_t* block_table, int32_t max_pages_per_head,
     int32_t* global_lengths, uint8_t* local_is_global, void* local_pre_key,
     int32_t* next_free_block, int32_t* cache_seqlens, int32_t* status,
-    void* quest_key_min, void* quest_key_max,
+    void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream) {
   if (!ring_state) return WGKV_ERR_ARG;
   return decode_append_launch(key, value, kv_stride_h, pre_key, pk_stride_h, g_mask, layer, num_layers, num_kv_heads,
                               head_dim, local_window, page_size, max_tokens_per_head, total_pages, 0, 0, ring_state,
                               advance, do_migrate, do_write, pool_k, pool_v, block_table, max_pages_per_head,
                               global_lengths, local_is_global, local_pre_key, next_free_block, cache_seqlens, status,
-                              quest_key_min, quest_key_max, stream);
+                              quest_key_min, quest_key_max, free_ids, free_count, stream);
 }

@@ -69,7 +69,7 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr, c_i32,
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr,
-        c_ptr, c_ptr,
+        c_ptr, c_ptr, c_ptr, c_ptr,
         c_ptr]),
     "wgkv_decode_append_ring": (ctypes.c_int, [
         c_ptr, c_ptr, c_i64,
@@ -81,7 +81,7 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr, c_i32,
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr,
-        c_ptr, c_ptr,
+        c_ptr, c_ptr, c_ptr, c_ptr,
         c_ptr]),
     "wgkv_gate_scores": (ctypes.c_int, [
         c_ptr, c_i64, c_i64, c_i64,

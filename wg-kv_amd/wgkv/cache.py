@@ -57,6 +57,21 @@ class DualCache:
         self.local_region_starts = ((torch.arange(L, **i32)[:, None] * H + torch.arange(H, **i32)[None, :]) * W)
         self.local_pre_key = (torch.empty(L, H, W, head_dim, dtype=dtype, device=device)
                               if getattr(config, "g_defer", False) else None)
+        if getattr(config, "snapkv_enabled", False):  # reference :1249-1261
+            if getattr(config, "use_quest", False):
+                raise AssertionError("SnapKV and QUEST are exclusive")
+            if not (config.snapkv_max_cached_tokens > 0 and 0.0 < config.snapkv_evict_ratio <= 1.0
+                    and config.snapkv_kernel_size % 2 == 1):
+                raise AssertionError("invalid SnapKV settings")
+            self.snapkv_query_buffer = torch.empty(L, config.snapkv_window_size, config.num_attention_heads,
+                                                   head_dim, dtype=dtype, device=device)
+            self.snapkv_query_length = 0
+            self.snapkv_query_ptr = 0
+            self.snapkv_evict_count = 0
+            # the released pages, in release order, and their count -- on the device,
+            # where the promotion kernel takes pages from the end of the list
+            self.free_block_ids_dev = torch.zeros(self.total_blocks, **i32)
+            self.free_count_dev = torch.zeros(1, **i32)
         if getattr(config, "use_quest", False):  # page key bounds (reference :1232-1240)
             self.quest_block_key_min = torch.empty(self.total_blocks, head_dim, dtype=dtype, device=device)
             self.quest_block_key_max = torch.empty(self.total_blocks, head_dim, dtype=dtype, device=device)
@@ -89,6 +104,13 @@ class DualCache:
             self.local_length += 1
         else:
             self.local_ptr = (self.local_ptr + 1) % self.local_window_size
+
+    @property
+    def free_block_ids(self):
+        """SnapKV's released-page list (a host copy; the device list is
+        ``free_block_ids_dev[:free_count_dev]``)."""
+        n = int(self.free_count_dev.item())
+        return self.free_block_ids_dev[:n].tolist()
 
     @property
     def next_free_block(self):

@@ -10,9 +10,9 @@ HIP library (kernels (1)-(4)).  ``self`` needs ``config``, ``layer_idx``,
 (and ``g_predictors`` when the gate is learned).
 
 Only inference (gating_mode 3) is on the hot path.  Of the comparison
-baselines, QUEST page selection (``use_quest``) runs on the same page tables
-and decode kernel; the training modes, DuoAttention, AdaEA and SnapKV are
-outside it and raise NotImplementedError.
+baselines, QUEST page selection (``use_quest``) and SnapKV eviction
+(``snapkv_enabled``) run on the same page tables and kernels; the training
+modes, DuoAttention and AdaEA are outside it and raise NotImplementedError.
 """
 from dataclasses import dataclass, field
 from typing import List, Optional
@@ -55,6 +55,10 @@ class WGKVConfig:
     use_quest: bool = False
     quest_token_budget: Optional[int] = None
     snapkv_enabled: bool = False
+    snapkv_max_cached_tokens: int = -1
+    snapkv_evict_ratio: float = 0.0
+    snapkv_window_size: int = 256
+    snapkv_kernel_size: int = 5
     check_capacity: bool = True  # read the device status after cache writes (a host sync)
 
     def __post_init__(self):
@@ -71,6 +75,82 @@ def get_random_g_scores(self, batch_size, kv_seq_len, device):
     """src/modeling_layers.py:1160-1166: 1 where U[0,1) >= random_sparsity."""
     r = torch.rand(batch_size, self.config.num_key_value_heads, kv_seq_len, dtype=torch.bfloat16, device=device)
     return (r >= self.config.random_sparsity).to(torch.bfloat16)
+
+
+def snapkv_record_queries(self, past_key_value, query_states):
+    """src/modeling_layers.py:579-592: keep the last snapkv_window_size
+    queries of each layer (the prompt's tail at prefill, one per decode step)."""
+    c = past_key_value
+    win = self.config.snapkv_window_size
+    q_len = query_states.shape[2]
+    if q_len > 1:
+        take = min(win, q_len)
+        c.snapkv_query_buffer[self.layer_idx, :take] = query_states[0, :, -take:, :].transpose(0, 1)
+        if self.layer_idx == self.config.num_hidden_layers - 1:
+            c.snapkv_query_length = take
+            c.snapkv_query_ptr = take % win
+    else:
+        c.snapkv_query_buffer[self.layer_idx, c.snapkv_query_ptr] = query_states[0, :, 0, :]
+        if self.layer_idx == self.config.num_hidden_layers - 1:
+            c.snapkv_query_length = min(win, c.snapkv_query_length + 1)
+            c.snapkv_query_ptr = (c.snapkv_query_ptr + 1) % win
+
+
+@torch.no_grad()
+def snapkv_evict(self, past_key_value, device, local_blocks_per_head):
+    """src/modeling_layers.py:595-671, on the device: per (layer, KV head),
+    score the global tokens by the window queries' attention (softmax in
+    fp32, max over the grouped heads, mean over the window, max-pooled),
+    drop the int(len * ratio) lowest (equal scores: lower position first),
+    pack the kept tokens into the head's first pages, release the rest to the
+    free list and reset their table slots.  The products are fp32 (the
+    reference multiplies in bf16)."""
+    import torch.nn.functional as F
+    c = past_key_value
+    cfg = self.config
+    if c.snapkv_query_length != cfg.snapkv_window_size:
+        raise AssertionError("SnapKV eviction needs a full query window")
+    P, D = c.block_size, c.head_dim
+    H, L = c.num_kv_heads, c.num_layers
+    G = cfg.num_attention_heads // cfg.num_key_value_heads
+    win, ksz = cfg.snapkv_window_size, cfg.snapkv_kernel_size
+    lb = local_blocks_per_head
+    lengths = c.global_lengths.cpu()
+    free_n = int(c.free_count_dev.item())
+    offs = torch.arange(P, dtype=torch.int64, device=device)
+    for l in range(L):
+        qw = c.snapkv_query_buffer[l].view(win, H, G, D).permute(1, 2, 0, 3).float()  # (H, G, win, D)
+        for h in range(H):
+            n = int(lengths[l, h])
+            n_evict = int(n * cfg.snapkv_evict_ratio)
+            if n_evict == 0:
+                continue
+            pages = (n + P - 1) // P
+            ids = c.block_table[l, h, lb:lb + pages].long()
+            linear = (ids[:, None] * P + offs[None, :]).reshape(-1)[:n]
+            keys = c.block_pool_k[linear].float()
+            attn = torch.softmax((qw[h] @ keys.T) * self.scaling, dim=-1)          # (G, win, n)
+            score = F.max_pool1d(attn.amax(dim=0).mean(dim=0).view(1, 1, -1), kernel_size=ksz, stride=1,
+                                 padding=ksz // 2).view(-1)
+            evict = torch.sort(score, stable=True).indices[:n_evict]
+            keep_mask = torch.ones(n, dtype=torch.bool, device=device)
+            keep_mask[evict] = False
+            keep = torch.nonzero(keep_mask).flatten()
+            kept = n - n_evict
+            new_pages = (kept + P - 1) // P
+            if kept > 0:
+                dst = linear[:kept]
+                kk = c.block_pool_k[linear[keep]]
+                vv = c.block_pool_v[linear[keep]]
+                c.block_pool_k[dst] = kk
+                c.block_pool_v[dst] = vv
+            if new_pages < pages:
+                freed = c.block_table[l, h, lb + new_pages:lb + pages].clone()
+                c.block_table[l, h, lb + new_pages:lb + pages] = c.total_blocks - 1
+                c.free_block_ids_dev[free_n:free_n + freed.numel()] = freed
+                free_n += freed.numel()
+            c.global_lengths[l, h] = kept
+    c.free_count_dev.fill_(free_n)
 
 
 def refresh_local_is_global(self, past_key_value, device):
@@ -198,10 +278,21 @@ def self_attn_forward_patch_inference(self, past_key_value, input_shape, query_s
         # with device_ring the ring-full condition is evaluated on the device
         migrate_local_kv_to_global(self, past_key_value, device, lbph)
     if is_prefilling:
-        return self.prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
-                                    batch_size, q_seq_len, device, g_mask, lbph)
-    return self.decode_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
-                               device, g_mask, lbph)
+        out = self.prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
+                                   batch_size, q_seq_len, device, g_mask, lbph)
+    else:
+        out = self.decode_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
+                                  device, g_mask, lbph)
+    if self.config.snapkv_enabled:  # :1500-1507
+        c = past_key_value
+        if c.device_ring:
+            raise AssertionError("SnapKV eviction is decided on the host; it cannot run with device_ring")
+        snapkv_record_queries(self, c, query_states)
+        if (self.layer_idx == self.config.num_hidden_layers - 1 and
+                int(c.global_lengths.sum().item()) > self.config.snapkv_max_cached_tokens):
+            c.snapkv_evict_count += 1
+            snapkv_evict(self, c, device, lbph)
+    return out
 
 
 def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, input_shape, query_states,
@@ -214,8 +305,6 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
         raise NotImplementedError("only inference (gating_mode 3) is on the MI355X path")
     if cfg.use_duo_attn or cfg.use_adaea:
         raise NotImplementedError("DuoAttention / AdaEA baselines are outside the hot path")
-    if cfg.snapkv_enabled:
-        raise NotImplementedError("SnapKV eviction is not built on the MI355X path")
     kv_seq_len = key_states.size(2)
     g_scores = None
     g_mask = None

@@ -217,6 +217,7 @@ def decode_append(cache, layer, key=None, value=None, g_mask=None, pre_key=None,
             _ptr(cache.global_lengths), _ptr(cache.local_is_global.view(torch.uint8)), _ptr(cache.local_pre_key),
             _ptr(cache.next_free_block_dev), _ptr(cache_seqlens), _ptr(cache.status),
             _ptr(getattr(cache, "quest_block_key_min", None)), _ptr(getattr(cache, "quest_block_key_max", None)),
+            _ptr(getattr(cache, "free_block_ids_dev", None)), _ptr(getattr(cache, "free_count_dev", None)),
             _lib.stream_handle(cache.block_pool_k.device))
     if getattr(cache, "device_ring", False):
         st = L.wgkv_decode_append_ring(*head, _ptr(cache.ring_state), int(advance), int(migrate), int(write), *tail)
