@@ -47,6 +47,11 @@ def parse():
     p.add_argument("--e2e-layers", type=int, default=32)
     p.add_argument("--e2e-admit", type=float, default=0.30)
     p.add_argument("--e2e-model", choices=["llama3-8b", "qwen3-8b"], default="llama3-8b")
+    p.add_argument("--e2e-profile", choices=["rms_linear_attn", "linear_attn", "attn", "wrapper", "kernel",
+                                             "predictor"], default=None,
+                   help="with --e2e: one more eager run per mode that times attention (at this granularity), "
+                        "MLP and LM head per phase, as the reference's --profile_attn_mlp --attn_granularity")
+    p.add_argument("--e2e-profile-steps", type=int, default=32)
     p.add_argument("--traffic-probe", action="store_true",
                    help="run only a 1 GiB torch copy x5 and the config-3 decode x5, for rocprofv3 --pmc "
                         "FETCH_SIZE / WRITE_SIZE passes (the copy calibrates the counters)")
@@ -390,6 +395,8 @@ def e2e_section(args):
            "data": "synthetic: random-init bf16 weights, uniform random token ids"}
     log("calibrating the gates")
     e2e.calibrate_gates(model, ids, args.e2e_admit)
+    # pass-through (phase "warmup") until a run switches them on; graph runs never do
+    timers = e2e.install_timing(model, args.e2e_profile) if args.e2e_profile else None
     for name, gated in (("gated", True), ("full", False)):
         model.cfg.use_baseline = not gated
         # the gated pool holds the expected admitted share with margin; the full pool every token
@@ -409,6 +416,17 @@ def e2e_section(args):
                      "model_gib": round(r.model_mib / 1024, 2), "kv_cache_gib": round(r.kv_mib / 1024, 2),
                      "first_tokens": r.tokens[:8]}
         log(f"{name}: {out[name]}")
+        if timers is not None:
+            log(f"{name}: eager run timing {args.e2e_profile}, MLP and LM head per phase")
+            for key in timers.ms:
+                timers.ms[key] = 0.0
+            rp = e2e.run(model, ids, args.e2e_profile_steps, progress=log, timers=timers)
+            torch.cuda.empty_cache()
+            out[name]["profile"] = {"attn_granularity": args.e2e_profile, "decode_steps": args.e2e_profile_steps,
+                                    "eager_prefill_ms": round(rp.prefill_ms, 1),
+                                    "eager_tpot_ms": round(sum(rp.decode_ms) / len(rp.decode_ms), 3),
+                                    **timers.report()}
+            log(f"{name}: {out[name]['profile']}")
     out["gated_vs_full"] = {"prefill_speedup": round(out["full"]["prefill_ms"] / out["gated"]["prefill_ms"], 3),
                             "decode_speedup": round(out["full"]["tpot_ms"] / out["gated"]["tpot_ms"], 3),
                             "kv_ratio": round(out["gated"]["kv_cache_gib"] / out["full"]["kv_cache_gib"], 3)}

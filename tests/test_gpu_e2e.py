@@ -125,3 +125,27 @@ def test_graph_decode_matches_eager(gated):
         assert cb.ring_state.tolist() == [cb.local_ptr, cb.local_length]
     assert torch.equal(ca.global_lengths, cb.global_lengths)
     assert ca.local_ptr == cb.local_ptr and ca.local_length == cb.local_length
+
+
+@pytest.mark.parametrize("granularity", ["rms_linear_attn", "kernel", "predictor"])
+def test_timed_run_matches_untimed(granularity):
+    """With the per-granularity timers installed (profiling.py
+    --profile_attn_mlp), an eager run decodes the same tokens as without
+    them, and attention, MLP and LM head each accumulate time in both the
+    prefill and the decode phase (nothing in warm-up)."""
+    from wgkv import e2e
+    print(f"[e2e] timed run {granularity}", flush=True)
+    ids = torch.randint(0, 1000, (1, 640), generator=torch.Generator().manual_seed(4)).to(DEV)
+    m = tiny_model(True)
+    e2e.calibrate_gates(m, ids, 0.3, chunk=256)
+    plain = e2e.run(m, ids, steps=4, chunk=256, warmup_steps=1)
+    t = e2e.install_timing(m, granularity)
+    timed = e2e.run(m, ids, steps=4, chunk=256, warmup_steps=1, timers=t)
+    assert timed.tokens == plain.tokens
+    rep = t.report()
+    for ph in ("prefill", "decode"):
+        for part in ("attn", "mlp", "lm_head"):
+            assert rep[f"{ph}_{part}_ms"] > 0, (ph, part)
+    assert t.phase == "warmup"
+    with pytest.raises(ValueError):
+        e2e.run(m, ids, steps=1, chunk=256, graph=True, timers=t)

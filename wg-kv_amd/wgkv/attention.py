@@ -89,6 +89,7 @@ class LlamaAttention(nn.Module):
         self.prefill_wrapper = layers.prefill_wrapper
         self.decode_wrapper = layers.decode_wrapper
         self.prefill_kernel = ops.sparse_attn_func
+        self.chunk_prefill_kernel = ops.chunk_attend  # prompt chunks after the first (no reference counterpart)
         self.decode_kernel_handle = ops.paged_decode_attn_handle
         self.decode_kernel_executor = lambda func: func()
 

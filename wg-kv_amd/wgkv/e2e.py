@@ -60,10 +60,16 @@ class DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size)
         self.mlp = MLP(cfg.hidden_size, inter)
 
-    def forward(self, x, pos_emb, cache):
+    def rmsnorm_and_self_attn(self, x, pos_emb, cache):
+        """Input norm, attention, residual add and the post-attention norm
+        (src/modeling_llama.py:337-371): returns (residual, MLP input)."""
         h, _, _ = self.self_attn(3, self.input_layernorm(x), pos_emb, None, cache)
         x = x + h
-        return x + self.mlp(self.post_attention_layernorm(x))
+        return x, self.post_attention_layernorm(x)
+
+    def forward(self, x, pos_emb, cache):
+        residual, h = self.rmsnorm_and_self_attn(x, pos_emb, cache)
+        return residual + self.mlp(h)
 
 
 @dataclass
@@ -224,6 +230,82 @@ def calibrate_gates(model, ids, frac, chunk=4096):
     del cache
 
 
+GRANULARITIES = ("rms_linear_attn", "linear_attn", "attn", "wrapper", "kernel", "predictor")
+
+
+class PhaseTimers:
+    """Accumulated attention / MLP / LM-head time (ms) per phase, as
+    profiling.py's ElapsedTimeTracker / TimingPhase pair (:8-13, :241-268).
+    ``phase`` is "warmup", "prefill" or "decode"; nothing is recorded in
+    the warm-up phase."""
+
+    def __init__(self, granularity):
+        self.granularity = granularity
+        self.phase = "warmup"
+        self.ms = {(part, ph): 0.0 for part in ("attn", "mlp", "lm_head") for ph in ("prefill", "decode")}
+
+    def timed(self, part, func):
+        """func wrapped as profiling.py's get_func_with_timing (:186-194):
+        synchronise, record, call, record, synchronise (measure_time,
+        :113-120), and add the time to the tracker of the current phase."""
+        events = []
+
+        def wrapper(*args, **kwargs):
+            if self.phase not in ("prefill", "decode"):
+                return func(*args, **kwargs)
+            if not events:
+                events.extend(torch.cuda.Event(enable_timing=True) for _ in range(2))
+            start, end = events
+            torch.cuda.synchronize()
+            start.record()
+            out = func(*args, **kwargs)
+            end.record()
+            torch.cuda.synchronize()
+            self.ms[(part, self.phase)] += start.elapsed_time(end)
+            return out
+        return wrapper
+
+    def report(self):
+        """The lines profiling.py prints for --profile_attn_mlp (:411-417)."""
+        return {f"{ph}_{part}_ms": round(v, 3) for (part, ph), v in self.ms.items()}
+
+
+def install_timing(model, granularity="kernel"):
+    """Wrap, in every layer, the function that the reference's
+    ``--attn_granularity`` names (profiling.py:273-334) plus the MLP and the
+    LM head (:336-343), each with a HIP-event timer; returns the timers.
+    ``kernel`` also wraps ``chunk_prefill_kernel``, the attention of prompt
+    chunks after the first; ``predictor`` wraps the gate's fused
+    score-and-admit call, which is what this build's layer calls for the
+    predictor.  The timers synchronise
+    around every call, so they are for eager runs (not captured graphs)."""
+    if granularity not in GRANULARITIES:
+        raise ValueError(f"granularity must be one of {GRANULARITIES}")
+    t = PhaseTimers(granularity)
+    for layer in model.layers:
+        a = layer.self_attn
+        if granularity == "rms_linear_attn":
+            layer.rmsnorm_and_self_attn = t.timed("attn", layer.rmsnorm_and_self_attn)
+        elif granularity == "linear_attn":
+            a.forward = t.timed("attn", a.forward)
+        elif granularity == "attn":
+            a.self_attn_forward_patch = t.timed("attn", a.self_attn_forward_patch)
+        elif granularity == "wrapper":
+            a.prefill_wrapper = t.timed("attn", a.prefill_wrapper)
+            a.decode_wrapper = t.timed("attn", a.decode_wrapper)
+        elif granularity == "kernel":
+            a.prefill_kernel = t.timed("attn", a.prefill_kernel)
+            a.chunk_prefill_kernel = t.timed("attn", a.chunk_prefill_kernel)
+            a.decode_kernel_executor = t.timed("attn", a.decode_kernel_executor)
+        else:
+            gp = getattr(a, "g_predictors", None)
+            if gp is not None:
+                gp.scores_and_mask = t.timed("attn", gp.scores_and_mask)
+        layer.mlp.forward = t.timed("mlp", layer.mlp.forward)
+    model.lm_head.forward = t.timed("lm_head", model.lm_head.forward)
+    return t
+
+
 @dataclass
 class E2EResult:
     prompt_length: int
@@ -249,16 +331,21 @@ def kv_cache_mib(cache):
 
 
 @torch.no_grad()
-def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=False):
+def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=False, timers=None):
     """Chunked prefill of ids (1, S), then ``steps`` greedy decode steps, each
     timed with HIP events on the launch stream after a synchronisation (as
     profiling.py's measure_time, :113-120); with ``graph`` every step is a
-    replay of a captured HIP graph (GraphDecoder)."""
+    replay of a captured HIP graph (GraphDecoder).  ``timers`` (from
+    ``install_timing``) is switched to the phase being run."""
+    if timers is not None and graph:
+        raise ValueError("per-granularity timers synchronise around each call; use an eager run")
+    phase = (lambda name: setattr(timers, "phase", name)) if timers is not None else (lambda name: None)
     S = ids.shape[1]
     cache = DualCache()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
+    phase("prefill")
     ev0.record()
     logits = None
     for c0 in range(0, S, chunk):
@@ -277,6 +364,7 @@ def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=Fals
         gd = GraphDecoder(model, cache, tok, pos)
         warmup_steps = max(0, warmup_steps - gd.warm_tokens)
     for i in range(warmup_steps + steps):
+        phase("decode" if i >= warmup_steps else "warmup")
         torch.cuda.synchronize()
         ev0.record()
         if gd is not None:
@@ -290,6 +378,7 @@ def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=Fals
             res.decode_ms.append(ev0.elapsed_time(ev1))
             res.tokens.append(int(tok.item()))
         pos += 1
+    phase("warmup")
     cache.raise_if_failed("decode")
     res.tokens_after = avg_tokens_in_cache(cache, model)
     res.model_mib = sum(p.numel() * p.element_size() for p in model.parameters()) / (1024 * 1024)

@@ -202,9 +202,13 @@ def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, val
             raise AssertionError(f"chunked prefill needs prefill_length >= W, chunk >= W and a 64-aligned start "
                                  f"(prefill_length={c0}, chunk={q_seq_len}, W={W})")
         before = c.global_lengths[self.layer_idx].clone() if self.config.use_quest else None
-        out = ops.chunk_prefill(c, self.layer_idx, query_states[0].transpose(0, 1), key_states[0].transpose(0, 1),
-                                value_states[0].transpose(0, 1), g_mask[0], c0, self.scaling,
-                                pre_key=pre_key[0].transpose(0, 1) if (defer and pre_key is not None) else None)
+        step = ops.ChunkStep(c, self.layer_idx, query_states[0].transpose(0, 1), key_states[0].transpose(0, 1),
+                             value_states[0].transpose(0, 1), g_mask[0], c0, self.scaling,
+                             pre_key=pre_key[0].transpose(0, 1) if (defer and pre_key is not None) else None)
+        step.admit()
+        # the chunk's attention kernel behind its own swap point (the one-shot path's is prefill_kernel)
+        out = getattr(self, "chunk_prefill_kernel", ops.chunk_attend)(step)
+        step.ring()
         _layer_cache_check(self, c, f"prefill_wrapper chunk at {c0} (layer {self.layer_idx})")
         if self.config.use_quest:
             ops.quest_update_bounds(c, self.layer_idx, from_lengths=before)

@@ -367,6 +367,12 @@ def chunk_prefill(cache, layer, q, key, value, g_mask, chunk_start, softmax_scal
     return out
 
 
+def chunk_attend(step):
+    """The attention kernel of an admitted chunk (``ChunkStep.attend``): the
+    default ``chunk_prefill_kernel`` swap point of the layer."""
+    return step.attend()
+
+
 # ---------------------------------------------------------------------------
 # QUEST page selection (the reference's comparison baseline) over kernel (2)
 # ---------------------------------------------------------------------------
