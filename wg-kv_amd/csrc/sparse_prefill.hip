@@ -15,8 +15,15 @@
 // S^T = K Q^T on v_mfma_f32_16x16x32_bf16 (K from LDS as the A operand, the
 // wave's queries held as the B operand), which leaves each lane with 4
 // consecutive keys of one query row: after the online softmax those
-// probabilities are already the B operand of O^T = V^T P^T, with V^T read
-// from a transposed LDS tile.  Softmax runs in the log2 domain in fp32.
+// probabilities are already the B operand of O^T = V^T P^T, with the V^T
+// operand read from the row-major V tile by LDS transpose reads
+// (ds_read_b64_tr_b16).  Softmax runs in the log2 domain in fp32.
+//
+// K and V tiles go from global memory straight into LDS
+// (global_load_lds_dwordx4: each wave instruction fills 1 KB of LDS, lane i
+// at byte 16*i), so a tile is stored unpadded, D*2 bytes per key, and bank
+// conflicts are avoided by permuting the 16-byte slices of each key row:
+// slice c of row r sits at slice c ^ (r & 7) in K and c ^ 2*(r & 3) in V.
 #include "wgkv_common.h"
 
 namespace {
@@ -39,14 +46,20 @@ __device__ __forceinline__ float xor32_max(float x) {
   return fmax_ieee(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-__device__ __forceinline__ float xor16_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef short v8i16_t __attribute__((ext_vector_type(8)));
+
+// global_load_lds_dwordx4: the 16 bytes at g go to LDS at lds + 16 * lane
+// (lds must be the same in every lane)
+__device__ __forceinline__ void lds_dma16(const uint16_t* g, uint16_t* lds) {
+  __builtin_amdgcn_global_load_lds(g, lds, 16, 0, 0);
 }
-__device__ __forceinline__ float xor32_sum(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+
+// ds_read_b64_tr_b16: see the V^T operand read in the kernel for the layout
+__device__ __forceinline__ v4i16_t lds_read_tr16(const uint16_t* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16_t __attribute__((address_space(3)))*)(p));
 }
+
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -83,18 +96,27 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   constexpr int KS = D / 32;       // k-steps over head_dim
   constexpr int DT = D / 16;       // 16-wide d tiles
   constexpr int CH = D / 8;        // 16-byte slices per row
-  constexpr int LDK = D + 8;       // K tile row stride (elements)
-  constexpr int LDV = kBlk + 4;    // V^T tile row stride (elements)
-  constexpr int KITEMS = kBlk * CH;         // (row, slice) items of a K tile
-  constexpr int VITEMS = (kBlk / 2) * CH;   // (key pair, slice) items of a V tile
-  __shared__ __attribute__((aligned(16))) uint16_t sKb[2][kBlk * LDK];
-  __shared__ __attribute__((aligned(16))) uint16_t sVtb[2][D * LDV];
+  constexpr int NW = 2 * HPW;      // waves
+  constexpr int RPB = 64 / CH;     // key rows per 1 KB LDS block (one wave load instruction)
+  constexpr int NBLK = kBlk / RPB; // 1 KB blocks per K (or V) tile
+  constexpr int KPT = NBLK / NW;   // blocks per wave and tile
+  static_assert(NBLK % NW == 0, "every wave loads whole 1 KB blocks");
+  // double buffers as four distinct LDS objects: the DMA into one buffer
+  // provably does not alias the reads of the other, so no wait for the
+  // in-flight tile is placed before them
+  __shared__ __attribute__((aligned(16))) uint16_t sK0[kBlk * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sK1[kBlk * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV0[kBlk * D];
+  __shared__ __attribute__((aligned(16))) uint16_t sV1[kBlk * D];
+  // block offsets are read-only metadata: scalar loads
+  const int32_t __attribute__((address_space(4)))* bofs =
+      (const int32_t __attribute__((address_space(4)))*)a.block_offset;
 
   const int r = blockIdx.x;
   const int bh = blockIdx.y;
   const int b = bh / a.Hkv, h = bh - b * a.Hkv;
   const int t = threadIdx.x;
-  const int lane = t & 63, wid = t >> 6;
+  const int lane = t & 63, wid = __builtin_amdgcn_readfirstlane(t >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int hq = h * a.G + blockIdx.z * HPW + (wid >> 1);
   const int lrow0 = r * kBlk + (wid & 1) * 32;   // first query row of this wave (tensor row)
@@ -112,7 +134,10 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   }
 
   float m_run[2] = {-INFINITY, -INFINITY};
-  float l_part[2] = {0.f, 0.f};
+  // row sums of the (bf16) probabilities, accumulated by the matrix core as
+  // ones . P^T: every entry of lsum[rt] holds the sum of query row rt*16+n
+  f32x4_t lsum[2] = {(f32x4_t){0.f, 0.f, 0.f, 0.f}, (f32x4_t){0.f, 0.f, 0.f, 0.f}};
+  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
   f32x4_t o[DT][2];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt)
@@ -135,30 +160,19 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
   const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
 
-  // Tile loading: K items are (row, 16-byte slice), V items are (key pair,
-  // slice); thread t takes items t, t+NT, ...  The keys of the next tile are
-  // looked up one tile ahead and its rows loaded into registers one tile
-  // ahead, so both latencies overlap the current tile's arithmetic.
-  constexpr int KPT = (KITEMS + NT - 1) / NT;
-  constexpr int VPT = (VITEMS + NT - 1) / NT;
-  constexpr bool KFULL = KITEMS % NT == 0;  // every thread has all its K items
-  constexpr bool VFULL = VITEMS % NT == 0;
-  int krow[KPT], kcol[KPT], vkp[VPT], vcol[VPT];
+  // Tile loading: wave w fills the 1 KB blocks w, w+NW, ... of the K and of
+  // the V tile; in block q, lane i loads key row q*RPB + i/CH, slice
+  // position i%CH, i.e. global slice (i%CH) ^ (row & 7) for K and
+  // (i%CH) ^ 2*(row & 3) for V.  The keys of the next tile are looked up one
+  // tile ahead and its rows loaded one tile ahead, so both latencies overlap
+  // the current tile's arithmetic.
+  int krow[KPT], kcolK[KPT], kcolV[KPT];
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int e = t + i * NT;
-    krow[i] = e < KITEMS ? e / CH : -1;
-    kcol[i] = e % CH;
-  }
-#pragma unroll
-  for (int i = 0; i < VPT; ++i) {
-    const int e = t + i * NT;
-    vkp[i] = e < VITEMS ? e % (kBlk / 2) : -1;
-    {
-      // slices x and x^1 (the two half-waves) land 2 slices apart: bank-disjoint V^T writes
-      const int x = e / (kBlk / 2);
-      vcol[i] = (x & ~3) | ((x & 1) << 1) | ((x >> 1) & 1);
-    }
+    const int row = (wid + i * NW) * RPB + lane / CH;
+    krow[i] = row;
+    kcolK[i] = (lane % CH) ^ (row & 7);
+    kcolV[i] = (lane % CH) ^ ((row & 3) << 1);
   }
   // A tile's rows are fetched in two stages.  Two tiles ahead, tile_idx
   // loads the indirections -- the admitted columns' positions or, in chunked
@@ -168,12 +182,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   // the row loads means no wait for an index also waits for the rows issued
   // before it (memory counters retire in order).
   struct Idx {
-    int k[KPT];     // per K item: column position / page id / band position
-    int v[VPT][2];  // per V item (two keys)
-  };
-  struct Regs {
-    u32x4_t k[KPT];
-    u32x4_t v[VPT][2];
+    int k[KPT];     // per item: column position / page id / band position
   };
   const int32_t* bt_h = CHUNK ? a.bt + (int64_t)h * a.bt_sh : nullptr;
   auto tile_idx = [&](int tl, Idx& ix) {
@@ -181,24 +190,13 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
       const int nval = min(kBlk, nv - tl * kBlk);
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
-        const int j = tl * kBlk + min(max(krow[i], 0), nval - 1);
+        const int j = tl * kBlk + min(krow[i], nval - 1);
         ix.k[i] = CHUNK ? bt_h[j / a.page] : cidx[j];
       }
-#pragma unroll
-      for (int i = 0; i < VPT; ++i)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const int j = tl * kBlk + min(2 * max(vkp[i], 0) + u, nval - 1);
-          ix.v[i][u] = CHUNK ? bt_h[j / a.page] : cidx[j];
-        }
     } else {
-      const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : a.block_offset[r * a.bo_width + (tl - n_vtiles)];
+      const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : bofs[r * a.bo_width + (tl - n_vtiles)];
 #pragma unroll
-      for (int i = 0; i < KPT; ++i) ix.k[i] = min(b0 + max(krow[i], 0), a.S - 1);
-#pragma unroll
-      for (int i = 0; i < VPT; ++i)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) ix.v[i][u] = min(b0 + 2 * max(vkp[i], 0) + u, a.S - 1);
+      for (int i = 0; i < KPT; ++i) ix.k[i] = min(b0 + krow[i], a.S - 1);
     }
   };
   // row start of key x of tile tl in the K (or V) source
@@ -214,60 +212,55 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     if (CHUNK && x < a.c0) return pool + (a.ring_row0 + (int64_t)h * a.W + (x - (a.c0 - a.W))) * D;
     return tensor_base + (int64_t)(x - (CHUNK ? a.c0 : 0)) * a.kv_ss;
   };
-  auto tile_load = [&](int tl, const Idx& ix, Regs& rg) {
+  auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) {
     const bool vertical = tl < n_vtiles;
     const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
 #pragma unroll
-    for (int i = 0; i < KPT; ++i)
-      if (KFULL || krow[i] >= 0) {
-        const uint16_t* row = row_ptr(tl, vertical, ix.k[i], min(krow[i], nval - 1), kbase, a.pool_k);
-        rg.k[i] = *(const u32x4_t*)(row + kcol[i] * 8);
-      }
-#pragma unroll
-    for (int i = 0; i < VPT; ++i)
-      if (VFULL || vkp[i] >= 0)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const uint16_t* row = row_ptr(tl, vertical, ix.v[i][u], min(2 * vkp[i] + u, nval - 1), vbase, a.pool_v);
-          rg.v[i][u] = *(const u32x4_t*)(row + vcol[i] * 8);
-        }
+    for (int i = 0; i < KPT; ++i) {
+      const int kt = min(krow[i], nval - 1);
+      const int blk = (wid + i * NW) * 512;  // element offset of this wave's block (1 KB)
+      lds_dma16(row_ptr(tl, vertical, ix.k[i], kt, kbase, a.pool_k) + kcolK[i] * 8, dK + blk);
+      lds_dma16(row_ptr(tl, vertical, ix.k[i], kt, vbase, a.pool_v) + kcolV[i] * 8, dV + blk);
+    }
   };
+  // Per-lane LDS element offsets of the fragments (the slice permutations
+  // above, resolved once): K row kt*16+n, slice j*4+g sits at slice
+  // ((j ^ nbit) * 4 + (g ^ (n & 3))) with nbit = (n >> 2) & 1; the transpose
+  // read of lane n in group g (row 4g + n/4 + 16u + 32s, d slice 2*dt + (n&3)/2,
+  // half n&1) finds its slice at 2*(dt ^ ((n >> 2) & 3)) + (n&3)/2.
+  const int nbit = (n >> 2) & 1;
+  int koff[KS];
+#pragma unroll
+  for (int j = 0; j < KS; ++j) koff[j] = n * D + ((j ^ nbit) * 4 + (g ^ (n & 3))) * 8;
+  const int vm = (n >> 2) & 3;
+  int voff[4];
+#pragma unroll
+  for (int dq = 0; dq < 4; ++dq)
+    voff[dq] = (4 * g + (n >> 2)) * D + (2 * (dq ^ vm) + ((n & 3) >> 1)) * 8 + (n & 1) * 4;
 
   Idx idx_next;
-  Regs regs;
   if (ntiles > 0) {
     Idx i0;
     tile_idx(0, i0);
-    tile_load(0, i0, regs);
+    tile_load(0, i0, sK0, sV0);
     if (ntiles > 1) tile_idx(1, idx_next);
   }
 
-  for (int tile = 0; tile < ntiles; ++tile) {
+  // one 64-key tile: K and V of the tile in (sK, sV); the next tile's rows go to (nK, nV)
+  auto step = [&](int tile, const uint16_t* sK, const uint16_t* sV, uint16_t* nK,
+                  uint16_t* nV) __attribute__((always_inline)) {
     const bool vert = tile < n_vtiles;
     int band0 = 0, nvalid = kBlk;
     if (vert) nvalid = min(kBlk, nv - tile * kBlk);
-    else band0 = CHUNK ? band_start + (tile - n_vtiles) * kBlk : a.block_offset[r * a.bo_width + (tile - n_vtiles)];
+    else band0 = CHUNK ? band_start + (tile - n_vtiles) * kBlk : bofs[r * a.bo_width + (tile - n_vtiles)];
 
-    uint16_t* sK = sKb[tile & 1];
-    uint16_t* sVt = sVtb[tile & 1];
-#pragma unroll
-    for (int i = 0; i < KPT; ++i)
-      if (KFULL || krow[i] >= 0) *(u32x4_t*)(&sK[krow[i] * LDK + kcol[i] * 8]) = regs.k[i];
-#pragma unroll
-    for (int i = 0; i < VPT; ++i) {
-      if (!VFULL && vkp[i] < 0) continue;
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t lo = (regs.v[i][0][w] & 0xffffu) | (regs.v[i][1][w] << 16);
-        const uint32_t hi = (regs.v[i][0][w] >> 16) | (regs.v[i][1][w] & 0xffff0000u);
-        *(uint32_t*)(&sVt[(vcol[i] * 8 + 2 * w) * LDV + 2 * vkp[i]]) = lo;
-        *(uint32_t*)(&sVt[(vcol[i] * 8 + 2 * w + 1) * LDV + 2 * vkp[i]]) = hi;
-      }
-    }
+    // this wave's loads of the tile (and of the next tile's indices) have
+    // landed; the barrier publishes every wave's and frees the other buffer
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
-    // the next tile's rows stream in under this tile's arithmetic
+    // the next tile's rows stream into the other buffer under this tile's arithmetic
     if (tile + 1 < ntiles) {
-      tile_load(tile + 1, idx_next, regs);
+      tile_load(tile + 1, idx_next, nK, nV);
       if (tile + 2 < ntiles) tile_idx(tile + 2, idx_next);
     }
 
@@ -284,7 +277,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
       bf16x8_t kf[4];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        kf[kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[(kt * 16 + n) * LDK + (j * 4 + g) * 8]));
+        kf[kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[j]]));
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
@@ -330,7 +323,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
         const float mnew = need ? mxs[rt] : m_run[rt];
         const float alpha = mnew == m_run[rt] ? 1.f : fast_exp2(m_run[rt] - mnew);
         m_run[rt] = mnew;
-        l_part[rt] *= alpha;
+        lsum[rt] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
       }
@@ -346,7 +339,6 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
         for (int i = 0; i < 4; i += 2) {
           const float p0 = fast_exp2(fmaf(sc[kt][rt][i], a.scale_log2, -mref));
           const float p1 = fast_exp2(fmaf(sc[kt][rt][i + 1], a.scale_log2, -mref));
-          l_part[rt] += p0 + p1;
           pw[kt * 2 + i / 2] = pack_bf16x2(p0, p1);
         }
       // k-step s covers key tiles 2s (slots 0-3) and 2s+1 (slots 4-7)
@@ -357,28 +349,35 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
       }
     }
     // ---- O^T += V^T P^T ------------------------------------------------------
+    // The A operand (lane: d = dt*16 + n, keys 32s+4g+0..3 and 32s+16+4g+0..3,
+    // the key order of pb) comes from two transpose reads of the row-major V
+    // tile: within each 16-lane group, lane n addresses row kb + n/4 at column
+    // d0 + 4*(n%4), and receives V[kb+k][d0+n] for k = 0..3.
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint16_t* vt = &sVt[(dt * 16 + n) * LDV + s * 32 + 4 * g];
-        const uint64_t lo = *(const uint64_t*)vt;
-        const uint64_t hi = *(const uint64_t*)(vt + 16);
-        const u32x4_t w = (u32x4_t){(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-        const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, w);
+        const uint16_t* vrd = sV + voff[dt & 3] + (dt >> 2) * 64 + s * 32 * D;
+        const v4i16_t lo = lds_read_tr16(vrd);
+        const v4i16_t hi = lds_read_tr16(vrd + 16 * D);
+        const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
           o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[rt][s], o[dt][rt], 0, 0, 0);
       }
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rt][s], lsum[rt], 0, 0, 0);
     }
+  };
+  for (int tile = 0; tile < ntiles; tile += 2) {
+    step(tile, sK0, sV0, sK1, sV1);
+    if (tile + 1 < ntiles) step(tile + 1, sK1, sV1, sK0, sV0);
   }
 
   // ---- normalise and store: lane holds O[row rt*16+n][dt*16 + 4g + i] -------
 #pragma unroll
   for (int rt = 0; rt < 2; ++rt) {
-    float l = l_part[rt];
-    l = xor16_sum(l);
-    l = xor32_sum(l);
+    const float l = lsum[rt][0];
     const float inv = l > 0.f ? 1.f / l : 0.f;
     const int s = lrow0 + rt * 16 + n;
     if (s < nrows) {
@@ -403,20 +402,17 @@ hipError_t launch(const PrefillArgs& a, hipStream_t st, bool chunked) {
   return hipGetLastError();
 }
 
-// Query heads per workgroup: min(G, kHeadsPerWg)
-#ifndef WGKV_PREFILL_HPW
-#define WGKV_PREFILL_HPW 4
-#endif
-constexpr int kHeadsPerWg = WGKV_PREFILL_HPW;
+// Query heads per workgroup: min(G, 4)
+constexpr int kHeadsPerWg = 4;
 
 hipError_t launch_any(PrefillArgs& a, hipStream_t st, int head_dim, int G, bool chunked) {
   a.G = G;
   const int hpw = G < kHeadsPerWg ? G : kHeadsPerWg;
   if (head_dim == 128)
     return hpw == 1 ? launch<128, 1>(a, st, chunked) : hpw == 2 ? launch<128, 2>(a, st, chunked)
-         : hpw == 4 ? launch<128, 4>(a, st, chunked) : launch<128, 8>(a, st, chunked);
+                    : launch<128, 4>(a, st, chunked);
   return hpw == 1 ? launch<64, 1>(a, st, chunked) : hpw == 2 ? launch<64, 2>(a, st, chunked)
-       : hpw == 4 ? launch<64, 4>(a, st, chunked) : launch<64, 8>(a, st, chunked);
+                  : launch<64, 4>(a, st, chunked);
 }
 
 }  // namespace
