@@ -23,7 +23,7 @@
 // (global_load_lds_dwordx4: each wave instruction fills 1 KB of LDS, lane i
 // at byte 16*i), so a tile is stored unpadded, D*2 bytes per key, and bank
 // conflicts are avoided by permuting the 16-byte slices of each key row:
-// slice c of row r sits at slice c ^ (r & 7) in K and c ^ 2*(r & 3) in V.
+// slice c of row r sits at slice c ^ swz_k(r) in K and c ^ swz_v(r) in V.
 #include "wgkv_common.h"
 
 namespace {
@@ -60,6 +60,22 @@ __device__ __forceinline__ v4i16_t lds_read_tr16(const uint16_t* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((v4i16_t __attribute__((address_space(3)))*)(p));
 }
 
+
+// LDS slice permutations of the K and V tiles (16-byte slices, D*2-byte key
+// rows, no padding).  The LDS serves 256 bytes per clock: 16 lanes of a
+// 16-byte read or 32 lanes of an 8-byte transpose read.  K fragment reads
+// take one slice from each of 16 consecutive rows, so those rows must land
+// on 16 distinct slice positions modulo 256 bytes; a transpose read takes a
+// 32-byte slice pair from each of 8 consecutive rows.  The permutation only
+// uses the row bits that the 16-row and 32-row fragment offsets keep.
+template <int D>
+__device__ __forceinline__ int swz_k(int row) {
+  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+}
+template <int D>
+__device__ __forceinline__ int swz_v(int row) {
+  return D == 128 ? 2 * (row & 7) : 2 * ((row >> 1) & 3);
+}
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -162,8 +178,8 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
 
   // Tile loading: wave w fills the 1 KB blocks w, w+NW, ... of the K and of
   // the V tile; in block q, lane i loads key row q*RPB + i/CH, slice
-  // position i%CH, i.e. global slice (i%CH) ^ (row & 7) for K and
-  // (i%CH) ^ 2*(row & 3) for V.  The keys of the next tile are looked up one
+  // position i%CH, i.e. global slice (i%CH) ^ swz_k(row) for K and
+  // (i%CH) ^ swz_v(row) for V.  The keys of the next tile are looked up one
   // tile ahead and its rows loaded one tile ahead, so both latencies overlap
   // the current tile's arithmetic.
   int krow[KPT], kcolK[KPT], kcolV[KPT];
@@ -171,8 +187,8 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   for (int i = 0; i < KPT; ++i) {
     const int row = (wid + i * NW) * RPB + lane / CH;
     krow[i] = row;
-    kcolK[i] = (lane % CH) ^ (row & 7);
-    kcolV[i] = (lane % CH) ^ ((row & 3) << 1);
+    kcolK[i] = (lane % CH) ^ swz_k<D>(row);
+    kcolV[i] = (lane % CH) ^ swz_v<D>(row);
   }
   // A tile's rows are fetched in two stages.  Two tiles ahead, tile_idx
   // loads the indirections -- the admitted columns' positions or, in chunked
@@ -225,18 +241,17 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   };
   // Per-lane LDS element offsets of the fragments (the slice permutations
   // above, resolved once): K row kt*16+n, slice j*4+g sits at slice
-  // ((j ^ nbit) * 4 + (g ^ (n & 3))) with nbit = (n >> 2) & 1; the transpose
-  // read of lane n in group g (row 4g + n/4 + 16u + 32s, d slice 2*dt + (n&3)/2,
-  // half n&1) finds its slice at 2*(dt ^ ((n >> 2) & 3)) + (n&3)/2.
-  const int nbit = (n >> 2) & 1;
+  // (j*4+g) ^ swz_k(n); the transpose read of lane n in group g (row
+  // 4g + n/4 + 16u + 32s, d slice 2*dt + (n&3)/2, half n&1) finds its slice at
+  // (2*dt + (n&3)/2) ^ swz_v(4g + n/4).
   int koff[KS];
 #pragma unroll
-  for (int j = 0; j < KS; ++j) koff[j] = n * D + ((j ^ nbit) * 4 + (g ^ (n & 3))) * 8;
-  const int vm = (n >> 2) & 3;
-  int voff[4];
+  for (int j = 0; j < KS; ++j) koff[j] = n * D + ((j * 4 + g) ^ swz_k<D>(n)) * 8;
+  const int vrow = 4 * g + (n >> 2);
+  int voff[DT];
 #pragma unroll
-  for (int dq = 0; dq < 4; ++dq)
-    voff[dq] = (4 * g + (n >> 2)) * D + (2 * (dq ^ vm) + ((n & 3) >> 1)) * 8 + (n & 1) * 4;
+  for (int dt = 0; dt < DT; ++dt)
+    voff[dt] = vrow * D + ((2 * dt + ((n & 3) >> 1)) ^ swz_v<D>(vrow)) * 8 + (n & 1) * 4;
 
   Idx idx_next;
   if (ntiles > 0) {
@@ -357,7 +372,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     for (int s = 0; s < 2; ++s) {
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const uint16_t* vrd = sV + voff[dt & 3] + (dt >> 2) * 64 + s * 32 * D;
+        const uint16_t* vrd = sV + voff[dt] + s * 32 * D;
         const v4i16_t lo = lds_read_tr16(vrd);
         const v4i16_t hi = lds_read_tr16(vrd + 16 * D);
         const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
