@@ -6,7 +6,8 @@
 //   h  = act(W1[h] x + b1[h])                                        (inner)
 //   g  = sigmoid(w2[h] . h + b2[h]);  conv path: g = max(g, clamp_min)
 //   mask = g > threshold
-// One workgroup = 64 tokens of one (batch, KV head).  The normalised inputs
+// One workgroup = 64 tokens of one (batch, KV head), heads dealt across the
+// XCDs so each head's W1 stays in one L2.  The normalised inputs
 // go to LDS (fp32, rows padded for conflict-free 16-byte reads); the hidden
 // columns are dealt round-robin to the 4 waves in 16-column tiles, so W1[h]
 // is read once per workgroup; x @ W1^T runs on v_mfma_f32_16x16x4f32 with
@@ -55,36 +56,52 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
   __shared__ float xs[kTok * LDX];
   __shared__ float s_part[4][kTok];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int tile = blockIdx.x, bh = blockIdx.y;
+  // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by linear
+  // id, so taking (batch, head) = id mod B*H keeps each head's workgroups on
+  // few XCDs and its W1 resident in their L2
+  const int nbh = a.B * a.H;
+  const int lid = blockIdx.x + blockIdx.y * gridDim.x;
+  const int bh = lid % nbh, tile = lid / nbh;
   const int b = bh / a.H, h = bh - b * a.H;
   const int s0 = tile * kTok;
   const int D = a.D;
 
   // ---- normalised inputs -> LDS: wave w handles tokens w*16 .. w*16+15 ----
-  for (int tt = 0; tt < 16; ++tt) {
-    const int m = wid * 16 + tt;
-    const int s = min(s0 + m, a.S - 1);  // rows past S are computed and discarded
-    for (int i = 0; i < a.n_in; ++i) {
-      float v[2];
-      float sq = 0.f;
+  // Four tokens at a time: all their input loads are issued before the first
+  // reduction, so the load latency is paid four times per wave, not sixteen.
+  constexpr int kGroup = 4;
+  for (int tt0 = 0; tt0 < 16; tt0 += kGroup) {
+    float v[kGroup][3][2];
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int d = lane + e * 64;
-        v[e] = d < D ? load_in(a, i, b, h, s, d) : 0.f;
-        sq += v[e] * v[e];
-      }
-      float scale = 1.f;
-      if (a.rms) {
-        const float var = wave_sum(sq) / (float)D;
-        scale = 1.0f / sqrtf(var + 1e-6f);
-      }
+    for (int u = 0; u < kGroup; ++u) {
+      const int s = min(s0 + wid * 16 + tt0 + u, a.S - 1);  // rows past S are computed and discarded
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const int d = lane + e * 64;
-        if (d < D) {
-          float y = a.rms ? v[e] * scale : v[e];
-          if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
-          xs[m * LDX + i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+      for (int i = 0; i < 3; ++i)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int d = lane + e * 64;
+          v[u][i][e] = (i < a.n_in && d < D) ? load_in(a, i, b, h, s, d) : 0.f;
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < kGroup; ++u) {
+      const int m = wid * 16 + tt0 + u;
+#pragma unroll
+      for (int i = 0; i < 3; ++i) {
+        if (i >= a.n_in) break;
+        float scale = 1.f;
+        if (a.rms) {
+          const float var = wave_sum(v[u][i][0] * v[u][i][0] + v[u][i][1] * v[u][i][1]) / (float)D;
+          scale = 1.0f / sqrtf(var + 1e-6f);
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int d = lane + e * 64;
+          if (d < D) {
+            float y = a.rms ? v[u][i][e] * scale : v[u][i][e];
+            if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
+            xs[m * LDX + i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+          }
         }
       }
     }
