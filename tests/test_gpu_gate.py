@@ -113,3 +113,27 @@ def test_cached_fp32_weights_follow_in_place_updates():
     second = g16(pre_k.cuda(), post_k.cuda(), value.cuda()).cpu()
     assert not torch.equal(first, second)
     assert (second - ref).abs().max().item() <= 2e-6
+
+
+@pytest.mark.parametrize("g_inputs", [("pre_k", "post_k", "v"), ("post_k",), ("pre_k", "v")])
+@pytest.mark.parametrize("S", [1, 3, 130])
+@pytest.mark.parametrize("D", [128, 64])
+def test_gate_input_sets_match_oracle(g_inputs, S, D):
+    """The other input sets the reference's GatingPredictor accepts
+    (src/modeling_layers.py:135-146, :170-205): one, two or three normalised
+    inputs (n_in * D columns of W1), through the few-token decode kernel
+    (S <= 4) and the 64-token MFMA kernel."""
+    from wgkv.gate import GatingPredictor
+    H, g_expand = 4, 4.0
+    gen = torch.Generator().manual_seed(7 * S + D + len(g_inputs))
+    g = GatingPredictor(D, H, list(g_inputs), "gelu", g_expand, 1e-3, True, True)
+    params = {}
+    for k, v in g.state_dict().items():
+        params[k] = torch.randn(v.shape, generator=gen) * (0.05 if "conv" in k else 1.0) + (1.0 if "norm" in k else 0.0)
+    g.load_state_dict(params, strict=True)
+    g = g.cuda()
+    pre_k, post_k, value = (torch.randn(1, H, S, D, generator=gen) for _ in range(3))
+    ref = ogate.gate_scores(pre_k, post_k, value, params, g_inputs=g_inputs)
+    thr = float(torch.quantile(ref.flatten().double(), 0.5))
+    scores, mask = g.scores_and_mask(pre_k.cuda(), post_k.cuda(), value.cuda(), thr)
+    compare(scores, mask, ref, thr, f"inputs {'+'.join(g_inputs)} D{D} S{S}")

@@ -259,33 +259,40 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   float logit[kSmallTok];
 #pragma unroll
   for (int t = 0; t < kSmallTok; ++t) logit[t] = 0.f;
+  // columns in groups of JB: with two input chunks per lane, 8 W1 rows in
+  // flight keep the registers within the 1024-thread budget
+  constexpr int JB = CPL > 1 ? 8 : 16;
   for (int c0 = wid * 16; c0 < a.inner; c0 += 16 * kSmallWaves) {
-    float dot[kSmallTok][16];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      f32x4_t w[CPL];
+    for (int j0 = 0; j0 < 16; j0 += JB) {
+      float dot[kSmallTok][JB];
 #pragma unroll
-      for (int c = 0; c < CPL; ++c) {
-        const int kc = lane + c * 64;
-        w[c] = kc < KC ? *(const f32x4_t*)(w1h + (int64_t)(c0 + j) * K + kc * 4) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < JB; ++j) {
+        f32x4_t w[CPL];
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const int kc = lane + c * 64;
+          w[c] = kc < KC ? *(const f32x4_t*)(w1h + (int64_t)(c0 + j0 + j) * K + kc * 4)
+                         : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int t = 0; t < kSmallTok; ++t) {
+          float acc = 0.f;
+#pragma unroll
+          for (int c = 0; c < CPL; ++c)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc = fmaf(w[c][e], xr[t][c][e], acc);
+          dot[t][j] = acc;
+        }
       }
 #pragma unroll
       for (int t = 0; t < kSmallTok; ++t) {
-        float acc = 0.f;
+        if (t >= nt) break;
 #pragma unroll
-        for (int c = 0; c < CPL; ++c)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) acc = fmaf(w[c][e], xr[t][c][e], acc);
-        dot[t][j] = acc;
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < kSmallTok; ++t) {
-      if (t >= nt) break;
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const float z = wave_sum(dot[t][j]) + b1h[c0 + j];
-        if (lane == j) logit[t] = fmaf(w2h[c0 + j], a.act ? silu(z) : gelu_erf(z), logit[t]);
+        for (int j = 0; j < JB; ++j) {
+          const float z = wave_sum(dot[t][j]) + b1h[c0 + j0 + j];
+          if (lane == j0 + j) logit[t] = fmaf(w2h[c0 + j0 + j], a.act ? silu(z) : gelu_erf(z), logit[t]);
+        }
       }
     }
   }
