@@ -4,7 +4,7 @@ Host side of the path: the reference's layer/cache API on top of the HIP
 C-ABI library ``libwgkv.so`` (include/wgkv.h).  Device work always goes
 through that library; there is no CPU fallback.
 """
-from . import _lib, ops  # noqa: F401
+from . import _lib, ops, torch_ops  # noqa: F401  (torch_ops registers torch.ops.wgkv.*)
 from .ops import (  # noqa: F401
     flash_attn_with_kvcache_wrapper,
     flash_attn_with_kvcache_wrapper_handle,

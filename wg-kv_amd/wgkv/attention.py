@@ -15,7 +15,7 @@ and q/k/v are rounded to bf16 after gating.
 import torch
 import torch.nn as nn
 
-from . import layers, ops
+from . import layers, ops, torch_ops
 from .gate import GatingPredictor
 
 
@@ -88,9 +88,9 @@ class LlamaAttention(nn.Module):
         self.self_attn_forward_patch = layers.self_attn_forward_patch
         self.prefill_wrapper = layers.prefill_wrapper
         self.decode_wrapper = layers.decode_wrapper
-        self.prefill_kernel = ops.sparse_attn_func
+        self.prefill_kernel = torch_ops.sparse_attn_func  # torch.ops.wgkv.sparse_attn
         self.chunk_prefill_kernel = ops.chunk_attend  # prompt chunks after the first (no reference counterpart)
-        self.decode_kernel_handle = ops.paged_decode_attn_handle
+        self.decode_kernel_handle = torch_ops.paged_decode_attn_handle  # torch.ops.wgkv.paged_decode_attn
         self.decode_kernel_executor = lambda func: func()
 
     def forward(self, gating_mode, hidden_states, position_embeddings, attention_mask=None, past_key_value=None,

@@ -72,52 +72,72 @@ class GatingPredictor(nn.Module):
 
     def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True):
         """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S))."""
-        ref = post_key
-        B, H, S, D = ref.shape
+        B, H, S, D = post_key.shape
         if H != self.num_kv_heads or D != self.head_dim:
             raise AssertionError("gate input shape does not match the predictor")
-        dt = ref.dtype
-        if dt not in (torch.bfloat16, torch.float32):
-            raise TypeError("gate inputs must be bf16 or fp32")
-        ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
-        bits = 0
-        args = []
-        for name in ("pre_k", "post_k", "v"):
-            t = ins[name] if name in self.g_inputs else None
-            if t is not None:
-                if t.dtype != dt or t.shape != ref.shape or t.stride(3) != 1:
-                    raise AssertionError("gate inputs must share shape/dtype with a contiguous last dim")
-                _require_cuda(t)
-                bits |= _INPUT_BITS[name]
-                args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
-            else:
-                args += [None, 0, 0, 0]
         norms = [self.pre_key_norm, self.post_key_norm, self.value_norm]
         wn = [self._f32(m.weight) if isinstance(m, GatingRMSNorm) else None for m in norms]
-        w1 = self._f32(self.conv1.weight)
-        b1 = self._f32(self.conv1.bias)
-        w2 = self._f32(self.conv2.weight)
-        b2 = self._f32(self.conv2.bias)
-        dev = ref.device
-        scores = None
-        if want_scores:
-            scores = scores_out if scores_out is not None else torch.empty(B, H, S, dtype=torch.float32, device=dev)
-        mask = mask_out if mask_out is not None else torch.empty(B, H, S, dtype=torch.bool, device=dev)
-        mk = mask.view(torch.uint8)
-        st = _lib.lib().wgkv_gate_scores(
-            *args,
-            0 if dt == torch.bfloat16 else 1, bits,
-            _ptr(wn[0]), _ptr(wn[1]), _ptr(wn[2]),
-            _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
-            B, H, S, D, self.inner_dim,
-            self.act, int(self.g_rms), 0.0 if self.g_fast_path else float(self.g_epsilon), float(threshold),
-            _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
-            _ptr(mk), mk.stride(0), mk.stride(1),
-            _lib.stream_handle(dev))
-        _lib.check(st, "wgkv_gate_scores")
-        return scores, mask
+        return gate_scores_and_mask(
+            pre_key if "pre_k" in self.g_inputs else None, post_key if "post_k" in self.g_inputs else None,
+            value if "v" in self.g_inputs else None, wn[0], wn[1], wn[2],
+            self._f32(self.conv1.weight), self._f32(self.conv1.bias), self._f32(self.conv2.weight),
+            self._f32(self.conv2.bias), self.inner_dim, self.act, self.g_rms,
+            0.0 if self.g_fast_path else float(self.g_epsilon), threshold,
+            like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores)
 
     def forward(self, pre_key, post_key, value):
         """Scores (B, H, S) float32, as the reference's forward returns."""
         scores, _ = self.scores_and_mask(pre_key, post_key, value, threshold=0.0)
         return scores
+
+
+def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
+                         clamp_min, threshold, like=None, scores_out=None, mask_out=None, want_scores=True):
+    """The gate kernel on explicit fp32 parameters (GatingPredictor.forward,
+    src/modeling_layers.py:170-205, with the admission of :1465): inputs
+    (B, H, S, D) bf16 or fp32 (None for inputs not used), RMS-norm weights (D)
+    or None, conv1 weight (H*inner, n_in*D, 1) / bias, conv2 weight
+    (H, inner, 1) / bias, act 0 = GELU (erf) / 1 = SiLU, clamp_min > 0 for the
+    conv path's clamp.  Returns (scores f32 (B,H,S) or None, mask bool
+    (B,H,S))."""
+    ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
+    ref = like if like is not None else next(t for t in (post_key, pre_key, value) if t is not None)
+    B, H, S, D = ref.shape
+    dt = ref.dtype
+    if dt not in (torch.bfloat16, torch.float32):
+        raise TypeError("gate inputs must be bf16 or fp32")
+    bits = 0
+    args = []
+    for name in ("pre_k", "post_k", "v"):
+        t = ins[name]
+        if t is not None:
+            if t.dtype != dt or t.shape != ref.shape or t.stride(3) != 1:
+                raise AssertionError("gate inputs must share shape/dtype with a contiguous last dim")
+            _require_cuda(t)
+            bits |= _INPUT_BITS[name]
+            args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+        else:
+            args += [None, 0, 0, 0]
+    if bits == 0:
+        raise AssertionError("the gate needs at least one input")
+    for w in (w_pre, w_post, w_v, w1, b1, w2, b2):
+        if w is not None and (w.dtype != torch.float32 or not w.is_contiguous()):
+            raise TypeError("gate parameters must be contiguous fp32")
+    dev = ref.device
+    scores = None
+    if want_scores:
+        scores = scores_out if scores_out is not None else torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    mask = mask_out if mask_out is not None else torch.empty(B, H, S, dtype=torch.bool, device=dev)
+    mk = mask.view(torch.uint8)
+    st = _lib.lib().wgkv_gate_scores(
+        *args,
+        0 if dt == torch.bfloat16 else 1, bits,
+        _ptr(w_pre), _ptr(w_post), _ptr(w_v),
+        _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
+        B, H, S, D, int(inner),
+        int(act), int(bool(rms)), float(clamp_min), float(threshold),
+        _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
+        _ptr(mk), mk.stride(0), mk.stride(1),
+        _lib.stream_handle(dev))
+    _lib.check(st, "wgkv_gate_scores")
+    return scores, mask
