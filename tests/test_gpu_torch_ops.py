@@ -23,9 +23,9 @@ def test_ops_equal_direct_calls():
     mo = torch.ops.wgkv.generate_sparse_indices(gm, W)
     R = (S + 63) // 64
     assert torch.equal(md[0], mo[0]) and torch.equal(md[1], mo[1]) and torch.equal(md[2], mo[2])
-    for h in range(Hkv):  # only the valid prefix of column_index carries meaning
-        n = int(gm[0, h].sum())
-        assert torch.equal(md[3][0, h, 0, :n], mo[3][0, h, 0, :n])
+    for h in range(Hkv):  # only the prefix the kernels read (the last row's column count) carries meaning
+        n = int(md[2][0, h, -1])
+        assert n > 0 and torch.equal(md[3][0, h, 0, :n], mo[3][0, h, 0, :n])
     a = wgkv.sparse_attn_func(q, k, v, *md, softmax_scale=D ** -0.5)
     b = torch.ops.wgkv.sparse_attn(q, k, v, *mo, D ** -0.5)
     assert torch.equal(a, b)
