@@ -284,7 +284,7 @@ int wgkv_chunk_cache_update(
  * chunk's k/v (chunk_len, Hkv, D) with strides kv_ss/kv_sh; pool_k/pool_v
  * (pages*page_size, D) and block_table (L, Hkv, max_pages_per_head) of the
  * cache, column_count (Hkv, R_c) from stage 0.  Supported: D in {64,128},
- * G in {1,2,4,8}. */
+ * G in {1,2,4,8}, page_size 16 (the reference's page, :1209-1216). */
 int wgkv_chunk_prefill_attn(
     const void* q, int64_t q_ss, int64_t q_sh,
     const void* k, const void* v, int64_t kv_ss, int64_t kv_sh,

@@ -29,6 +29,7 @@
 namespace {
 
 constexpr int kBlk = 64;     // query rows per block and keys per tile
+constexpr int kPage = 16;    // cache page (tokens) of the chunked instance
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 units a row maximum may grow before O / l are rescaled
 
@@ -207,7 +208,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const int j = tl * kBlk + min(krow[i], nval - 1);
-        ix.k[i] = CHUNK ? bt_h[j / a.page] : cidx[j];
+        ix.k[i] = CHUNK ? bt_h[j / kPage] : cidx[j];
       }
     } else {
       const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : bofs[r * a.bo_width + (tl - n_vtiles)];
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     if (vertical) {
       if (CHUNK) {
         const int j = tl * kBlk + key_in_tile;
-        return pool + ((int64_t)x * a.page + j % a.page) * D;
+        return pool + ((int64_t)x * kPage + j % kPage) * D;
       }
       return tensor_base + (int64_t)x * a.kv_ss;
     }
@@ -499,6 +500,7 @@ extern "C" int wgkv_chunk_prefill_attn(
   if (chunk_len <= 0 || chunk_start < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return WGKV_ERR_ARG;
   if (local_window <= 0 || local_window % kBlk || chunk_start % kBlk || page_size <= 0 || local_window % page_size)
     return WGKV_ERR_ARG;
+  if (page_size != kPage) return WGKV_ERR_UNSUPPORTED;
   if (chunk_start > 0 && chunk_start < local_window) return WGKV_ERR_ARG;  // the ring must be full
   const int G = num_q_heads / num_kv_heads;
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
