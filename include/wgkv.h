@@ -196,7 +196,14 @@ int wgkv_decode_append_ring(
  * clamp_min > 0 applies the conv path's clamp (:205).  Outputs (may be NULL,
  * not both): scores f32 (B,H,S), mask u8 (B,H,S) = scores > threshold.
  * Supported: D in {64,128}, inner a multiple of 16, n_in*D <= 384.
+ * workspace (may be NULL): for seq_len <= 4 (decode steps) the hidden
+ * columns of each head are split over several workgroups whose partial
+ * logits meet in the workspace; it must hold wgkv_gate_workspace_bytes()
+ * bytes, be zero-filled before its first use and not be shared by
+ * concurrent calls (each call leaves its counters at zero again).  With
+ * NULL one workgroup per head takes all columns.
  * ---------------------------------------------------------------------- */
+int64_t wgkv_gate_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t inner);
 int wgkv_gate_scores(
     const void* pre_key, int64_t pk_sb, int64_t pk_sh, int64_t pk_ss,
     const void* post_key, int64_t k_sb, int64_t k_sh, int64_t k_ss,
@@ -208,6 +215,7 @@ int wgkv_gate_scores(
     int32_t act, int32_t rms, float clamp_min, float threshold,
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
+    void* workspace, int64_t workspace_bytes,
     void* stream);
 
 /* ------------------------------------------------------------------------

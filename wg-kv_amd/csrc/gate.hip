@@ -35,6 +35,12 @@ struct GateArgs {
   int64_t sc_sb, sc_sh;
   uint8_t* mask;
   int64_t mk_sb, mk_sh;
+  // few-token kernel: hidden columns split over nsplit workgroups per head;
+  // partial logits part[(bh*nsplit + split)*kSmallTok + t], arrival counters
+  // counter[bh] (zero between launches)
+  int nsplit;
+  float* part;
+  int32_t* counter;
 };
 
 __device__ __forceinline__ float load_in(const GateArgs& a, int i, int b, int h, int s, int d) {
@@ -190,16 +196,20 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
   }
 }
 
-// Few tokens (decode steps): one workgroup per (batch, KV head) and group of
-// up to kSmallTok tokens.  The MFMA tile above would compute 64 token rows to
-// use one and stream W1[h] through a single dependent chain; here the lanes
-// of a wave split the K dimension, so each W1 row is read with one coalesced
-// load per wave, and each of the 16 waves takes 16 hidden columns at a time
-// (interleaved in 16-column tiles).  Per column the lane partials are
-// summed over the wave; lane i < 16 then applies bias, activation and w2 for
-// column i.  Column order is fixed, so results are deterministic.
+// Few tokens (decode steps, S <= kSmallTok).  The hidden columns of a head
+// are split over nsplit workgroups of 4 waves, 64 columns each, so a head's
+// W1 streams through many CUs at once; within a wave the lanes split the K
+// dimension (each W1 row is one coalesced load per wave) and the wave takes
+// 16 columns.  Per column the lane partials are summed over the wave; lane
+// i < 16 then applies bias, activation and w2 for column i.  Each workgroup
+// stores its partial logits; the last workgroup of the head to arrive (a
+// device-scope counter, reset to zero by that workgroup) adds the partials in
+// split order and applies sigmoid, clamp and threshold, so results do not
+// depend on arrival order.  Without a workspace (nsplit = 1) one workgroup
+// takes all columns.
 constexpr int kSmallTok = 4;
-constexpr int kSmallWaves = 16;  // 16 waves: W1 rows of 16 x 16 columns in flight at once
+constexpr int kSmallWaves = 4;
+constexpr int kSplitCols = 16 * kSmallWaves;  // hidden columns per workgroup and pass
 
 template <int K>
 __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a) {
@@ -208,34 +218,61 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   __shared__ __attribute__((aligned(16))) float xs[kSmallTok][K];
   __shared__ float s_part[kSmallWaves][kSmallTok];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
-  const int bh = blockIdx.y;
+  const int split = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh - b * a.H;
-  const int s0 = blockIdx.x * kSmallTok;
-  const int nt = min(kSmallTok, a.S - s0);
+  const int nt = a.S;  // <= kSmallTok
   const int D = a.D;
+  // sigmoid, clamp, threshold and the stores of token s's logit z (before b2)
+  auto finish = [&](int s, float z) {
+    z += a.b2[h];
+    float g = 1.0f / (1.0f + expf(-z));
+    if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+    if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
+    if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
+  };
 
-  // normalised inputs -> LDS: wave w handles token w
+  // The first W1 rows of this wave do not depend on the inputs: their loads
+  // are issued first, so their latency overlaps the input normalisation.
+  const float* w1h = a.w1 + (int64_t)h * a.inner * K;
+  constexpr int JB = CPL > 1 ? 8 : 16;  // W1 rows in flight per wave (two input chunks per lane: 8)
+  f32x4_t wrow[JB][CPL];
+  auto load_rows = [&](int c0) {
+#pragma unroll
+    for (int j = 0; j < JB; ++j)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int kc = lane + c * 64;
+        wrow[j][c] = kc < KC ? *(const f32x4_t*)(w1h + (int64_t)(c0 + j) * K + kc * 4) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
+      }
+  };
+  const int c_first = split * kSplitCols + wid * 16;
+  if (c_first < a.inner) load_rows(c_first);
+
+  // normalised inputs -> LDS: wave w handles token w; all its input loads
+  // are issued before the first reduction
   if (wid < nt) {
-    const int s = s0 + wid;
-    for (int i = 0; i < a.n_in; ++i) {
-      float v[2];
-      float sq = 0.f;
+    const int s = wid;
+    float v[3][2];
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int d = lane + e * 64;
-        v[e] = d < D ? load_in(a, i, b, h, s, d) : 0.f;
-        sq += v[e] * v[e];
+        v[i][e] = (i < a.n_in && d < D) ? load_in(a, i, b, h, s, d) : 0.f;
       }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+      if (i >= a.n_in) break;
       float scale = 1.f;
       if (a.rms) {
-        const float var = wave_sum(sq) / (float)D;
+        const float var = wave_sum(v[i][0] * v[i][0] + v[i][1] * v[i][1]) / (float)D;
         scale = 1.0f / sqrtf(var + 1e-6f);
       }
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
         const int d = lane + e * 64;
         if (d < D) {
-          float y = a.rms ? v[e] * scale : v[e];
+          float y = a.rms ? v[i][e] * scale : v[i][e];
           if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
           xs[wid][i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
         }
@@ -253,38 +290,27 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
       const int kc = lane + c * 64;
       xr[t][c] = (t < nt && kc < KC) ? *(const f32x4_t*)(&xs[t][kc * 4]) : (f32x4_t){0.f, 0.f, 0.f, 0.f};
     }
-  const float* w1h = a.w1 + (int64_t)h * a.inner * K;
   const float* b1h = a.b1 + (int64_t)h * a.inner;
   const float* w2h = a.w2 + (int64_t)h * a.inner;
   float logit[kSmallTok];
 #pragma unroll
   for (int t = 0; t < kSmallTok; ++t) logit[t] = 0.f;
-  // columns in groups of JB: with two input chunks per lane, 8 W1 rows in
-  // flight keep the registers within the 1024-thread budget
-  constexpr int JB = CPL > 1 ? 8 : 16;
-  for (int c0 = wid * 16; c0 < a.inner; c0 += 16 * kSmallWaves) {
+  for (int c0 = c_first; c0 < a.inner; c0 += kSplitCols * a.nsplit) {
 #pragma unroll
     for (int j0 = 0; j0 < 16; j0 += JB) {
+      if (c0 != c_first || j0 != 0) load_rows(c0 + j0);
       float dot[kSmallTok][JB];
 #pragma unroll
-      for (int j = 0; j < JB; ++j) {
-        f32x4_t w[CPL];
-#pragma unroll
-        for (int c = 0; c < CPL; ++c) {
-          const int kc = lane + c * 64;
-          w[c] = kc < KC ? *(const f32x4_t*)(w1h + (int64_t)(c0 + j0 + j) * K + kc * 4)
-                         : (f32x4_t){0.f, 0.f, 0.f, 0.f};
-        }
+      for (int j = 0; j < JB; ++j)
 #pragma unroll
         for (int t = 0; t < kSmallTok; ++t) {
           float acc = 0.f;
 #pragma unroll
           for (int c = 0; c < CPL; ++c)
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc = fmaf(w[c][e], xr[t][c][e], acc);
+            for (int e = 0; e < 4; ++e) acc = fmaf(wrow[j][c][e], xr[t][c][e], acc);
           dot[t][j] = acc;
         }
-      }
 #pragma unroll
       for (int t = 0; t < kSmallTok; ++t) {
         if (t >= nt) break;
@@ -303,30 +329,57 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
     if (lane == 0) s_part[wid][t] = v;
   }
   __syncthreads();
-  if (threadIdx.x < nt) {
-    const int t = threadIdx.x;
-    const int s = s0 + t;
-    float z = 0.f;
+  const int t = threadIdx.x;
+  if (a.nsplit > 1) {
+    // thread 0 publishes this workgroup's partials and counts its arrival
+    // (acquire-release at device scope); the last to arrive sums the
+    // partials in split order and resets the counter
+    if (t != 0) return;
+    float* part = a.part + (int64_t)bh * a.nsplit * kSmallTok;
+    for (int tt = 0; tt < nt; ++tt) {
+      float zz = 0.f;
+#pragma unroll
+      for (int w = 0; w < kSmallWaves; ++w) zz += s_part[w][tt];
+      part[split * kSmallTok + tt] = zz;
+    }
+    const int prev = __hip_atomic_fetch_add(&a.counter[bh], 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev != a.nsplit - 1) return;
+    __hip_atomic_store(&a.counter[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int tt = 0; tt < nt; ++tt) {
+      float z = 0.f;
+      for (int sp = 0; sp < a.nsplit; ++sp) z += part[sp * kSmallTok + tt];
+      finish(tt, z);
+    }
+    return;
+  }
+  float z = 0.f;
+  if (t < nt) {
 #pragma unroll
     for (int w = 0; w < kSmallWaves; ++w) z += s_part[w][t];
-    z += a.b2[h];
-    float g = 1.0f / (1.0f + expf(-z));
-    if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
-    if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
-    if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
   }
+  if (t < nt) finish(t, z);
 }
 
 template <int K>
 void launch_gate(const GateArgs& a, hipStream_t st) {
   if (a.S <= kSmallTok) {
-    hipLaunchKernelGGL(gate_small_kernel<K>, dim3(1, a.B * a.H), dim3(64 * kSmallWaves), 0, st, a);
+    hipLaunchKernelGGL(gate_small_kernel<K>, dim3(a.nsplit, a.B * a.H), dim3(64 * kSmallWaves), 0, st, a);
   } else {
     hipLaunchKernelGGL(gate_kernel<K>, dim3((a.S + kTok - 1) / kTok, a.B * a.H), dim3(kThreads), 0, st, a);
   }
 }
 
 }  // namespace
+
+namespace {
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" int64_t wgkv_gate_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t inner) {
+  const int64_t nsplit = (inner + kSplitCols - 1) / kSplitCols;
+  const int64_t bh = (int64_t)batch * num_kv_heads;
+  return align256(bh * 4) + align256(bh * nsplit * kSmallTok * 4);
+}
 
 extern "C" int wgkv_gate_scores(
     const void* pre_key, int64_t pk_sb, int64_t pk_sh, int64_t pk_ss,
@@ -339,6 +392,7 @@ extern "C" int wgkv_gate_scores(
     int32_t act, int32_t rms, float clamp_min, float threshold,
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
+    void* workspace, int64_t workspace_bytes,
     void* stream) {
   if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0) return WGKV_ERR_ARG;
   if (!w1 || !b1 || !w2 || !b2 || (!scores && !mask)) return WGKV_ERR_ARG;
@@ -382,6 +436,14 @@ extern "C" int wgkv_gate_scores(
   a.mask = mask;
   a.mk_sb = mk_sb;
   a.mk_sh = mk_sh;
+  a.nsplit = 1;
+  if (workspace && seq_len <= kSmallTok) {
+    const int nsplit = (inner + kSplitCols - 1) / kSplitCols;
+    if (workspace_bytes < wgkv_gate_workspace_bytes(batch, num_kv_heads, inner)) return WGKV_ERR_ARG;
+    a.nsplit = nsplit;
+    a.counter = (int32_t*)workspace;
+    a.part = (float*)((char*)workspace + align256((int64_t)batch * num_kv_heads * 4));
+  }
   if (((uintptr_t)w1 & 15) != 0) return WGKV_ERR_UNSUPPORTED;
   const int K = n_in * head_dim;
   hipStream_t st = (hipStream_t)stream;

@@ -208,7 +208,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         const int j = tl * kBlk + min(krow[i], nval - 1);
-        ix.k[i] = CHUNK ? bt_h[j / kPage] : cidx[j];
+        ix.k[i] = CHUNK ? bt_h[(unsigned)j / kPage] : cidx[j];  // j >= 0
       }
     } else {
       const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : bofs[r * a.bo_width + (tl - n_vtiles)];
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     if (vertical) {
       if (CHUNK) {
         const int j = tl * kBlk + key_in_tile;
-        return pool + ((int64_t)x * kPage + j % kPage) * D;
+        return pool + ((int64_t)x * kPage + (unsigned)j % kPage) * D;  // j >= 0
       }
       return tensor_base + (int64_t)x * a.kv_ss;
     }

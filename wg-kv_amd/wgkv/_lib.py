@@ -94,7 +94,9 @@ SIGNATURES = {
         c_i32, c_i32, c_f32, c_f32,
         c_ptr, c_i64, c_i64,
         c_ptr, c_i64, c_i64,
+        c_ptr, c_i64,
         c_ptr]),
+    "wgkv_gate_workspace_bytes": (ctypes.c_int64, [c_i32, c_i32, c_i32]),
     "wgkv_sparse_prefill_attn": (ctypes.c_int, [
         c_ptr, c_i64, c_i64, c_i64,
         c_ptr, c_ptr, c_i64, c_i64, c_i64,

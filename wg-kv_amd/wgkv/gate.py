@@ -129,6 +129,7 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         scores = scores_out if scores_out is not None else torch.empty(B, H, S, dtype=torch.float32, device=dev)
     mask = mask_out if mask_out is not None else torch.empty(B, H, S, dtype=torch.bool, device=dev)
     mk = mask.view(torch.uint8)
+    ws = _decode_workspace(dev, B, H, int(inner)) if S <= 4 else None
     st = _lib.lib().wgkv_gate_scores(
         *args,
         0 if dt == torch.bfloat16 else 1, bits,
@@ -138,6 +139,22 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         int(act), int(bool(rms)), float(clamp_min), float(threshold),
         _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
         _ptr(mk), mk.stride(0), mk.stride(1),
+        _ptr(ws), 0 if ws is None else ws.numel(),
         _lib.stream_handle(dev))
     _lib.check(st, "wgkv_gate_scores")
     return scores, mask
+
+
+_DECODE_WS = {}
+
+
+def _decode_workspace(device, B, H, inner):
+    """Zero-filled workspace of the few-token gate (partial logits and
+    per-head counters that each launch leaves at zero), one per device, grown
+    when a call needs more; calls on one stream reuse it in turn."""
+    need = int(_lib.lib().wgkv_gate_workspace_bytes(B, H, inner))
+    ws = _DECODE_WS.get(device)
+    if ws is None or ws.numel() < need:
+        ws = torch.zeros(max(need, 65536), dtype=torch.uint8, device=device)
+        _DECODE_WS[device] = ws
+    return ws
