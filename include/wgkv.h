@@ -346,6 +346,36 @@ int wgkv_quest_select(
     int32_t* sel_block_table, int32_t sel_cap, int32_t* sel_seqlens,
     void* workspace, size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Decoder building blocks for the end-to-end harness around the path (bf16).
+ * No counterpart among the path's functions: each replaces a chain of torch
+ * kernels of the reference model with one launch, with the same bf16
+ * rounding points.
+ *
+ * wgkv_rms_norm -- LlamaRMSNorm (src/modeling_llama.py:61-76), optionally
+ *   after the residual add (:366, :399): rows of `hidden` bf16 (row strides
+ *   in elements); with residual (and residual_out, may equal x) h = x +
+ *   residual is stored to residual_out and normalised.  out = weight *
+ *   bf16(h * rsqrt(mean(h^2) + eps)).  hidden a multiple of 8, <= 8192.
+ * wgkv_rope_qk -- apply_rotary_pos_emb (:115-146) for q (B,S,Hq,D) and k
+ *   (B,S,Hkv,D) with element strides (batch, seq, head; d contiguous) and the
+ *   step's cos / sin (B,S,D) bf16; writes contiguous q_out (B,S,Hq,D) and
+ *   k_out (B,S,Hkv,D).  D a multiple of 16.
+ * wgkv_silu_mul -- LlamaMLP's act_fn(gate) * up (:161): n bf16 elements,
+ *   contiguous, n a multiple of 8.
+ * ---------------------------------------------------------------------- */
+int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t res_row_stride,
+                  const void* weight, void* out, int64_t out_row_stride, void* residual_out,
+                  int64_t res_out_row_stride, int32_t rows, int32_t hidden, float eps, void* stream);
+
+int wgkv_rope_qk(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                 const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                 const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                 void* q_out, void* k_out, int32_t batch, int32_t seq_len,
+                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream);
+
+int wgkv_silu_mul(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

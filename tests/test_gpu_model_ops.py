@@ -1,0 +1,64 @@
+"""The fused decoder building blocks of the end-to-end harness
+(csrc/model_ops.hip) against the torch compositions they replace (the
+reference model's LlamaRMSNorm, apply_rotary_pos_emb, SwiGLU): RoPE and the
+SwiGLU product bit-identical, the residual add bit-identical, RMSNorm within
+one bf16 rounding step (its fp32 mean of squares is summed in another order)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+
+
+def torch_rms(x, w, eps):
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return w * xf.to(x.dtype)
+
+
+@pytest.mark.parametrize("rows,hidden", [(1, 4096), (37, 4096), (5, 512), (3, 8192), (2, 136)])
+def test_rms_norm(rows, hidden):
+    from wgkv import model_ops
+    print(f"[model_ops] rms_norm {rows}x{hidden}", flush=True)
+    g = torch.Generator().manual_seed(rows * hidden)
+    x = (torch.randn(rows, hidden, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    r = torch.randn(rows, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.rand(hidden, generator=g) + 0.5).to(torch.bfloat16).to(DEV)
+    out, none = model_ops.rms_norm(x, w, 1e-5)
+    assert none is None
+    ref = torch_rms(x, w, 1e-5)
+    ulp = (ref.float().abs() * 2 ** -7).clamp_min(1e-30)
+    assert ((out.float() - ref.float()).abs() <= ulp * 1.01 + 1e-30).all()
+    assert (out == ref).float().mean().item() > 0.99
+    out2, h = model_ops.rms_norm(x, w, 1e-5, residual=r)
+    assert torch.equal(h, x + r)
+    ref2 = torch_rms(x + r, w, 1e-5)
+    assert ((out2.float() - ref2.float()).abs() <= (ref2.float().abs() * 2 ** -7) * 1.01 + 1e-30).all()
+
+
+@pytest.mark.parametrize("B,S,Hq,Hkv,D", [(1, 1, 32, 8, 128), (1, 300, 8, 2, 64), (2, 17, 4, 4, 128)])
+def test_rope_bit_identical(B, S, Hq, Hkv, D):
+    from wgkv import model_ops
+    from wgkv.attention import LlamaRotaryEmbedding, apply_rotary_pos_emb
+    print(f"[model_ops] rope B{B} S{S} Hq{Hq} Hkv{Hkv} D{D}", flush=True)
+    g = torch.Generator().manual_seed(S + D)
+    qp = torch.randn(B, S, Hq * D, generator=g).to(torch.bfloat16).to(DEV)
+    kp = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).to(DEV)
+    q = qp.view(B, S, Hq, D).transpose(1, 2)
+    k = kp.view(B, S, Hkv, D).transpose(1, 2)
+    rot = LlamaRotaryEmbedding(D, 500000.0).to(DEV)
+    pos = torch.arange(1000, 1000 + S, device=DEV)[None].expand(B, S)
+    cos, sin = rot(qp, pos)
+    rq, rk = apply_rotary_pos_emb(q, k, cos, sin)
+    fq, fk = model_ops.rope_qk(q, k, cos, sin)
+    assert torch.equal(fq, rq) and torch.equal(fk, rk)
+
+
+@pytest.mark.parametrize("n", [14336, 4096 * 8, 96])
+def test_silu_mul_bit_identical(n):
+    from wgkv import model_ops
+    g = torch.Generator().manual_seed(n)
+    a = (torch.randn(n, generator=g) * 4).to(torch.bfloat16).to(DEV)
+    b = torch.randn(n, generator=g).to(torch.bfloat16).to(DEV)
+    assert torch.equal(model_ops.silu_mul(a, b), F.silu(a) * b)

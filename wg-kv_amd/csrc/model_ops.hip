@@ -1,0 +1,211 @@
+// Fused bf16 building blocks of the decoder around the path (the end-to-end
+// harness): RMSNorm with the residual add before it, rotary embedding of q
+// and k, and the SwiGLU product.  Each replaces a chain of small torch
+// kernels (LlamaRMSNorm, src/modeling_llama.py:61-76; apply_rotary_pos_emb
+// :115-146; LlamaMLP :149-161; the residual adds :366, :399) with one launch
+// and follows the same bf16 rounding points as the torch composition: every
+// bf16 x bf16 product and sum is rounded to bf16 where torch rounds it.
+#include "wgkv_common.h"
+
+namespace {
+
+// round an f32 to the nearest bf16, returned as f32
+WGKV_DEVICE float rb(float x) { return bf16lo(f32_to_bf16(x)); }
+
+WGKV_DEVICE void unpack8(const u32x4_t w, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = bf16lo(w[i]);
+    f[2 * i + 1] = bf16hi(w[i]);
+  }
+}
+
+WGKV_DEVICE u32x4_t pack8(const float (&f)[8]) {
+  u32x4_t w;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) w[i] = (uint32_t)f32_to_bf16(f[2 * i]) | ((uint32_t)f32_to_bf16(f[2 * i + 1]) << 16);
+  return w;
+}
+
+// ---- RMSNorm (optionally after the residual add) ---------------------------
+// One workgroup per row of `hidden` elements, 8 per 16-byte chunk, at most 4
+// chunks per thread (hidden <= 8192).  With a residual: h = bf16(x + res) is
+// both the new residual stream (res_out) and the norm's input.
+// out = bf16(w * bf16(h * rsqrt(mean(h^2) + eps))).
+constexpr int kNormThreads = 256;
+constexpr int kNormChunks = 4;
+
+struct NormArgs {
+  const uint16_t* x;
+  int64_t x_rs;
+  const uint16_t* res;
+  int64_t r_rs;
+  const uint16_t* w;
+  uint16_t* out;
+  int64_t o_rs;
+  uint16_t* res_out;
+  int64_t ro_rs;
+  int hidden;
+  float eps;
+};
+
+template <bool RES>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
+  __shared__ float s_sum[kNormThreads / 64];
+  const int row = blockIdx.x, t = threadIdx.x;
+  const int nch = a.hidden / 8;
+  float h[kNormChunks][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = t + c * kNormThreads;
+    if (ch < nch) {
+      unpack8(*(const u32x4_t*)(a.x + row * a.x_rs + ch * 8), h[c]);
+      if (RES) {
+        float r[8];
+        unpack8(*(const u32x4_t*)(a.res + row * a.r_rs + ch * 8), r);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) h[c][i] = rb(h[c][i] + r[i]);
+        *(u32x4_t*)(a.res_out + row * a.ro_rs + ch * 8) = pack8(h[c]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(h[c][i], h[c][i], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  if ((t & 63) == 0) s_sum[t >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int wv = 0; wv < kNormThreads / 64; ++wv) tot += s_sum[wv];
+  const float scale = rsqrtf(tot / (float)a.hidden + a.eps);
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int ch = t + c * kNormThreads;
+    if (ch < nch) {
+      float w[8], y[8];
+      unpack8(*(const u32x4_t*)(a.w + ch * 8), w);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) y[i] = w[i] * rb(h[c][i] * scale);
+      *(u32x4_t*)(a.out + row * a.o_rs + ch * 8) = pack8(y);
+    }
+  }
+}
+
+// ---- rotary embedding of q and k -------------------------------------------
+// Thread = (token, head of q or k, 8 consecutive d of the first half) and the
+// matching 8 of the second half: out[d] = bf16(bf16(x[d] cos[d]) + bf16(-x[d+h] sin[d])),
+// out[d+h] = bf16(bf16(x[d+h] cos[d+h]) + bf16(x[d] sin[d+h])), h = D/2.
+struct RopeArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_ss, q_sh;
+  const uint16_t* k;
+  int64_t k_sb, k_ss, k_sh;
+  const uint16_t* cos;
+  const uint16_t* sin;
+  int64_t cs_sb, cs_ss;
+  uint16_t* qo;
+  uint16_t* ko;
+  int B, S, Hq, Hkv, D;
+};
+
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+  const int half = a.D / 2, hch = half / 8;
+  const int64_t total = (int64_t)a.B * a.S * (a.Hq + a.Hkv) * hch;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int c = (int)(i % hch);
+  int64_t r = i / hch;
+  const int hh = (int)(r % (a.Hq + a.Hkv));
+  r /= a.Hq + a.Hkv;
+  const int s = (int)(r % a.S), b = (int)(r / a.S);
+  const bool isq = hh < a.Hq;
+  const int head = isq ? hh : hh - a.Hq;
+  const uint16_t* src = isq ? a.q + b * a.q_sb + s * a.q_ss + head * a.q_sh
+                            : a.k + b * a.k_sb + s * a.k_ss + head * a.k_sh;
+  const int H = isq ? a.Hq : a.Hkv;
+  uint16_t* dst = (isq ? a.qo : a.ko) + (((int64_t)b * a.S + s) * H + head) * a.D;
+  const uint16_t* cs = a.cos + b * a.cs_sb + s * a.cs_ss;
+  const uint16_t* sn = a.sin + b * a.cs_sb + s * a.cs_ss;
+  const int d0 = c * 8;
+  float x1[8], x2[8], c1[8], c2[8], s1[8], s2[8], o1[8], o2[8];
+  unpack8(*(const u32x4_t*)(src + d0), x1);
+  unpack8(*(const u32x4_t*)(src + half + d0), x2);
+  unpack8(*(const u32x4_t*)(cs + d0), c1);
+  unpack8(*(const u32x4_t*)(cs + half + d0), c2);
+  unpack8(*(const u32x4_t*)(sn + d0), s1);
+  unpack8(*(const u32x4_t*)(sn + half + d0), s2);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o1[e] = rb(rb(x1[e] * c1[e]) + rb(-x2[e] * s1[e]));
+    o2[e] = rb(rb(x2[e] * c2[e]) + rb(x1[e] * s2[e]));
+  }
+  *(u32x4_t*)(dst + d0) = pack8(o1);
+  *(u32x4_t*)(dst + half + d0) = pack8(o2);
+}
+
+// ---- SwiGLU: out = bf16(bf16(silu(g)) * u) ----------------------------------
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* out,
+                                                       int64_t n8) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n8) return;
+  float gv[8], uv[8], o[8];
+  unpack8(*(const u32x4_t*)(g + i * 8), gv);
+  unpack8(*(const u32x4_t*)(u + i * 8), uv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = rb(gv[e] / (1.0f + expf(-gv[e]))) * uv[e];
+  *(u32x4_t*)(out + i * 8) = pack8(o);
+}
+
+bool misaligned(const void* p) { return ((uintptr_t)p & 15) != 0; }
+
+}  // namespace
+
+extern "C" int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t res_row_stride,
+                             const void* weight, void* out, int64_t out_row_stride, void* residual_out,
+                             int64_t res_out_row_stride, int32_t rows, int32_t hidden, float eps, void* stream) {
+  if (!x || !weight || !out || rows < 0 || hidden <= 0) return WGKV_ERR_ARG;
+  if ((residual == nullptr) != (residual_out == nullptr)) return WGKV_ERR_ARG;
+  if (hidden % 8 || hidden > 8 * kNormChunks * kNormThreads) return WGKV_ERR_UNSUPPORTED;
+  if (misaligned(x) || misaligned(weight) || misaligned(out) || misaligned(residual) || misaligned(residual_out))
+    return WGKV_ERR_UNSUPPORTED;
+  if ((x_row_stride | res_row_stride | out_row_stride | res_out_row_stride) & 7) return WGKV_ERR_UNSUPPORTED;
+  if (rows == 0) return WGKV_OK;
+  NormArgs a = {(const uint16_t*)x, x_row_stride, (const uint16_t*)residual, res_row_stride,
+                (const uint16_t*)weight, (uint16_t*)out, out_row_stride, (uint16_t*)residual_out,
+                res_out_row_stride, hidden, eps};
+  if (residual)
+    hipLaunchKernelGGL(rms_norm_kernel<true>, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(rms_norm_kernel<false>, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_rope_qk(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                            const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                            const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                            void* q_out, void* k_out, int32_t batch, int32_t seq_len,
+                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream) {
+  if (!q || !k || !cos || !sin || !q_out || !k_out) return WGKV_ERR_ARG;
+  if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0 || num_kv_heads <= 0) return WGKV_ERR_ARG;
+  if (head_dim % 16) return WGKV_ERR_UNSUPPORTED;
+  if (misaligned(q) || misaligned(k) || misaligned(cos) || misaligned(sin) || misaligned(q_out) || misaligned(k_out))
+    return WGKV_ERR_UNSUPPORTED;
+  if ((q_sb | q_ss | q_sh | k_sb | k_ss | k_sh | cs_sb | cs_ss) & 7) return WGKV_ERR_UNSUPPORTED;
+  RopeArgs a = {(const uint16_t*)q, q_sb, q_ss, q_sh, (const uint16_t*)k, k_sb, k_ss, k_sh,
+                (const uint16_t*)cos, (const uint16_t*)sin, cs_sb, cs_ss, (uint16_t*)q_out, (uint16_t*)k_out,
+                batch, seq_len, num_q_heads, num_kv_heads, head_dim};
+  const int64_t total = (int64_t)batch * seq_len * (num_q_heads + num_kv_heads) * (head_dim / 16);
+  hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_silu_mul(const void* gate, const void* up, void* out, int64_t n, void* stream) {
+  if (!gate || !up || !out || n < 0) return WGKV_ERR_ARG;
+  if (n % 8 || misaligned(gate) || misaligned(up) || misaligned(out)) return WGKV_ERR_UNSUPPORTED;
+  if (n == 0) return WGKV_OK;
+  const int64_t n8 = n / 8;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)gate, (const uint16_t*)up, (uint16_t*)out, n8);
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}

@@ -15,7 +15,7 @@ and q/k/v are rounded to bf16 after gating.
 import torch
 import torch.nn as nn
 
-from . import layers, ops, torch_ops
+from . import layers, model_ops, ops, torch_ops
 from .gate import GatingPredictor
 
 
@@ -106,7 +106,11 @@ class LlamaAttention(nn.Module):
         v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
         pre_key = k if "pre_k" in self.config.g_inputs else None
         cos, sin = position_embeddings
-        q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        if (model_ops.usable(q, k, cos, sin) and self.head_dim % 16 == 0 and q.stride(3) == 1 and k.stride(3) == 1
+                and cos.dim() == 3):
+            q, k = model_ops.rope_qk(q, k, cos, sin)  # one launch, the same bf16 rounding
+        else:
+            q, k = apply_rotary_pos_emb(q, k, cos, sin)
         out, attn_weights, g_scores = self.self_attn_forward_patch(
             self, gating_mode, attention_mask, past_key_value, input_shape, q, pre_key, k, v)
         out = out.reshape(*input_shape, -1).to(hidden_states.dtype).contiguous()

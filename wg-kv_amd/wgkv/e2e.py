@@ -23,6 +23,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from . import model_ops
 from .attention import LlamaAttention, LlamaRotaryEmbedding
 from .cache import DualCache
 from .layers import WGKVConfig
@@ -34,11 +35,19 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(hidden))
         self.eps = eps
 
-    def forward(self, x):
+    def forward(self, x, residual=None):
+        """RMSNorm of x (+ residual); with a residual returns (out, x + residual).
+        bf16 on the GPU: one fused launch (wgkv_rms_norm)."""
+        if model_ops.usable(x, self.weight) and x.shape[-1] % 8 == 0 and x.shape[-1] <= 8192:
+            out, h = model_ops.rms_norm(x, self.weight, self.eps, residual)
+            return out if residual is None else (out, h)
+        if residual is not None:
+            x = x + residual
         dt = x.dtype
         xf = x.float()
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return self.weight * xf.to(dt)
+        out = self.weight * xf.to(dt)
+        return out if residual is None else (out, x)
 
 
 class MLP(nn.Module):
@@ -49,7 +58,10 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(inter, hidden, bias=False)
 
     def forward(self, x):
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        g, u = self.gate_proj(x), self.up_proj(x)
+        if model_ops.usable(g, u) and g.is_contiguous() and u.is_contiguous() and g.numel() % 8 == 0:
+            return self.down_proj(model_ops.silu_mul(g, u))
+        return self.down_proj(F.silu(g) * u)
 
 
 class DecoderLayer(nn.Module):
@@ -64,8 +76,8 @@ class DecoderLayer(nn.Module):
         """Input norm, attention, residual add and the post-attention norm
         (src/modeling_llama.py:337-371): returns (residual, MLP input)."""
         h, _, _ = self.self_attn(3, self.input_layernorm(x), pos_emb, None, cache)
-        x = x + h
-        return x, self.post_attention_layernorm(x)
+        mlp_in, x = self.post_attention_layernorm(h, residual=x)  # residual add fused into the norm
+        return x, mlp_in
 
     def forward(self, x, pos_emb, cache):
         residual, h = self.rmsnorm_and_self_attn(x, pos_emb, cache)
