@@ -357,24 +357,31 @@ int wgkv_quest_select(
  *   in elements); with residual (and residual_out, may equal x) h = x +
  *   residual is stored to residual_out and normalised.  out = weight *
  *   bf16(h * rsqrt(mean(h^2) + eps)).  hidden a multiple of 8, <= 8192.
- * wgkv_rope_qk -- apply_rotary_pos_emb (:115-146) for q (B,S,Hq,D) and k
- *   (B,S,Hkv,D) with element strides (batch, seq, head; d contiguous) and the
- *   step's cos / sin (B,S,D) bf16; writes contiguous q_out (B,S,Hq,D) and
- *   k_out (B,S,Hkv,D).  D a multiple of 16.
- * wgkv_silu_mul -- LlamaMLP's act_fn(gate) * up (:161): n bf16 elements,
- *   contiguous, n a multiple of 8.
+ * wgkv_rope_qkv -- apply_rotary_pos_emb (:115-146) for q (B,S,Hq,D) and k
+ *   (B,S,Hkv,D) with the step's cos / sin (B,S,D) bf16, and v (B,S,Hkv,D)
+ *   copied alongside (v and v_out may be NULL), so the three outputs can
+ *   share one buffer and its strides.  Every tensor has element strides
+ *   (batch, seq, head) and a contiguous head_dim; D a multiple of 16.
+ * wgkv_silu_mul -- LlamaMLP's act_fn(gate) * up (:161): rows of `cols`
+ *   bf16 (cols a multiple of 8), gate and up with their own row strides
+ *   (e.g. the two halves of one fused projection), out contiguous.
  * ---------------------------------------------------------------------- */
 int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t res_row_stride,
                   const void* weight, void* out, int64_t out_row_stride, void* residual_out,
                   int64_t res_out_row_stride, int32_t rows, int32_t hidden, float eps, void* stream);
 
-int wgkv_rope_qk(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
-                 const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
-                 const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
-                 void* q_out, void* k_out, int32_t batch, int32_t seq_len,
-                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream);
+int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                  const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                  const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                  const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                  void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                  void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                  void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
+                  int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                  int32_t head_dim, void* stream);
 
-int wgkv_silu_mul(const void* gate, const void* up, void* out, int64_t n, void* stream);
+int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,
+                  void* out, int64_t rows, int32_t cols, void* stream);
 
 #ifdef __cplusplus
 }

@@ -39,6 +39,8 @@ def test_rms_norm(rows, hidden):
 
 @pytest.mark.parametrize("B,S,Hq,Hkv,D", [(1, 1, 32, 8, 128), (1, 300, 8, 2, 64), (2, 17, 4, 4, 128)])
 def test_rope_bit_identical(B, S, Hq, Hkv, D):
+    """q and k rotated bit-identically to apply_rotary_pos_emb; v copied into
+    the same buffer (k and v share strides)."""
     from wgkv import model_ops
     from wgkv.attention import LlamaRotaryEmbedding, apply_rotary_pos_emb
     print(f"[model_ops] rope B{B} S{S} Hq{Hq} Hkv{Hkv} D{D}", flush=True)
@@ -51,14 +53,21 @@ def test_rope_bit_identical(B, S, Hq, Hkv, D):
     pos = torch.arange(1000, 1000 + S, device=DEV)[None].expand(B, S)
     cos, sin = rot(qp, pos)
     rq, rk = apply_rotary_pos_emb(q, k, cos, sin)
-    fq, fk = model_ops.rope_qk(q, k, cos, sin)
-    assert torch.equal(fq, rq) and torch.equal(fk, rk)
+    vp = torch.randn(B, S, Hkv * D, generator=g).to(torch.bfloat16).to(DEV)
+    v = vp.view(B, S, Hkv, D).transpose(1, 2)
+    fq, fk, fv = model_ops.rope_qkv(q, k, v, cos, sin)
+    assert torch.equal(fq, rq) and torch.equal(fk, rk) and torch.equal(fv, v)
+    assert fk.stride() == fv.stride()
 
 
-@pytest.mark.parametrize("n", [14336, 4096 * 8, 96])
-def test_silu_mul_bit_identical(n):
+@pytest.mark.parametrize("rows,cols", [(1, 14336), (8, 4096), (3, 96)])
+def test_silu_mul_bit_identical(rows, cols):
+    """Contiguous inputs and the strided halves of one fused projection."""
     from wgkv import model_ops
-    g = torch.Generator().manual_seed(n)
-    a = (torch.randn(n, generator=g) * 4).to(torch.bfloat16).to(DEV)
-    b = torch.randn(n, generator=g).to(torch.bfloat16).to(DEV)
+    g = torch.Generator().manual_seed(rows * cols)
+    a = (torch.randn(rows, cols, generator=g) * 4).to(torch.bfloat16).to(DEV)
+    b = torch.randn(rows, cols, generator=g).to(torch.bfloat16).to(DEV)
     assert torch.equal(model_ops.silu_mul(a, b), F.silu(a) * b)
+    gu = (torch.randn(rows, 2 * cols, generator=g) * 4).to(torch.bfloat16).to(DEV)
+    ga, ua = gu[:, :cols], gu[:, cols:]
+    assert torch.equal(model_ops.silu_mul(ga, ua), F.silu(ga) * ua)

@@ -92,45 +92,60 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
   }
 }
 
-// ---- rotary embedding of q and k -------------------------------------------
-// Thread = (token, head of q or k, 8 consecutive d of the first half) and the
-// matching 8 of the second half: out[d] = bf16(bf16(x[d] cos[d]) + bf16(-x[d+h] sin[d])),
-// out[d+h] = bf16(bf16(x[d+h] cos[d+h]) + bf16(x[d] sin[d+h])), h = D/2.
+// ---- rotary embedding of q and k (and the copy of v) ------------------------
+// Tensor i (0 = q, 1 = k, 2 = v) has H[i] heads, input and output element
+// strides (batch, seq, head) and a contiguous head_dim.  Thread = (token,
+// head of one of the tensors, 8 consecutive d of the first half) and the
+// matching 8 of the second half.  q and k are rotated:
+// out[d] = bf16(bf16(x[d] cos[d]) + bf16(-x[d+h] sin[d])),
+// out[d+h] = bf16(bf16(x[d+h] cos[d+h]) + bf16(x[d] sin[d+h])), h = D/2;
+// v is copied, so the three outputs can share one buffer and strides.
 struct RopeArgs {
-  const uint16_t* q;
-  int64_t q_sb, q_ss, q_sh;
-  const uint16_t* k;
-  int64_t k_sb, k_ss, k_sh;
+  const uint16_t* in[3];
+  int64_t is[3][3];
+  uint16_t* out[3];
+  int64_t os[3][3];
+  int H[3];
   const uint16_t* cos;
   const uint16_t* sin;
   int64_t cs_sb, cs_ss;
-  uint16_t* qo;
-  uint16_t* ko;
-  int B, S, Hq, Hkv, D;
+  int B, S, D;
 };
 
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int half = a.D / 2, hch = half / 8;
-  const int64_t total = (int64_t)a.B * a.S * (a.Hq + a.Hkv) * hch;
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= total) return;
-  const int c = (int)(i % hch);
-  int64_t r = i / hch;
-  const int hh = (int)(r % (a.Hq + a.Hkv));
-  r /= a.Hq + a.Hkv;
+  const int Ht = a.H[0] + a.H[1] + a.H[2];
+  const int64_t total = (int64_t)a.B * a.S * Ht * hch;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int c = (int)(idx % hch);
+  int64_t r = idx / hch;
+  int hh = (int)(r % Ht);
+  r /= Ht;
   const int s = (int)(r % a.S), b = (int)(r / a.S);
-  const bool isq = hh < a.Hq;
-  const int head = isq ? hh : hh - a.Hq;
-  const uint16_t* src = isq ? a.q + b * a.q_sb + s * a.q_ss + head * a.q_sh
-                            : a.k + b * a.k_sb + s * a.k_ss + head * a.k_sh;
-  const int H = isq ? a.Hq : a.Hkv;
-  uint16_t* dst = (isq ? a.qo : a.ko) + (((int64_t)b * a.S + s) * H + head) * a.D;
+  int ten = 0;
+  if (hh >= a.H[0]) {
+    hh -= a.H[0];
+    ten = 1;
+    if (hh >= a.H[1]) {
+      hh -= a.H[1];
+      ten = 2;
+    }
+  }
+  const uint16_t* src = a.in[ten] + b * a.is[ten][0] + s * a.is[ten][1] + hh * a.is[ten][2];
+  uint16_t* dst = a.out[ten] + b * a.os[ten][0] + s * a.os[ten][1] + hh * a.os[ten][2];
+  const int d0 = c * 8;
+  const u32x4_t w1 = *(const u32x4_t*)(src + d0), w2 = *(const u32x4_t*)(src + half + d0);
+  if (ten == 2) {
+    *(u32x4_t*)(dst + d0) = w1;
+    *(u32x4_t*)(dst + half + d0) = w2;
+    return;
+  }
   const uint16_t* cs = a.cos + b * a.cs_sb + s * a.cs_ss;
   const uint16_t* sn = a.sin + b * a.cs_sb + s * a.cs_ss;
-  const int d0 = c * 8;
   float x1[8], x2[8], c1[8], c2[8], s1[8], s2[8], o1[8], o2[8];
-  unpack8(*(const u32x4_t*)(src + d0), x1);
-  unpack8(*(const u32x4_t*)(src + half + d0), x2);
+  unpack8(w1, x1);
+  unpack8(w2, x2);
   unpack8(*(const u32x4_t*)(cs + d0), c1);
   unpack8(*(const u32x4_t*)(cs + half + d0), c2);
   unpack8(*(const u32x4_t*)(sn + d0), s1);
@@ -145,16 +160,20 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
 }
 
 // ---- SwiGLU: out = bf16(bf16(silu(g)) * u) ----------------------------------
-__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, const uint16_t* u, uint16_t* out,
-                                                       int64_t n8) {
+// rows of `cols` elements; g and u with their own row strides, out contiguous
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_t g_rs, const uint16_t* u,
+                                                       int64_t u_rs, uint16_t* out, int64_t rows, int cols) {
+  const int c8 = cols / 8;
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n8) return;
+  if (i >= rows * c8) return;
+  const int64_t row = i / c8;
+  const int c = (int)(i - row * c8) * 8;
   float gv[8], uv[8], o[8];
-  unpack8(*(const u32x4_t*)(g + i * 8), gv);
-  unpack8(*(const u32x4_t*)(u + i * 8), uv);
+  unpack8(*(const u32x4_t*)(g + row * g_rs + c), gv);
+  unpack8(*(const u32x4_t*)(u + row * u_rs + c), uv);
 #pragma unroll
   for (int e = 0; e < 8; ++e) o[e] = rb(gv[e] / (1.0f + expf(-gv[e]))) * uv[e];
-  *(u32x4_t*)(out + i * 8) = pack8(o);
+  *(u32x4_t*)(out + row * (int64_t)cols + c) = pack8(o);
 }
 
 bool misaligned(const void* p) { return ((uintptr_t)p & 15) != 0; }
@@ -181,31 +200,62 @@ extern "C" int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* re
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_rope_qk(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
-                            const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
-                            const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
-                            void* q_out, void* k_out, int32_t batch, int32_t seq_len,
-                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream) {
-  if (!q || !k || !cos || !sin || !q_out || !k_out) return WGKV_ERR_ARG;
+extern "C" int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                             const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                             const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                             const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                             void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                             void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                             void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
+                             int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, void* stream) {
+  if (!q || !k || !cos || !sin || !q_out || !k_out || (v == nullptr) != (v_out == nullptr)) return WGKV_ERR_ARG;
   if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0 || num_kv_heads <= 0) return WGKV_ERR_ARG;
   if (head_dim % 16) return WGKV_ERR_UNSUPPORTED;
-  if (misaligned(q) || misaligned(k) || misaligned(cos) || misaligned(sin) || misaligned(q_out) || misaligned(k_out))
+  if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(cos) || misaligned(sin) || misaligned(q_out) ||
+      misaligned(k_out) || misaligned(v_out))
     return WGKV_ERR_UNSUPPORTED;
-  if ((q_sb | q_ss | q_sh | k_sb | k_ss | k_sh | cs_sb | cs_ss) & 7) return WGKV_ERR_UNSUPPORTED;
-  RopeArgs a = {(const uint16_t*)q, q_sb, q_ss, q_sh, (const uint16_t*)k, k_sb, k_ss, k_sh,
-                (const uint16_t*)cos, (const uint16_t*)sin, cs_sb, cs_ss, (uint16_t*)q_out, (uint16_t*)k_out,
-                batch, seq_len, num_q_heads, num_kv_heads, head_dim};
-  const int64_t total = (int64_t)batch * seq_len * (num_q_heads + num_kv_heads) * (head_dim / 16);
+  if ((q_sb | q_ss | q_sh | k_sb | k_ss | k_sh | v_sb | v_ss | v_sh | cs_sb | cs_ss | qo_sb | qo_ss | qo_sh | ko_sb |
+       ko_ss | ko_sh | vo_sb | vo_ss | vo_sh) & 7)
+    return WGKV_ERR_UNSUPPORTED;
+  RopeArgs a = {};
+  a.in[0] = (const uint16_t*)q;
+  a.in[1] = (const uint16_t*)k;
+  a.in[2] = (const uint16_t*)v;
+  a.out[0] = (uint16_t*)q_out;
+  a.out[1] = (uint16_t*)k_out;
+  a.out[2] = (uint16_t*)v_out;
+  const int64_t is[3][3] = {{q_sb, q_ss, q_sh}, {k_sb, k_ss, k_sh}, {v_sb, v_ss, v_sh}};
+  const int64_t os[3][3] = {{qo_sb, qo_ss, qo_sh}, {ko_sb, ko_ss, ko_sh}, {vo_sb, vo_ss, vo_sh}};
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      a.is[i][j] = is[i][j];
+      a.os[i][j] = os[i][j];
+    }
+  a.H[0] = num_q_heads;
+  a.H[1] = num_kv_heads;
+  a.H[2] = v ? num_kv_heads : 0;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.cs_sb = cs_sb;
+  a.cs_ss = cs_ss;
+  a.B = batch;
+  a.S = seq_len;
+  a.D = head_dim;
+  const int64_t total = (int64_t)batch * seq_len * (a.H[0] + a.H[1] + a.H[2]) * (head_dim / 16);
   hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_silu_mul(const void* gate, const void* up, void* out, int64_t n, void* stream) {
-  if (!gate || !up || !out || n < 0) return WGKV_ERR_ARG;
-  if (n % 8 || misaligned(gate) || misaligned(up) || misaligned(out)) return WGKV_ERR_UNSUPPORTED;
-  if (n == 0) return WGKV_OK;
-  const int64_t n8 = n / 8;
+extern "C" int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,
+                             void* out, int64_t rows, int32_t cols, void* stream) {
+  if (!gate || !up || !out || rows < 0 || cols <= 0) return WGKV_ERR_ARG;
+  if (cols % 8 || misaligned(gate) || misaligned(up) || misaligned(out) || (gate_row_stride | up_row_stride) & 7)
+    return WGKV_ERR_UNSUPPORTED;
+  if (rows == 0) return WGKV_OK;
+  const int64_t n8 = rows * (cols / 8);
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)gate, (const uint16_t*)up, (uint16_t*)out, n8);
+                     (const uint16_t*)gate, gate_row_stride, (const uint16_t*)up, up_row_stride, (uint16_t*)out,
+                     rows, cols);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

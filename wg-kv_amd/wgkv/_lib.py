@@ -99,10 +99,11 @@ SIGNATURES = {
     "wgkv_gate_workspace_bytes": (ctypes.c_int64, [c_i32, c_i32, c_i32]),
     "wgkv_rms_norm": (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr, c_i64,
                                      c_i32, c_i32, c_f32, c_ptr]),
-    "wgkv_rope_qk": (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,
-                                    c_ptr, c_ptr, c_i64, c_i64, c_ptr, c_ptr,
-                                    c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr]),
-    "wgkv_silu_mul": (ctypes.c_int, [c_ptr, c_ptr, c_ptr, c_i64, c_ptr]),
+    "wgkv_rope_qkv": (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,
+                                     c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64,
+                                     c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,
+                                     c_ptr, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr]),
+    "wgkv_silu_mul": (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i32, c_ptr]),
     "wgkv_sparse_prefill_attn": (ctypes.c_int, [
         c_ptr, c_i64, c_i64, c_i64,
         c_ptr, c_ptr, c_i64, c_i64, c_i64,

@@ -92,23 +92,47 @@ class LlamaAttention(nn.Module):
         self.chunk_prefill_kernel = ops.chunk_attend  # prompt chunks after the first (no reference counterpart)
         self.decode_kernel_handle = torch_ops.paged_decode_attn_handle  # torch.ops.wgkv.paged_decode_attn
         self.decode_kernel_executor = lambda func: func()
+        self._qkv_weight = None
+
+    @torch.no_grad()
+    def fuse_qkv(self):
+        """Put q_proj, k_proj and v_proj's weights into one (Nq+2Nk, hidden)
+        buffer (the parameters become views of it, names and values kept), so
+        the forward projects q, k and v with one GEMM.  Not for biased
+        projections."""
+        if self._qkv_weight is not None or self.q_proj.bias is not None:
+            return
+        w = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight], dim=0)
+        nq, nk = self.q_proj.weight.shape[0], self.k_proj.weight.shape[0]
+        self.q_proj.weight = nn.Parameter(w[:nq], requires_grad=False)
+        self.k_proj.weight = nn.Parameter(w[nq:nq + nk], requires_grad=False)
+        self.v_proj.weight = nn.Parameter(w[nq + nk:], requires_grad=False)
+        self._qkv_weight = w
 
     def forward(self, gating_mode, hidden_states, position_embeddings, attention_mask=None, past_key_value=None,
                 cache_position=None, **kwargs):
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
-        q = self.q_proj(hidden_states).view(hidden_shape)
-        k = self.k_proj(hidden_states).view(hidden_shape)
+        if self._qkv_weight is not None and self._qkv_weight.device == hidden_states.device:
+            nq, nk = self.q_proj.weight.shape[0], self.k_proj.weight.shape[0]
+            qkv = torch.nn.functional.linear(hidden_states, self._qkv_weight)
+            q = qkv[..., :nq].view(hidden_shape)
+            k = qkv[..., nq:nq + nk].view(hidden_shape)
+            v_src = qkv[..., nq + nk:]
+        else:
+            q = self.q_proj(hidden_states).view(hidden_shape)
+            k = self.k_proj(hidden_states).view(hidden_shape)
+            v_src = None
         if self.qk_norm:
             q, k = self.q_norm(q), self.k_norm(k)
         q = q.transpose(1, 2)
         k = k.transpose(1, 2)
-        v = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        v = (v_src if v_src is not None else self.v_proj(hidden_states)).view(hidden_shape).transpose(1, 2)
         pre_key = k if "pre_k" in self.config.g_inputs else None
         cos, sin = position_embeddings
-        if (model_ops.usable(q, k, cos, sin) and self.head_dim % 16 == 0 and q.stride(3) == 1 and k.stride(3) == 1
-                and cos.dim() == 3):
-            q, k = model_ops.rope_qk(q, k, cos, sin)  # one launch, the same bf16 rounding
+        if (model_ops.usable(q, k, v, cos, sin) and self.head_dim % 16 == 0 and q.stride(3) == 1
+                and k.stride(3) == 1 and v.stride(3) == 1 and cos.dim() == 3):
+            q, k, v = model_ops.rope_qkv(q, k, v, cos, sin)  # one launch, the same bf16 rounding; v copied beside k
         else:
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
         out, attn_weights, g_scores = self.self_attn_forward_patch(

@@ -40,26 +40,38 @@ def rms_norm(x, weight, eps, residual=None):
     return out.view(x.shape), None if ores is None else ores.view(x.shape)
 
 
-def rope_qk(q, k, cos, sin):
-    """q (B,H,S,D), k (B,Hkv,S,D) views (d contiguous), cos/sin (B,S,D) ->
-    rotated (q, k) as (B,H,S,D) views of contiguous (B,S,H,D) tensors."""
+def rope_qkv(q, k, v, cos, sin):
+    """q (B,Hq,S,D), k / v (B,Hkv,S,D) views (d contiguous), cos/sin (B,S,D)
+    -> (rotated q, rotated k, v) as (B,H,S,D) views of one contiguous
+    (B, S, Hq+2*Hkv, D) buffer, so k and v share strides."""
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     if cos.stride(-1) != 1:
         cos, sin = cos.contiguous(), sin.contiguous()
-    qo = torch.empty(B, S, Hq, D, dtype=q.dtype, device=q.device)
-    ko = torch.empty(B, S, Hkv, D, dtype=k.dtype, device=k.device)
-    st = _lib.lib().wgkv_rope_qk(
-        _ptr(q), q.stride(0), q.stride(2), q.stride(1), _ptr(k), k.stride(0), k.stride(2), k.stride(1),
-        _ptr(cos), _ptr(sin), cos.stride(0), cos.stride(1), _ptr(qo), _ptr(ko), B, S, Hq, Hkv, D,
-        _lib.stream_handle(q.device))
-    _lib.check(st, "wgkv_rope_qk")
-    return qo.transpose(1, 2), ko.transpose(1, 2)
+    buf = torch.empty(B, S, Hq + 2 * Hkv, D, dtype=q.dtype, device=q.device)
+    qo, ko, vo = buf[:, :, :Hq], buf[:, :, Hq:Hq + Hkv], buf[:, :, Hq + Hkv:]
+
+    def st(t):  # (batch, seq, head) strides of a (B, H, S, D) view
+        return t.stride(0), t.stride(2), t.stride(1)
+
+    def so(t):  # of a (B, S, H, D) view
+        return t.stride(0), t.stride(1), t.stride(2)
+
+    r = _lib.lib().wgkv_rope_qkv(
+        _ptr(q), *st(q), _ptr(k), *st(k), _ptr(v), *st(v), _ptr(cos), _ptr(sin), cos.stride(0), cos.stride(1),
+        _ptr(qo), *so(qo), _ptr(ko), *so(ko), _ptr(vo), *so(vo), B, S, Hq, Hkv, D, _lib.stream_handle(q.device))
+    _lib.check(r, "wgkv_rope_qkv")
+    return qo.transpose(1, 2), ko.transpose(1, 2), vo.transpose(1, 2)
 
 
 def silu_mul(gate, up):
-    """bf16(bf16(silu(gate)) * up) for contiguous tensors of the same shape."""
-    out = torch.empty_like(gate)
-    st = _lib.lib().wgkv_silu_mul(_ptr(gate), _ptr(up), _ptr(out), gate.numel(), _lib.stream_handle(gate.device))
+    """bf16(bf16(silu(gate)) * up) over the last dim for same-shape tensors
+    whose rows may be strided (the halves of one fused projection); returns
+    a contiguous tensor."""
+    g2, u2 = _as_rows(gate), _as_rows(up)
+    rows, cols = g2.shape
+    out = torch.empty(gate.shape, dtype=gate.dtype, device=gate.device)
+    st = _lib.lib().wgkv_silu_mul(_ptr(g2), g2.stride(0), _ptr(u2), u2.stride(0), _ptr(out), rows, cols,
+                                  _lib.stream_handle(gate.device))
     _lib.check(st, "wgkv_silu_mul")
     return out
