@@ -196,6 +196,13 @@ int wgkv_decode_append_ring(
  * clamp_min > 0 applies the conv path's clamp (:205).  Outputs (may be NULL,
  * not both): scores f32 (B,H,S), mask u8 (B,H,S) = scores > threshold.
  * Supported: D in {64,128}, inner a multiple of 16, n_in*D <= 384.
+ * w1_packed (may be NULL): the same weights as written by
+ * wgkv_gate_pack_weights.  With bf16 inputs (16-byte aligned, strides
+ * multiples of 8 elements) and seq_len > 4 the first layer then runs on the
+ * bf16 matrix core: the norm weights are folded into w1 in fp32 and the
+ * product split into three bf16 planes that carry all its bits, so the
+ * result equals the fp32 layer up to rounding order.  Otherwise ignored
+ * (w1 and the norm weights are always read by the other paths).
  * workspace (may be NULL): for seq_len <= 4 (decode steps) the hidden
  * columns of each head are split over several workgroups whose partial
  * logits meet in the workspace; it must hold wgkv_gate_workspace_bytes()
@@ -215,8 +222,23 @@ int wgkv_gate_scores(
     int32_t act, int32_t rms, float clamp_min, float threshold,
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
+    const void* w1_packed,
     void* workspace, int64_t workspace_bytes,
     void* stream);
+
+/* Packed first-layer weights of the gate (no reference counterpart: a
+ * one-time layout of GatingPredictor's conv1.weight and norm weights,
+ * src/modeling_layers.py:134-161, for the bf16 matrix-core path above).
+ * wgkv_gate_packed_bytes: size for in_features = n_in * head_dim (a multiple
+ * of 32) and inner (a multiple of 16), or -1.  wgkv_gate_pack_weights writes
+ * w_norm_i[d] * w1[h*inner + j][i*D + d] (norm weights only with rms != 0)
+ * as three bf16 planes hi + mid + lo; inputs_mask and rms as for
+ * wgkv_gate_scores.  Repack after the weights change. */
+int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, int32_t in_features);
+int wgkv_gate_pack_weights(
+    const float* w_pre, const float* w_post, const float* w_v, int32_t inputs_mask, int32_t rms,
+    const float* w1, int32_t num_kv_heads, int32_t head_dim, int32_t inner,
+    void* packed, int64_t packed_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Sparse (vertical-slash) causal prefill attention.

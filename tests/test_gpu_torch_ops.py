@@ -38,12 +38,18 @@ def test_ops_equal_direct_calls():
     gp = GatingPredictor(D, Hkv, ["pre_k", "post_k"], "gelu", 4.0, 1e-3, True, True).to(DEV)
     x1 = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16).to(DEV)
     x2 = torch.randn(B, Hkv, S, D, generator=g).to(torch.bfloat16).to(DEV)
-    s1, m1 = gp.scores_and_mask(x1, x2, None, 0.5)
-    s2, m2 = torch.ops.wgkv.gate_scores_and_mask(
-        x1, x2, None, gp.pre_key_norm.weight.detach(), gp.post_key_norm.weight.detach(), None,
-        gp.conv1.weight.detach(), gp.conv1.bias.detach(), gp.conv2.weight.detach(), gp.conv2.bias.detach(),
-        gp.inner_dim, 0, True, 0.0, 0.5)
+    s1, m1 = gp.scores_and_mask(x1, x2, None, 0.5)  # bf16 inputs, 700 tokens: the packed path
+    wn = (gp.pre_key_norm.weight.detach(), gp.post_key_norm.weight.detach(), None)
+    packed = torch.ops.wgkv.gate_pack_weights(*wn, gp.conv1.weight.detach(), 3, True, Hkv, D, gp.inner_dim)
+    assert torch.equal(packed, gp.packed_weights())
+    args = (x1, x2, None, *wn, gp.conv1.weight.detach(), gp.conv1.bias.detach(), gp.conv2.weight.detach(),
+            gp.conv2.bias.detach(), gp.inner_dim, 0, True, 0.0, 0.5)
+    s2, m2 = torch.ops.wgkv.gate_scores_and_mask(*args, w1_packed=packed)
     assert torch.equal(s1, s2) and torch.equal(m1, m2)
+    # without packed weights: the fp32 path, as the module function runs it
+    s3, m3 = torch.ops.wgkv.gate_scores_and_mask(*args)
+    s4, m4 = wgkv.gate.gate_scores_and_mask(*args)
+    assert torch.equal(s3, s4) and torch.equal(m3, m4)
 
 
 def test_compiled_graph_through_the_operators():

@@ -7,7 +7,8 @@ import torch
 
 def test_registered_with_schemas():
     import wgkv  # noqa: F401  (registers the operators)
-    names = {"sparse_attn", "paged_decode_attn", "generate_sparse_indices", "gate_scores_and_mask"}
+    names = {"sparse_attn", "paged_decode_attn", "generate_sparse_indices", "gate_scores_and_mask",
+             "gate_pack_weights"}
     for n in names:
         op = getattr(torch.ops.wgkv, n)
         schema = str(op.default._schema)
@@ -43,6 +44,25 @@ def test_meta_shapes(S, W):
     x = torch.empty(B, Hkv, S, D, dtype=torch.bfloat16, **meta)
     sc, mk = torch.ops.wgkv.gate_scores_and_mask(x, x, None, wn, wn, None, w1, b1, w2, b2, inner, 0, True, 0.0, 0.1)
     assert sc.shape == (B, Hkv, S) and sc.dtype == torch.float32 and mk.dtype == torch.bool
+    pk = torch.ops.wgkv.gate_pack_weights(wn, wn, None, w1, 3, True, Hkv, D, inner)
+    sc2, _ = torch.ops.wgkv.gate_scores_and_mask(x, x, None, wn, wn, None, w1, b1, w2, b2, inner, 0, True, 0.0, 0.1,
+                                                 w1_packed=pk)
+    assert sc2.shape == sc.shape
+
+
+@pytest.mark.parametrize("H,D,inner,n_in", [(8, 128, 512, 2), (2, 64, 96, 3), (8, 128, 192, 1), (4, 64, 256, 2)])
+def test_pack_meta_size_is_the_library_size(H, D, inner, n_in):
+    """The Meta kernel of gate_pack_weights allocates what
+    wgkv_gate_packed_bytes (a host function of the library) asks for."""
+    import wgkv
+    w1 = torch.empty(H * inner, n_in * D, 1, device="meta")
+    wn = torch.empty(D, device="meta")
+    mask = (1 << n_in) - 1
+    pk = torch.ops.wgkv.gate_pack_weights(wn, wn, wn, w1, mask, True, H, D, inner)
+    assert pk.dtype == torch.uint8 and pk.numel() == wgkv._lib.lib().wgkv_gate_packed_bytes(H, inner, n_in * D)
+    # shapes the packed layout does not take
+    assert wgkv._lib.lib().wgkv_gate_packed_bytes(H, 100, 2 * D) == -1
+    assert wgkv._lib.lib().wgkv_gate_packed_bytes(H, inner, 48) == -1
 
 
 def test_prefill_swap_point_contract():

@@ -56,6 +56,33 @@ __device__ __forceinline__ float round_bf16(float x) {
 __device__ __forceinline__ float gelu_erf(float z) { return 0.5f * z * (1.0f + erff(z * 0.70710678118654752f)); }
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
 
+// End of a 64-token tile: lane (n, kq) holds partial logits of tokens
+// mt*16 + 4*kq + i over its columns; sum over the 16 lanes of each row, then
+// over the 4 waves, and apply b2, sigmoid, clamp and threshold.
+__device__ __forceinline__ void finish_tile(const GateArgs& a, const float (&logit)[4][4], float (*s_part)[kTok],
+                                            int lane, int wid, int b, int h, int s0) {
+  const int n = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = row_sum16(logit[mt][i]);
+      if (n == 0) s_part[wid][mt * 16 + 4 * kq + i] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < kTok) {
+    const int m = threadIdx.x;
+    const int s = s0 + m;
+    if (s < a.S) {
+      const float z = ((s_part[0][m] + s_part[1][m]) + (s_part[2][m] + s_part[3][m])) + a.b2[h];
+      float g = 1.0f / (1.0f + expf(-z));
+      if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+      if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
+      if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
+    }
+  }
+}
+
 template <int K>  // n_in * D
 __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
   constexpr int LDX = K + 4;  // padded row (floats)
@@ -174,26 +201,7 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
         }
     }
   }
-  // sum over the 16 columns held by the lanes of each row, then over waves
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float v = row_sum16(logit[mt][i]);
-      if (n == 0) s_part[wid][mt * 16 + 4 * kq + i] = v;
-    }
-  __syncthreads();
-  if (threadIdx.x < kTok) {
-    const int m = threadIdx.x;
-    const int s = s0 + m;
-    if (s < a.S) {
-      const float z = ((s_part[0][m] + s_part[1][m]) + (s_part[2][m] + s_part[3][m])) + a.b2[h];
-      float g = 1.0f / (1.0f + expf(-z));
-      if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
-      if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
-      if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
-    }
-  }
+  finish_tile(a, logit, s_part, lane, wid, b, h, s0);
 }
 
 // Few tokens (decode steps, S <= kSmallTok).  The hidden columns of a head
@@ -360,6 +368,193 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   if (t < nt) finish(t, z);
 }
 
+// ---- bf16 inputs on the bf16 matrix core --------------------------------
+// With bf16 inputs each normalised row y = bf16(x * rsqrt(mean(x^2) + eps))
+// is exact in bf16, and the first layer is sum_d y_d * (w_norm_d * W1[j][d]).
+// The folded fp32 weights f = w_norm * W1 are split once into three bf16
+// planes, f = hi + mid + lo, each the round-to-nearest-even bf16 of what the
+// previous planes leave (the remainders are exact in fp32, so the planes
+// carry all 24 significand bits of f); a product y_d * plane is exact in
+// fp32 and the matrix core accumulates the three products in fp32, so the
+// layer costs three bf16 MFMAs where fp32 MFMAs would take eight times the
+// cycles of one.
+// Packed layout, bf16: [head][16-column tile][32-input k-step][plane][lane][8]
+// -- the B operand of v_mfma_f32_16x16x32_bf16, lane kg*16 + n holding
+// column n and inputs 8*kg .. 8*kg+7 -- so one wave load reads 1 KB.
+constexpr int kPlanes = 3;
+
+__global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0, const float* wn1,
+                                 const float* wn2, int H, int inner, int D, int n_in, u32x4_t* __restrict__ packed) {
+  const int K = n_in * D, NT = inner / 16, KS = K / 32;
+  const int64_t total = (int64_t)H * NT * KS * 64;
+  for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total; id += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(id % 64);
+    int64_t rest = id / 64;
+    const int ks = (int)(rest % KS);
+    rest /= KS;
+    const int nt = (int)(rest % NT);
+    const int h = (int)(rest / NT);
+    const int col = nt * 16 + (lane & 15), k0 = ks * 32 + (lane >> 4) * 8;
+    uint32_t w[kPlanes][4];
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) {
+      uint16_t pl[kPlanes][2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int k = k0 + e + u, i = k / D, d = k - i * D;
+        const float* wn = i == 0 ? wn0 : i == 1 ? wn1 : wn2;
+        const float f = w1[((int64_t)h * inner + col) * K + k] * (wn ? wn[d] : 1.f);
+        const uint16_t hi = f32_to_bf16(f);
+        const float r1 = f - bf16lo(hi);
+        const uint16_t mid = f32_to_bf16(r1);
+        const uint16_t lo = f32_to_bf16(r1 - bf16lo(mid));
+        pl[0][u] = hi;
+        pl[1][u] = mid;
+        pl[2][u] = lo;
+      }
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p) w[p][e / 2] = (uint32_t)pl[p][0] | ((uint32_t)pl[p][1] << 16);
+    }
+    u32x4_t* dst = packed + (((int64_t)(h * NT + nt) * KS + ks) * kPlanes) * 64 + lane;
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) dst[p * 64] = (u32x4_t){w[p][0], w[p][1], w[p][2], w[p][3]};
+  }
+}
+
+// One workgroup = 64 tokens of one (batch, KV head), as gate_kernel.  The
+// inputs are read 16 bytes per lane (a wave load covers 64 / (D/8) rows), the
+// row norms reduced over the D/8 lanes of a row, and y goes to LDS as bf16
+// (rows padded by 16 bytes: the 16 rows of a fragment read start 16 bytes
+// apart modulo 256).  Wave w takes 16-column tiles w, w+4, ... in groups of
+// four; per 32-input k-step it reads the four 64-token A fragments from LDS
+// and the 4 x 3 packed B fragments of the next k-step from global memory.
+// Two waves per SIMD (two workgroups per CU) hide each other's loads and
+// GELU epilogues.
+template <int D, int NIN>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_bf16_kernel(GateArgs a, const u32x4_t* __restrict__ packed) {
+  constexpr int K = NIN * D;
+  constexpr int KS = K / 32;
+  constexpr int LDY = K + 8;     // LDS row stride (bf16)
+  constexpr int LPR = D / 8;     // lanes per input row
+  constexpr int RPL = 64 / LPR;  // rows per wave load
+  constexpr int NLD = 16 / RPL;  // wave loads per input for the wave's 16 tokens
+  __shared__ __attribute__((aligned(16))) uint16_t ys[kTok * LDY];
+  __shared__ float s_part[4][kTok];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nbh = a.B * a.H;
+  const int lid = blockIdx.x + blockIdx.y * gridDim.x;  // XCD-aware order, as gate_kernel
+  const int bh = lid % nbh, tile = lid / nbh;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int s0 = tile * kTok;
+
+  // ---- normalised inputs -> LDS (bf16) ------------------------------------
+  {
+    const int c = lane % LPR;
+    u32x4_t v[NIN][NLD];
+#pragma unroll
+    for (int i = 0; i < NIN; ++i)
+#pragma unroll
+      for (int u = 0; u < NLD; ++u) {
+        const int s = min(s0 + wid * 16 + u * RPL + lane / LPR, a.S - 1);  // rows past S are computed and discarded
+        const uint16_t* row = (const uint16_t*)a.in[i] + (int64_t)b * a.sb[i] + (int64_t)h * a.sh[i] + (int64_t)s * a.ss[i];
+        v[i][u] = *(const u32x4_t*)(row + c * 8);
+      }
+#pragma unroll
+    for (int i = 0; i < NIN; ++i)
+#pragma unroll
+      for (int u = 0; u < NLD; ++u) {
+        u32x4_t y = v[i][u];
+        if (a.rms) {
+          float f[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            f[2 * e] = bf16lo(y[e]);
+            f[2 * e + 1] = bf16hi(y[e]);
+          }
+          float ss = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+          ss += dpp_f32<WGKV_DPP_QP_1032>(ss);
+          ss += dpp_f32<WGKV_DPP_QP_2301>(ss);
+          ss += dpp_f32<WGKV_DPP_ROW_HALF_MIRROR>(ss);
+          if (LPR == 16) ss += dpp_f32<WGKV_DPP_ROW_MIRROR>(ss);
+          const float scale = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(f[2 * e] * scale, f[2 * e + 1] * scale);  // cast back to bf16 (:128)
+        }
+        const int m = wid * 16 + u * RPL + lane / LPR;
+        *(u32x4_t*)(&ys[m * LDY + i * D + c * 8]) = y;
+      }
+  }
+  __syncthreads();
+
+  // ---- y @ (w_norm * W1[h])^T: three bf16 MFMAs per k-step and tile pair --
+  const int n = lane & 15, kg = lane >> 4;
+  const int ntot = a.inner / 16;
+  const u32x4_t* ph = packed + (int64_t)h * ntot * KS * kPlanes * 64 + lane;
+  const float* b1h = a.b1 + (int64_t)h * a.inner;
+  const float* w2h = a.w2 + (int64_t)h * a.inner;
+  float logit[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) logit[mt][i] = 0.f;
+  for (int t0 = wid; t0 < ntot; t0 += 16) {
+    int tj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) tj[j] = t0 + 4 * j < ntot ? t0 + 4 * j : t0;  // out-of-range tiles recompute t0, skipped below
+    f32x4_t c[4][4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) c[mt][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    u32x4_t bw[4][kPlanes];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p) bw[j][p] = ph[((int64_t)tj[j] * KS * kPlanes + p) * 64];
+#pragma unroll 2
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4_t bn[4][kPlanes];
+      if (ks + 1 < KS)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int p = 0; p < kPlanes; ++p) bn[j][p] = ph[(((int64_t)tj[j] * KS + ks + 1) * kPlanes + p) * 64];
+      bf16x8_t ax[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        ax[mt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&ys[(mt * 16 + n) * LDY + ks * 32 + kg * 8]));
+#pragma unroll
+      for (int p = kPlanes - 1; p >= 0; --p)  // smallest plane first
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            c[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt], __builtin_bit_cast(bf16x8_t, bw[j][p]), c[mt][j], 0, 0, 0);
+      if (ks + 1 < KS)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+          for (int p = 0; p < kPlanes; ++p) bw[j][p] = bn[j][p];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if (t0 + 4 * j >= ntot) break;
+      const int col = tj[j] * 16 + n;
+      const float bias = b1h[col], wo = w2h[col];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float z = c[mt][j][i] + bias;
+          logit[mt][i] = fmaf(wo, a.act ? silu(z) : gelu_erf(z), logit[mt][i]);
+        }
+    }
+  }
+  finish_tile(a, logit, s_part, lane, wid, b, h, s0);
+}
+
 template <int K>
 void launch_gate(const GateArgs& a, hipStream_t st) {
   if (a.S <= kSmallTok) {
@@ -392,6 +587,7 @@ extern "C" int wgkv_gate_scores(
     int32_t act, int32_t rms, float clamp_min, float threshold,
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
+    const void* w1_packed,
     void* workspace, int64_t workspace_bytes,
     void* stream) {
   if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0) return WGKV_ERR_ARG;
@@ -447,6 +643,28 @@ extern "C" int wgkv_gate_scores(
   if (((uintptr_t)w1 & 15) != 0) return WGKV_ERR_UNSUPPORTED;
   const int K = n_in * head_dim;
   hipStream_t st = (hipStream_t)stream;
+  if (w1_packed && in_dtype == 0 && seq_len > kSmallTok) {
+    // the packed path reads 16-byte input slices
+    bool aligned = ((uintptr_t)w1_packed & 15) == 0;
+    for (int i = 0; i < n_in; ++i)
+      aligned = aligned && ((uintptr_t)a.in[i] & 15) == 0 && ((a.sb[i] | a.sh[i] | a.ss[i]) & 7) == 0;
+    if (aligned) {
+      const u32x4_t* pk = (const u32x4_t*)w1_packed;
+      const dim3 grid((seq_len + kTok - 1) / kTok, batch * num_kv_heads);
+#define WGKV_GATE_BF16(DD, NN) hipLaunchKernelGGL((gate_bf16_kernel<DD, NN>), grid, dim3(kThreads), 0, st, a, pk)
+      if (head_dim == 128) {
+        if (n_in == 1) WGKV_GATE_BF16(128, 1);
+        else if (n_in == 2) WGKV_GATE_BF16(128, 2);
+        else WGKV_GATE_BF16(128, 3);
+      } else {
+        if (n_in == 1) WGKV_GATE_BF16(64, 1);
+        else if (n_in == 2) WGKV_GATE_BF16(64, 2);
+        else WGKV_GATE_BF16(64, 3);
+      }
+#undef WGKV_GATE_BF16
+      return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+    }
+  }
   switch (K) {
     case 64: launch_gate<64>(a, st); break;
     case 128: launch_gate<128>(a, st); break;
@@ -455,5 +673,35 @@ extern "C" int wgkv_gate_scores(
     case 384: launch_gate<384>(a, st); break;
     default: return WGKV_ERR_UNSUPPORTED;
   }
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, int32_t in_features) {
+  if (num_kv_heads <= 0 || inner <= 0 || inner % 16 || in_features <= 0 || in_features % 32) return -1;
+  return (int64_t)num_kv_heads * inner * in_features * kPlanes * 2;
+}
+
+extern "C" int wgkv_gate_pack_weights(
+    const float* w_pre, const float* w_post, const float* w_v, int32_t inputs_mask, int32_t rms,
+    const float* w1, int32_t num_kv_heads, int32_t head_dim, int32_t inner,
+    void* packed, int64_t packed_bytes, void* stream) {
+  if (!w1 || !packed || num_kv_heads <= 0) return WGKV_ERR_ARG;
+  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (inner <= 0 || inner % 16) return WGKV_ERR_UNSUPPORTED;
+  const float* wn_all[3] = {w_pre, w_post, w_v};
+  const float* wn[3] = {nullptr, nullptr, nullptr};
+  int n_in = 0;
+  for (int i = 0; i < 3; ++i) {
+    if (!(inputs_mask >> i & 1)) continue;
+    if (rms && !wn_all[i]) return WGKV_ERR_ARG;
+    wn[n_in++] = rms ? wn_all[i] : nullptr;
+  }
+  if (n_in == 0) return WGKV_ERR_ARG;
+  if (packed_bytes < wgkv_gate_packed_bytes(num_kv_heads, inner, n_in * head_dim)) return WGKV_ERR_ARG;
+  if (((uintptr_t)packed & 15) != 0) return WGKV_ERR_UNSUPPORTED;
+  const int64_t total = (int64_t)num_kv_heads * (inner / 16) * (n_in * head_dim / 32) * 64;
+  const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
+  hipLaunchKernelGGL(gate_pack_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, w1, wn[0], wn[1], wn[2],
+                     num_kv_heads, inner, head_dim, n_in, (u32x4_t*)packed);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

@@ -5,7 +5,10 @@ Parameter names and shapes are GatingPredictor's (src/modeling_layers.py:
 ``.post_key_norm.weight``, ``.conv1.{weight,bias}``, ``.conv2.{weight,bias}``)
 load with ``load_state_dict``.  The forward runs the HIP kernel
 ``wgkv_gate_scores`` (fp32 arithmetic, fp32 scores); bf16 parameters are
-widened to fp32 copies before the call.
+widened to fp32 copies before the call.  For bf16 inputs of more than four
+tokens the first layer runs on the bf16 matrix core from a packed copy of
+conv1.weight with the norm weights folded in (three bf16 planes that carry
+the fp32 product exactly), made once per device and weight version.
 """
 import torch
 import torch.nn as nn
@@ -70,20 +73,43 @@ class GatingPredictor(nn.Module):
         cache[key] = (p._version, c)
         return c
 
+    def _norm_weights(self):
+        norms = [self.pre_key_norm, self.post_key_norm, self.value_norm]
+        return [self._f32(m.weight) if isinstance(m, GatingRMSNorm) else None for m in norms]
+
+    def packed_weights(self):
+        """Packed first-layer weights (wgkv_gate_pack_weights) for the bf16
+        matrix-core path, cached per device and remade when conv1.weight or a
+        norm weight changes version."""
+        params = [self.conv1.weight] + [m.weight for m in (self.pre_key_norm, self.post_key_norm, self.value_norm)
+                                        if isinstance(m, GatingRMSNorm)]
+        key = (self.conv1.weight.device, tuple((p.data_ptr(), p._version) for p in params))
+        hit = self.__dict__.get("_packed_cache")
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        wn = self._norm_weights()
+        packed = pack_weights(wn[0], wn[1], wn[2], self._f32(self.conv1.weight), self.g_inputs, self.g_rms,
+                              self.num_kv_heads, self.head_dim, self.inner_dim)
+        self.__dict__["_packed_cache"] = (key, packed)
+        return packed
+
     def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True):
         """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S))."""
         B, H, S, D = post_key.shape
         if H != self.num_kv_heads or D != self.head_dim:
             raise AssertionError("gate input shape does not match the predictor")
-        norms = [self.pre_key_norm, self.post_key_norm, self.value_norm]
-        wn = [self._f32(m.weight) if isinstance(m, GatingRMSNorm) else None for m in norms]
+        wn = self._norm_weights()
+        w1 = self._f32(self.conv1.weight)
+        packed = None
+        if post_key.dtype == torch.bfloat16 and S > 4 and post_key.is_cuda:
+            packed = self.packed_weights()
         return gate_scores_and_mask(
             pre_key if "pre_k" in self.g_inputs else None, post_key if "post_k" in self.g_inputs else None,
             value if "v" in self.g_inputs else None, wn[0], wn[1], wn[2],
-            self._f32(self.conv1.weight), self._f32(self.conv1.bias), self._f32(self.conv2.weight),
+            w1, self._f32(self.conv1.bias), self._f32(self.conv2.weight),
             self._f32(self.conv2.bias), self.inner_dim, self.act, self.g_rms,
             0.0 if self.g_fast_path else float(self.g_epsilon), threshold,
-            like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores)
+            like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores, w1_packed=packed)
 
     def forward(self, pre_key, post_key, value):
         """Scores (B, H, S) float32, as the reference's forward returns."""
@@ -91,15 +117,40 @@ class GatingPredictor(nn.Module):
         return scores
 
 
+def pack_weights(w_pre, w_post, w_v, w1, g_inputs, rms, num_kv_heads, head_dim, inner):
+    """wgkv_gate_pack_weights: conv1 weight (H*inner, n_in*D[, 1]) fp32 times
+    the norm weights (when rms), as three bf16 planes in the matrix-core
+    operand layout.  Returns a uint8 device tensor."""
+    bits = 0
+    for name in g_inputs:
+        bits |= _INPUT_BITS[name]
+    n_in = bin(bits).count("1")
+    for w in (w_pre, w_post, w_v, w1):
+        if w is not None and (w.dtype != torch.float32 or not w.is_contiguous()):
+            raise TypeError("gate parameters must be contiguous fp32")
+    _require_cuda(w1)
+    L = _lib.lib()
+    nbytes = int(L.wgkv_gate_packed_bytes(num_kv_heads, inner, n_in * head_dim))
+    if nbytes <= 0:
+        raise ValueError("unsupported gate shape for packing")
+    packed = torch.empty(nbytes, dtype=torch.uint8, device=w1.device)
+    st = L.wgkv_gate_pack_weights(_ptr(w_pre), _ptr(w_post), _ptr(w_v), bits, int(bool(rms)), _ptr(w1),
+                                  num_kv_heads, head_dim, inner, _ptr(packed), nbytes, _lib.stream_handle(w1.device))
+    _lib.check(st, "wgkv_gate_pack_weights")
+    return packed
+
+
 def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
-                         clamp_min, threshold, like=None, scores_out=None, mask_out=None, want_scores=True):
+                         clamp_min, threshold, like=None, scores_out=None, mask_out=None, want_scores=True,
+                         w1_packed=None):
     """The gate kernel on explicit fp32 parameters (GatingPredictor.forward,
     src/modeling_layers.py:170-205, with the admission of :1465): inputs
     (B, H, S, D) bf16 or fp32 (None for inputs not used), RMS-norm weights (D)
     or None, conv1 weight (H*inner, n_in*D, 1) / bias, conv2 weight
     (H, inner, 1) / bias, act 0 = GELU (erf) / 1 = SiLU, clamp_min > 0 for the
-    conv path's clamp.  Returns (scores f32 (B,H,S) or None, mask bool
-    (B,H,S))."""
+    conv path's clamp; w1_packed (optional) = pack_weights() of the same
+    weights, used for bf16 inputs of more than four tokens.  Returns (scores
+    f32 (B,H,S) or None, mask bool (B,H,S))."""
     ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
     ref = like if like is not None else next(t for t in (post_key, pre_key, value) if t is not None)
     B, H, S, D = ref.shape
@@ -139,6 +190,7 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         int(act), int(bool(rms)), float(clamp_min), float(threshold),
         _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
         _ptr(mk), mk.stride(0), mk.stride(1),
+        _ptr(w1_packed),
         _ptr(ws), 0 if ws is None else ws.numel(),
         _lib.stream_handle(dev))
     _lib.check(st, "wgkv_gate_scores")

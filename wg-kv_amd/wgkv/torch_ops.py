@@ -13,12 +13,18 @@ Operators (schemas below):
   paged_decode_attn       -- flash_attn_with_kvcache as wrapped at :766-800
   generate_sparse_indices -- :384-409 (column_index width = seq_len)
   gate_scores_and_mask    -- GatingPredictor.forward (:170-205) plus the
-                             admission of :1465, on fp32 parameters
+                             admission of :1465, on fp32 parameters (with
+                             the optional packed first layer)
+  gate_pack_weights       -- the packed first layer of the bf16
+                             matrix-core gate path (no reference counterpart)
 """
 import torch
 
 from . import ops as _ops
 from .gate import gate_scores_and_mask as _gate_scores_and_mask
+from .gate import pack_weights as _pack_weights
+
+_INPUT_NAMES = ("pre_k", "post_k", "v")
 
 _LIB = torch.library.Library("wgkv", "DEF")
 _LIB.define("sparse_attn(Tensor q, Tensor k, Tensor v, Tensor block_count, Tensor block_offset, "
@@ -29,7 +35,9 @@ _LIB.define("generate_sparse_indices(Tensor g_mask, int local_window_size, int b
             "-> (Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("gate_scores_and_mask(Tensor? pre_key, Tensor? post_key, Tensor? value, Tensor? w_pre, "
             "Tensor? w_post, Tensor? w_v, Tensor w1, Tensor b1, Tensor w2, Tensor b2, int inner, int act, "
-            "bool rms, float clamp_min, float threshold) -> (Tensor, Tensor)")
+            "bool rms, float clamp_min, float threshold, Tensor? w1_packed=None) -> (Tensor, Tensor)")
+_LIB.define("gate_pack_weights(Tensor? w_pre, Tensor? w_post, Tensor? w_v, Tensor w1, int inputs_mask, bool rms, "
+            "int num_kv_heads, int head_dim, int inner) -> Tensor")
 
 
 # ---- CUDA (HIP) kernels: the library calls ----------------------------------
@@ -47,15 +55,22 @@ def _generate_sparse_indices(g_mask, local_window_size, block_size=64):
     return _ops.generate_sparse_indices(g_mask, local_window_size, B, H, S, block_size=block_size)
 
 
-def _gate(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, threshold):
+def _gate(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, threshold,
+          w1_packed=None):
     return _gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
-                                 clamp_min, threshold)
+                                 clamp_min, threshold, w1_packed=w1_packed)
+
+
+def _gate_pack(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner):
+    names = [n for i, n in enumerate(_INPUT_NAMES) if inputs_mask >> i & 1]
+    return _pack_weights(w_pre, w_post, w_v, w1, names, rms, num_kv_heads, head_dim, inner)
 
 
 _LIB.impl("sparse_attn", _sparse_attn, "CUDA")
 _LIB.impl("paged_decode_attn", _paged_decode_attn, "CUDA")
 _LIB.impl("generate_sparse_indices", _generate_sparse_indices, "CUDA")
 _LIB.impl("gate_scores_and_mask", _gate, "CUDA")
+_LIB.impl("gate_pack_weights", _gate_pack, "CUDA")
 
 
 # ---- Meta kernels: output shapes only ----------------------------------------
@@ -76,7 +91,8 @@ def _generate_sparse_indices_meta(g_mask, local_window_size, block_size=64):
             torch.empty(B, H, R, **i32), torch.empty(B, H, 1, S, **i32))
 
 
-def _gate_meta(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, threshold):
+def _gate_meta(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, threshold,
+               w1_packed=None):
     ref = next(t for t in (post_key, pre_key, value) if t is not None)
     B, H, S, _ = ref.shape
     return (torch.empty(B, H, S, dtype=torch.float32, device=ref.device),
@@ -86,7 +102,13 @@ def _gate_meta(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inn
 _LIB.impl("sparse_attn", _sparse_attn_meta, "Meta")
 _LIB.impl("paged_decode_attn", _paged_decode_attn_meta, "Meta")
 _LIB.impl("generate_sparse_indices", _generate_sparse_indices_meta, "Meta")
+def _gate_pack_meta(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner):
+    n_in = bin(inputs_mask & 7).count("1")
+    return torch.empty(num_kv_heads * inner * n_in * head_dim * 3 * 2, dtype=torch.uint8, device=w1.device)
+
+
 _LIB.impl("gate_scores_and_mask", _gate_meta, "Meta")
+_LIB.impl("gate_pack_weights", _gate_pack_meta, "Meta")
 
 
 # ---- the layer's swap points through the dispatcher ---------------------------
