@@ -387,6 +387,15 @@ int wgkv_quest_select(
  * wgkv_silu_mul -- LlamaMLP's act_fn(gate) * up (:161): rows of `cols`
  *   bf16 (cols a multiple of 8), gate and up with their own row strides
  *   (e.g. the two halves of one fused projection), out contiguous.
+ * wgkv_gemv -- the one-row nn.Linear of a decode step (LlamaAttention's
+ *   q/k/v and o projections, :252-323 of modeling_llama.py; LlamaMLP :149-161;
+ *   the LM head): y = W x with W (n, k) bf16 (row stride w_row_stride), x
+ *   (k) bf16, fp32 accumulation, y bf16 (k a multiple of 8, <= 32768; W and
+ *   x 16-byte aligned).  mode 0: y = bf16(W x) (n values).  mode 1: y =
+ *   bf16(residual + bf16(W x)), the residual add after the projection
+ *   (residual (n) bf16; y may equal residual).  mode 2: W holds the gate
+ *   rows 0..n-1 and the up rows n..2n-1 (one stacked [gate; up] weight) and
+ *   y = bf16(bf16(silu(bf16(W_gate x))) * bf16(W_up x)) (n values).
  * ---------------------------------------------------------------------- */
 int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t res_row_stride,
                   const void* weight, void* out, int64_t out_row_stride, void* residual_out,
@@ -404,6 +413,9 @@ int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
 
 int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,
                   void* out, int64_t rows, int32_t cols, void* stream);
+
+int wgkv_gemv(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+              int32_t mode, const void* residual, void* stream);
 
 #ifdef __cplusplus
 }

@@ -71,3 +71,50 @@ def test_silu_mul_bit_identical(rows, cols):
     gu = (torch.randn(rows, 2 * cols, generator=g) * 4).to(torch.bfloat16).to(DEV)
     ga, ua = gu[:, :cols], gu[:, cols:]
     assert torch.equal(model_ops.silu_mul(ga, ua), F.silu(ga) * ua)
+
+
+@pytest.mark.parametrize("n,k", [(6144, 4096), (4096, 14336), (14336, 4096), (37, 72), (3, 8)])
+def test_gemv_rows_meet_fp64_products(n, k):
+    """wgkv_gemv (mode 0) against the fp64 product: every output is the fp64
+    value rounded to bf16, give or take one bf16 unit where the fp32 sum
+    lands on the other side of a rounding boundary; repeated calls agree
+    bit for bit (no atomics)."""
+    from wgkv import model_ops
+    print(f"[model_ops] gemv n{n} k{k}", flush=True)
+    g = torch.Generator().manual_seed(n + k)
+    w = (torch.randn(n, k, generator=g) * 0.05).to(torch.bfloat16)
+    x = torch.randn(1, 1, k, generator=g).to(torch.bfloat16)
+    ref = (x.double().view(1, k) @ w.double().t()).view(-1)
+    y = model_ops.linear(x.to(DEV), w.to(DEV)).view(-1).cpu()
+    ulp = torch.exp2(torch.floor(torch.log2(ref.abs().clamp_min(1e-30))) - 7)
+    err = ((y.double() - ref).abs() / ulp).max().item()
+    assert err <= 1.0, err
+    assert torch.equal(model_ops.linear(x.to(DEV), w.to(DEV)).view(-1).cpu(), y)
+
+
+@pytest.mark.parametrize("n,k", [(14336, 4096), (40, 64)])
+def test_gemv_epilogues_equal_the_torch_compositions(n, k):
+    """Mode 1 is residual + (W x) and mode 2 silu(W_gate x) * (W_up x) with
+    torch's bf16 rounding, bit for bit against the torch ops applied to the
+    mode-0 products (each row's sum is computed the same way in every mode);
+    rows given as a strided view (weight rows wider than k) and a two-row
+    input (torch's GEMM) also work."""
+    from wgkv import model_ops
+    print(f"[model_ops] gemv epilogues n{n} k{k}", flush=True)
+    g = torch.Generator().manual_seed(3 * n + k)
+    gu = (torch.randn(2 * n, k, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    x = torch.randn(1, 1, k, generator=g).to(torch.bfloat16).to(DEV)
+    r = torch.randn(1, 1, 2 * n, generator=g).to(torch.bfloat16).to(DEV)
+    y0 = model_ops.linear(x, gu)
+    assert torch.equal(model_ops.linear(x, gu, residual=r), r + y0)
+    s = model_ops.swiglu_linear(x, gu)
+    assert torch.equal(s, F.silu(y0[..., :n]) * y0[..., n:])
+    # a weight whose rows are a strided view (the left k columns of a wider buffer)
+    wide = (torch.randn(n, k + 8, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    wv = wide[:, :k]
+    assert model_ops.gemv_usable(x, wv)
+    assert torch.equal(model_ops.linear(x, wv), model_ops.linear(x, wv.contiguous()))
+    # two rows: not a decode step, torch's GEMM
+    x2 = torch.randn(1, 2, k, generator=g).to(torch.bfloat16).to(DEV)
+    assert not model_ops.gemv_usable(x2, gu)
+    assert torch.equal(model_ops.linear(x2, gu), F.linear(x2, gu))

@@ -176,6 +176,98 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_
   *(u32x4_t*)(out + row * (int64_t)cols + c) = pack8(o);
 }
 
+// ---- one-token products y = W x (decode steps) -----------------------------
+// Replaces the torch GEMMs of a decode step, where the activation is a single
+// row (q/k/v, o, gate/up and down projections, LM head): W (N, K) bf16 with
+// row stride w_rs, x (K) bf16, fp32 accumulation, y bf16.  Workgroup = 4
+// waves; wave w of workgroup b computes row pair p = 4b + w -- rows 2p and
+// 2p+1, or for the SwiGLU product rows p and N + p of the stacked [gate; up]
+// weight.  x is staged in LDS; lane l streams 16-byte slices l, l+64, ...
+// of both rows, eight slices per row in flight, and multiplies them on
+// v_dot2_f32_bf16; each row is then summed over the wave.  Epilogues, with
+// torch's bf16 rounding points:
+//   mode 0  y[r] = bf16(acc)
+//   mode 1  y[r] = bf16(res[r] + bf16(acc))                       (residual add)
+//   mode 2  y[p] = bf16(bf16(silu(g)) * u), g = bf16(acc_gate), u = bf16(acc_up)
+constexpr int kGemvWaves = 4;
+constexpr int kGemvBatch = 8;  // slices per row and lane in flight
+
+struct GemvArgs {
+  const uint16_t* w;
+  int64_t w_rs;
+  const uint16_t* x;
+  uint16_t* y;
+  const uint16_t* res;
+  int N, K, mode;
+};
+
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2v_t;
+WGKV_DEVICE float dot2(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b), c, false);
+}
+
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
+  extern __shared__ u32x4_t xs[];
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int pair = blockIdx.x * kGemvWaves + wid;
+  const int npairs = a.mode == 2 ? a.N : (a.N + 1) / 2;
+  const int p = min(pair, npairs - 1);  // waves past the last pair compute it again and store nothing
+  const int r0 = a.mode == 2 ? p : 2 * p;
+  const int r1 = a.mode == 2 ? a.N + p : min(2 * p + 1, a.N - 1);
+  const u32x4_t* w0 = (const u32x4_t*)(a.w + (int64_t)r0 * a.w_rs);
+  const u32x4_t* w1 = (const u32x4_t*)(a.w + (int64_t)r1 * a.w_rs);
+  const int ns = a.K / 8;
+  // the first slices of the rows are requested before x is staged
+  u32x4_t b0[kGemvBatch], b1[kGemvBatch];
+#pragma unroll
+  for (int u = 0; u < kGemvBatch; ++u) {
+    const int sl = min(lane + 64 * u, ns - 1);
+    b0[u] = __builtin_nontemporal_load(w0 + sl);
+    b1[u] = __builtin_nontemporal_load(w1 + sl);
+  }
+  for (int sl = threadIdx.x; sl < ns; sl += 64 * kGemvWaves) xs[sl] = ((const u32x4_t*)a.x)[sl];
+  __syncthreads();
+  float acc0 = 0.f, acc1 = 0.f;
+  for (int s0 = 0;;) {
+#pragma unroll
+    for (int u = 0; u < kGemvBatch; ++u) {
+      const int sl = s0 + lane + 64 * u;
+      if (sl < ns) {
+        const u32x4_t xv = xs[sl];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc0 = dot2(b0[u][e], xv[e], acc0);
+          acc1 = dot2(b1[u][e], xv[e], acc1);
+        }
+      }
+    }
+    s0 += 64 * kGemvBatch;
+    if (s0 >= ns) break;
+#pragma unroll
+    for (int u = 0; u < kGemvBatch; ++u) {
+      const int sl = min(s0 + lane + 64 * u, ns - 1);
+      b0[u] = __builtin_nontemporal_load(w0 + sl);
+      b1[u] = __builtin_nontemporal_load(w1 + sl);
+    }
+  }
+  acc0 = wave_sum(acc0);
+  acc1 = wave_sum(acc1);
+  if (lane != 0 || pair >= npairs) return;
+  if (a.mode == 2) {
+    const float g = rb(acc0), u = rb(acc1);
+    a.y[p] = f32_to_bf16(rb(g / (1.0f + expf(-g))) * u);
+    return;
+  }
+  const float v0 = rb(acc0), v1 = rb(acc1);
+  if (a.mode == 1) {
+    a.y[r0] = f32_to_bf16(bf16lo(a.res[r0]) + v0);
+    if (r1 != r0) a.y[r1] = f32_to_bf16(bf16lo(a.res[r1]) + v1);
+  } else {
+    a.y[r0] = f32_to_bf16(v0);
+    if (r1 != r0) a.y[r1] = f32_to_bf16(v1);
+  }
+}
+
 bool misaligned(const void* p) { return ((uintptr_t)p & 15) != 0; }
 
 }  // namespace
@@ -257,5 +349,18 @@ extern "C" int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const vo
   hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)gate, gate_row_stride, (const uint16_t*)up, up_row_stride, (uint16_t*)out,
                      rows, cols);
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_gemv(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+                         int32_t mode, const void* residual, void* stream) {
+  if (!w || !x || !y || n <= 0 || k <= 0 || mode < 0 || mode > 2) return WGKV_ERR_ARG;
+  if (mode == 1 && !residual) return WGKV_ERR_ARG;
+  if (k % 8 || k > 8 * 4096 || w_row_stride % 8 || misaligned(w) || misaligned(x)) return WGKV_ERR_UNSUPPORTED;
+  GemvArgs a = {(const uint16_t*)w, w_row_stride, (const uint16_t*)x, (uint16_t*)y, (const uint16_t*)residual,
+                n, k, mode};
+  const int npairs = mode == 2 ? n : (n + 1) / 2;
+  const int blocks = (npairs + kGemvWaves - 1) / kGemvWaves;
+  hipLaunchKernelGGL(gemv_kernel, dim3(blocks), dim3(64 * kGemvWaves), (size_t)k * 2, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

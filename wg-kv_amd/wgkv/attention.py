@@ -72,10 +72,11 @@ class LlamaAttention(nn.Module):
         self.num_key_value_groups = config.num_attention_heads // config.num_key_value_heads
         self.scaling = self.head_dim ** -0.5
         bias = config.attention_bias
-        self.q_proj = nn.Linear(config.hidden_size, config.num_attention_heads * self.head_dim, bias=bias)
-        self.k_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
-        self.v_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
-        self.o_proj = nn.Linear(config.num_attention_heads * self.head_dim, config.hidden_size, bias=bias)
+        # nn.Linear modules whose one-row (decode-step) products run on wgkv_gemv
+        self.q_proj = model_ops.Linear(config.hidden_size, config.num_attention_heads * self.head_dim, bias=bias)
+        self.k_proj = model_ops.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
+        self.v_proj = model_ops.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=bias)
+        self.o_proj = model_ops.Linear(config.num_attention_heads * self.head_dim, config.hidden_size, bias=bias)
         self.qk_norm = qk_norm
         if qk_norm:
             self.q_norm = HeadRMSNorm(self.head_dim)
@@ -115,7 +116,7 @@ class LlamaAttention(nn.Module):
         hidden_shape = (*input_shape, -1, self.head_dim)
         if self._qkv_weight is not None and self._qkv_weight.device == hidden_states.device:
             nq, nk = self.q_proj.weight.shape[0], self.k_proj.weight.shape[0]
-            qkv = torch.nn.functional.linear(hidden_states, self._qkv_weight)
+            qkv = model_ops.linear(hidden_states, self._qkv_weight)
             q = qkv[..., :nq].view(hidden_shape)
             k = qkv[..., nq:nq + nk].view(hidden_shape)
             v_src = qkv[..., nq + nk:]

@@ -3,7 +3,9 @@ runs (the reference's scripts/profiling.py:198-420).
 
 Embedding, RMSNorm, the gated attention layer (``wgkv.attention.LlamaAttention``
 with its swap points), SwiGLU MLP and LM head, random-initialised in bf16 on
-the device; the dense projections are torch GEMMs (hipBLASLt).  The prompt is
+the device; the dense projections of a prompt are torch GEMMs (hipBLASLt), a
+decode step's one-row products run on wgkv_gemv (with the SwiGLU product and
+the residual adds fused).  The prompt is
 prefilled in chunks through the cache's chunk continuation and then decoded
 greedily, as profiling.py does (argmax of the last logits, :146-147).  The
 "full" run admits every token (``use_baseline``, src/modeling_layers.py:1556),
@@ -53,17 +55,38 @@ class RMSNorm(nn.Module):
 class MLP(nn.Module):
     def __init__(self, hidden, inter):
         super().__init__()
-        self.gate_proj = nn.Linear(hidden, inter, bias=False)
-        self.up_proj = nn.Linear(hidden, inter, bias=False)
-        self.down_proj = nn.Linear(inter, hidden, bias=False)
+        self.gate_proj = model_ops.Linear(hidden, inter, bias=False)
+        self.up_proj = model_ops.Linear(hidden, inter, bias=False)
+        self.down_proj = model_ops.Linear(inter, hidden, bias=False)
+        self._gate_up = None
 
-    def forward(self, x):
-        # separate GEMMs: for a decode step hipBLASLt runs the two 14336-wide
-        # products faster than one 28672-wide product (2 x 27 us vs 67 us)
+    @torch.no_grad()
+    def fuse_gate_up(self):
+        """Put gate_proj and up_proj's weights into one (2*inter, hidden)
+        buffer (the parameters become views of it, names and values kept), for
+        the one-launch SwiGLU product of a decode step."""
+        if self._gate_up is not None:
+            return
+        w = torch.cat([self.gate_proj.weight, self.up_proj.weight], dim=0)
+        n = self.gate_proj.weight.shape[0]
+        self.gate_proj.weight = nn.Parameter(w[:n], requires_grad=False)
+        self.up_proj.weight = nn.Parameter(w[n:], requires_grad=False)
+        self._gate_up = w
+
+    def forward(self, x, residual=None):
+        """down(silu(gate(x)) * up(x)) (+ residual, the decoder's add after
+        the MLP).  A decode step's row: two launches (the stacked gate/up
+        product with SwiGLU, the down product with the residual add)."""
+        gu = self._gate_up
+        if gu is not None and gu.device == x.device and model_ops.gemv_usable(x, gu):
+            return model_ops.linear(model_ops.swiglu_linear(x, gu), self.down_proj.weight, residual=residual)
+        # prompts: separate GEMMs and the fused SwiGLU product
         g, u = self.gate_proj(x), self.up_proj(x)
         if model_ops.usable(g, u) and g.shape[-1] % 8 == 0 and g.stride(-1) == 1 and u.stride(-1) == 1:
-            return self.down_proj(model_ops.silu_mul(g, u))
-        return self.down_proj(F.silu(g) * u)
+            out = self.down_proj(model_ops.silu_mul(g, u))
+        else:
+            out = self.down_proj(F.silu(g) * u)
+        return out if residual is None else residual + out
 
 
 class DecoderLayer(nn.Module):
@@ -83,7 +106,7 @@ class DecoderLayer(nn.Module):
 
     def forward(self, x, pos_emb, cache):
         residual, h = self.rmsnorm_and_self_attn(x, pos_emb, cache)
-        return residual + self.mlp(h)
+        return self.mlp(h, residual=residual)  # residual + mlp(h)
 
 
 @dataclass
@@ -127,10 +150,11 @@ class LlamaLite(nn.Module):
         self.layers = nn.ModuleList(DecoderLayer(self.cfg, i, ec.intermediate_size, ec.qk_norm)
                                     for i in range(ec.num_hidden_layers))
         self.norm = RMSNorm(ec.hidden_size)
-        self.lm_head = nn.Linear(ec.hidden_size, ec.vocab_size, bias=False)
+        self.lm_head = model_ops.Linear(ec.hidden_size, ec.vocab_size, bias=False)
         self.rotary_emb = LlamaRotaryEmbedding(self.cfg.head_dim, ec.rope_theta)
-        for layer in self.layers:  # q, k, v projected by one GEMM (weights are views of one buffer)
+        for layer in self.layers:  # q, k, v (and gate, up) projected by one product each
             layer.self_attn.fuse_qkv()
+            layer.mlp.fuse_gate_up()
 
     @torch.no_grad()
     def init_weights(self, seed=0, std=0.02):

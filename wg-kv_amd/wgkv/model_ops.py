@@ -1,11 +1,15 @@
 """Fused bf16 decoder building blocks for the end-to-end harness
 (csrc/model_ops.hip): RMSNorm with the residual add before it, rotary
-embedding of q and k, and the SwiGLU product.  Each replaces a chain of
-small torch kernels of the reference model (src/modeling_llama.py:61-76,
-:115-146, :149-161, :366, :399) with one launch and rounds to bf16 where the
-torch composition does.  ``usable`` says when a call qualifies (bf16 CUDA
-tensors of supported shapes); callers keep the torch ops otherwise."""
+embedding of q and k, the SwiGLU product, and the one-row products of a
+decode step (``linear``, ``swiglu_linear``, the ``Linear`` module).  Each
+replaces a chain of small torch kernels of the reference model
+(src/modeling_llama.py:61-76, :115-146, :149-161, :366, :399) or a
+hipBLASLt call with one launch and rounds to bf16 where the torch
+composition does.  ``usable`` says when a call qualifies (bf16 CUDA tensors
+of supported shapes); callers keep the torch ops otherwise."""
 import torch
+import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _lib
 from .ops import _ptr
@@ -75,3 +79,55 @@ def silu_mul(gate, up):
                                   _lib.stream_handle(gate.device))
     _lib.check(st, "wgkv_silu_mul")
     return out
+
+
+def gemv_usable(x, weight):
+    """x is one row (a decode step's activation) that wgkv_gemv takes with
+    this (n, k) weight."""
+    return (usable(x, weight) and x.numel() == x.shape[-1] == weight.shape[-1] and x.is_contiguous()
+            and weight.dim() == 2 and weight.stride(-1) == 1 and weight.stride(0) % 8 == 0
+            and weight.shape[-1] % 8 == 0 and weight.shape[-1] <= 32768
+            and x.data_ptr() % 16 == 0 and weight.data_ptr() % 16 == 0)
+
+
+def _gemv(x, weight, n, mode, residual=None):
+    y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=x.device)
+    st = _lib.lib().wgkv_gemv(_ptr(weight), weight.stride(0), n, weight.shape[-1], _ptr(x), _ptr(y), mode,
+                              _ptr(residual), _lib.stream_handle(x.device))
+    _lib.check(st, "wgkv_gemv")
+    return y
+
+
+def linear(x, weight, residual=None):
+    """x @ weight.T (+ residual): for one bf16 row on the decode GEMV
+    (wgkv_gemv mode 0, or mode 1 with the residual add fused), otherwise
+    F.linear (then residual + y, as torch rounds it)."""
+    n = weight.shape[0]
+    if gemv_usable(x, weight) and (residual is None or (usable(residual) and residual.is_contiguous()
+                                                        and residual.numel() == n)):
+        return _gemv(x, weight, n, 0 if residual is None else 1, residual)
+    y = F.linear(x, weight)
+    return y if residual is None else residual + y
+
+
+def swiglu_linear(x, gate_up_weight):
+    """bf16(silu(x @ W_gate.T)) * (x @ W_up.T) for the stacked (2n, k)
+    [gate; up] weight: one wgkv_gemv (mode 2) for a single bf16 row,
+    otherwise two F.linear and the SwiGLU product."""
+    n = gate_up_weight.shape[0] // 2
+    if gemv_usable(x, gate_up_weight):
+        return _gemv(x, gate_up_weight, n, 2)
+    g, u = F.linear(x, gate_up_weight[:n]), F.linear(x, gate_up_weight[n:])
+    if usable(g, u) and n % 8 == 0:
+        return silu_mul(g, u)
+    return F.silu(g) * u
+
+
+class Linear(nn.Linear):
+    """nn.Linear (same parameters and state-dict names) whose bias-free
+    one-row products -- a decode step's -- run on wgkv_gemv."""
+
+    def forward(self, x):
+        if self.bias is None:
+            return linear(x, self.weight)
+        return super().forward(x)
