@@ -215,6 +215,25 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
 // split order and applies sigmoid, clamp and threshold, so results do not
 // depend on arrival order.  Without a workspace (nsplit = 1) one workgroup
 // takes all columns.
+// Sums over the wave of 16 per-lane values at once (a transposing
+// butterfly: at each exchange a lane keeps half of its values and adds the
+// partner's copy of that half).  Returns, in lane l, the wave-wide sum of
+// v[(l >> 2) & 15].
+__device__ __forceinline__ float reduce16_columns(const float (&v)[16], int lane) {
+  float a8[8], a4[4], a2[2];
+  const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8, b2 = lane & 4;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a8[i] = (b5 ? v[8 + i] : v[i]) + __shfl_xor(b5 ? v[i] : v[8 + i], 32);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a4[i] = (b4 ? a8[4 + i] : a8[i]) + __shfl_xor(b4 ? a8[i] : a8[4 + i], 16);
+#pragma unroll
+  for (int i = 0; i < 2; ++i) a2[i] = (b3 ? a4[2 + i] : a4[i]) + __shfl_xor(b3 ? a4[i] : a4[2 + i], 8);
+  float r = (b2 ? a2[1] : a2[0]) + __shfl_xor(b2 ? a2[0] : a2[1], 4);
+  r += __shfl_xor(r, 2);
+  r += __shfl_xor(r, 1);
+  return r;
+}
+
 constexpr int kSmallTok = 4;
 constexpr int kSmallWaves = 4;
 constexpr int kSplitCols = 16 * kSmallWaves;  // hidden columns per workgroup and pass
@@ -303,11 +322,14 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   float logit[kSmallTok];
 #pragma unroll
   for (int t = 0; t < kSmallTok; ++t) logit[t] = 0.f;
+  // after the column reduction lane l holds column (l >> 2) & 15 of the
+  // wave's 16 (four lanes per column)
+  const int my_col = (lane >> 2) & 15;
   for (int c0 = c_first; c0 < a.inner; c0 += kSplitCols * a.nsplit) {
+    float dot[kSmallTok][16];
 #pragma unroll
     for (int j0 = 0; j0 < 16; j0 += JB) {
       if (c0 != c_first || j0 != 0) load_rows(c0 + j0);
-      float dot[kSmallTok][JB];
 #pragma unroll
       for (int j = 0; j < JB; ++j)
 #pragma unroll
@@ -317,23 +339,23 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
           for (int c = 0; c < CPL; ++c)
 #pragma unroll
             for (int e = 0; e < 4; ++e) acc = fmaf(wrow[j][c][e], xr[t][c][e], acc);
-          dot[t][j] = acc;
+          dot[t][j0 + j] = acc;
         }
+    }
+    const float bias = b1h[c0 + my_col], wo = w2h[c0 + my_col];
 #pragma unroll
-      for (int t = 0; t < kSmallTok; ++t) {
-        if (t >= nt) break;
-#pragma unroll
-        for (int j = 0; j < JB; ++j) {
-          const float z = wave_sum(dot[t][j]) + b1h[c0 + j0 + j];
-          if (lane == j0 + j) logit[t] = fmaf(w2h[c0 + j0 + j], a.act ? silu(z) : gelu_erf(z), logit[t]);
-        }
-      }
+    for (int t = 0; t < kSmallTok; ++t) {
+      if (t >= nt) break;
+      const float z = reduce16_columns(dot[t], lane) + bias;
+      const float y = wo * (a.act ? silu(z) : gelu_erf(z));  // one activation per lane
+      logit[t] += (lane & 3) == 0 ? y : 0.f;
     }
   }
-  // lanes 0..15 of each wave hold partial logits; sum them, then the waves
+  // sum the wave's partial logits over its lanes, then over the waves
 #pragma unroll
   for (int t = 0; t < kSmallTok; ++t) {
-    const float v = row_sum16(lane < 16 ? logit[t] : 0.f);
+    if (t >= nt) break;
+    const float v = wave_sum(logit[t]);
     if (lane == 0) s_part[wid][t] = v;
   }
   __syncthreads();
