@@ -396,6 +396,16 @@ int wgkv_quest_select(
  *   (residual (n) bf16; y may equal residual).  mode 2: W holds the gate
  *   rows 0..n-1 and the up rows n..2n-1 (one stacked [gate; up] weight) and
  *   y = bf16(bf16(silu(bf16(W_gate x))) * bf16(W_up x)) (n values).
+ * wgkv_gemv_ex -- wgkv_gemv with two fusions of a decode step.  With
+ *   norm_weight (k) the workgroups first apply wgkv_rms_norm to x (with
+ *   norm_residual: to x + norm_residual, stored to norm_residual_out), bit
+ *   for bit, and multiply the normalised row.  mode 3 is LlamaAttention's
+ *   q/k/v projection with apply_rotary_pos_emb (modeling_llama.py:265-271):
+ *   W holds the q, k and v rows of num_q_heads + 2 num_kv_heads heads of
+ *   head_dim (n = that many rows); y (n) gets the rotated q and k (cos, sin:
+ *   head_dim bf16 values of the token's position, wgkv_rope_qkv's rounding)
+ *   and v, in W's row order; k_raw (num_kv_heads * head_dim) the unrotated
+ *   k (the gate's pre-RoPE key).
  * ---------------------------------------------------------------------- */
 int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* residual, int64_t res_row_stride,
                   const void* weight, void* out, int64_t out_row_stride, void* residual_out,
@@ -416,6 +426,12 @@ int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int
 
 int wgkv_gemv(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
               int32_t mode, const void* residual, void* stream);
+
+int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+                 int32_t mode, const void* residual,
+                 const void* norm_weight, const void* norm_residual, void* norm_residual_out, float eps,
+                 const void* cos, const void* sin, void* k_raw,
+                 int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream);
 
 #ifdef __cplusplus
 }

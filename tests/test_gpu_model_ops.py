@@ -118,3 +118,54 @@ def test_gemv_epilogues_equal_the_torch_compositions(n, k):
     x2 = torch.randn(1, 2, k, generator=g).to(torch.bfloat16).to(DEV)
     assert not model_ops.gemv_usable(x2, gu)
     assert torch.equal(model_ops.linear(x2, gu), F.linear(x2, gu))
+
+
+@pytest.mark.parametrize("with_res", [False, True])
+@pytest.mark.parametrize("mode", [0, 2])
+def test_gemv_norm_prologue_equals_rms_norm_then_gemv(with_res, mode):
+    """The workgroups' own RMSNorm of x (+ residual) gives wgkv_rms_norm's
+    bits, so the fused launch equals rms_norm followed by the product."""
+    from wgkv import model_ops
+    print(f"[model_ops] gemv norm prologue res={with_res} mode={mode}", flush=True)
+    g = torch.Generator().manual_seed(5 + mode + int(with_res))
+    H, N = 4096, 1024
+    x = torch.randn(1, 1, H, generator=g).to(torch.bfloat16).to(DEV)
+    r = torch.randn(1, 1, H, generator=g).to(torch.bfloat16).to(DEV) if with_res else None
+    nw = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(2 * N if mode == 2 else N, H, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    y, h = model_ops.rms_norm_linear(x, nw, 1e-5, w, residual=r, mode=mode)
+    normed, h_ref = model_ops.rms_norm(x, nw, 1e-5, residual=r)
+    ref = model_ops.swiglu_linear(normed, w) if mode == 2 else model_ops.linear(normed, w)
+    assert torch.equal(y, ref)
+    if with_res:
+        assert torch.equal(h, h_ref)
+
+
+@pytest.mark.parametrize("with_norm", [False, True])
+@pytest.mark.parametrize("Hq,Hkv,D", [(32, 8, 128), (8, 2, 64)])
+def test_qkv_rope_equals_product_then_rope(with_norm, Hq, Hkv, D):
+    """Mode 3: the q/k/v rows with RoPE applied in the epilogue equal the
+    product followed by wgkv_rope_qkv (itself bit-identical to
+    apply_rotary_pos_emb), and k_raw is the unrotated k."""
+    from wgkv import model_ops
+    from wgkv.attention import LlamaRotaryEmbedding
+    print(f"[model_ops] qkv_rope Hq{Hq} Hkv{Hkv} D{D} norm={with_norm}", flush=True)
+    g = torch.Generator().manual_seed(Hq + D + int(with_norm))
+    hidden = 4096 if D == 128 else 512
+    n = (Hq + 2 * Hkv) * D
+    x = torch.randn(1, 1, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(n, hidden, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(DEV) if with_norm else None
+    rot = LlamaRotaryEmbedding(D, 500000.0, device=DEV)
+    cos, sin = rot(x, torch.tensor([[123457]], device=DEV))
+    buf, kraw = model_ops.qkv_rope(x, w, cos, sin, Hq, Hkv, D, nw, 1e-5)
+    xin = model_ops.rms_norm(x, nw, 1e-5)[0] if with_norm else x
+    qkv = model_ops.linear(xin, w)
+    q = qkv[..., :Hq * D].view(1, 1, Hq, D).transpose(1, 2)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].view(1, 1, Hkv, D).transpose(1, 2)
+    v = qkv[..., (Hq + Hkv) * D:].view(1, 1, Hkv, D).transpose(1, 2)
+    fq, fk, fv = model_ops.rope_qkv(q, k, v, cos, sin)
+    assert torch.equal(buf[:, :, :Hq].transpose(1, 2), fq)
+    assert torch.equal(buf[:, :, Hq:Hq + Hkv].transpose(1, 2), fk)
+    assert torch.equal(buf[:, :, Hq + Hkv:].transpose(1, 2), fv)
+    assert torch.equal(kraw.transpose(1, 2), k)

@@ -49,24 +49,30 @@ struct NormArgs {
   float eps;
 };
 
-template <bool RES>
-__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
-  __shared__ float s_sum[kNormThreads / 64];
-  const int row = blockIdx.x, t = threadIdx.x;
-  const int nch = a.hidden / 8;
+// The normalisation of one row by a 256-thread workgroup (shared by
+// rms_norm_kernel and the GEMV prologue, so both give the same bits): thread
+// t holds chunks t, t+256, ... of the row; h = x (+ res) rounded to bf16;
+// the mean of squares is summed per thread, over each wave, then over the
+// four waves in order.  emit_res(ch, h chunk) and emit(ch, out chunk) receive
+// the results.
+template <bool RES, typename EmitOut, typename EmitRes>
+WGKV_DEVICE void rms_norm_row(const uint16_t* x, const uint16_t* res, const uint16_t* w, int hidden, float eps,
+                              float* s_sum, EmitOut emit, EmitRes emit_res) {
+  const int t = threadIdx.x;
+  const int nch = hidden / 8;
   float h[kNormChunks][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kNormChunks; ++c) {
     const int ch = t + c * kNormThreads;
     if (ch < nch) {
-      unpack8(*(const u32x4_t*)(a.x + row * a.x_rs + ch * 8), h[c]);
+      unpack8(*(const u32x4_t*)(x + ch * 8), h[c]);
       if (RES) {
         float r[8];
-        unpack8(*(const u32x4_t*)(a.res + row * a.r_rs + ch * 8), r);
+        unpack8(*(const u32x4_t*)(res + ch * 8), r);
 #pragma unroll
         for (int i = 0; i < 8; ++i) h[c][i] = rb(h[c][i] + r[i]);
-        *(u32x4_t*)(a.res_out + row * a.ro_rs + ch * 8) = pack8(h[c]);
+        emit_res(ch, pack8(h[c]));
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(h[c][i], h[c][i], ss);
@@ -78,18 +84,28 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
   float tot = 0.f;
 #pragma unroll
   for (int wv = 0; wv < kNormThreads / 64; ++wv) tot += s_sum[wv];
-  const float scale = rsqrtf(tot / (float)a.hidden + a.eps);
+  const float scale = rsqrtf(tot / (float)hidden + eps);
 #pragma unroll
   for (int c = 0; c < kNormChunks; ++c) {
     const int ch = t + c * kNormThreads;
     if (ch < nch) {
-      float w[8], y[8];
-      unpack8(*(const u32x4_t*)(a.w + ch * 8), w);
+      float wv[8], y[8];
+      unpack8(*(const u32x4_t*)(w + ch * 8), wv);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) y[i] = w[i] * rb(h[c][i] * scale);
-      *(u32x4_t*)(a.out + row * a.o_rs + ch * 8) = pack8(y);
+      for (int i = 0; i < 8; ++i) y[i] = wv[i] * rb(h[c][i] * scale);
+      emit(ch, pack8(y));
     }
   }
+}
+
+template <bool RES>
+__global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
+  __shared__ float s_sum[kNormThreads / 64];
+  const int64_t row = blockIdx.x;
+  rms_norm_row<RES>(
+      a.x + row * a.x_rs, RES ? a.res + row * a.r_rs : nullptr, a.w, a.hidden, a.eps, s_sum,
+      [&](int ch, u32x4_t v) { *(u32x4_t*)(a.out + row * a.o_rs + ch * 8) = v; },
+      [&](int ch, u32x4_t v) { *(u32x4_t*)(a.res_out + row * a.ro_rs + ch * 8) = v; });
 }
 
 // ---- rotary embedding of q and k (and the copy of v) ------------------------
@@ -180,17 +196,24 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* g, int64_
 // Replaces the torch GEMMs of a decode step, where the activation is a single
 // row (q/k/v, o, gate/up and down projections, LM head): W (N, K) bf16 with
 // row stride w_rs, x (K) bf16, fp32 accumulation, y bf16.  Workgroup = 4
-// waves; wave w of workgroup b computes row pair p = 4b + w -- rows 2p and
-// 2p+1, or for the SwiGLU product rows p and N + p of the stacked [gate; up]
-// weight.  x is staged in LDS; lane l streams 16-byte slices l, l+64, ...
-// of both rows, eight slices per row in flight, and multiplies them on
-// v_dot2_f32_bf16; each row is then summed over the wave.  Epilogues, with
-// torch's bf16 rounding points:
-//   mode 0  y[r] = bf16(acc)
-//   mode 1  y[r] = bf16(res[r] + bf16(acc))                       (residual add)
-//   mode 2  y[p] = bf16(bf16(silu(g)) * u), g = bf16(acc_gate), u = bf16(acc_up)
+// waves; wave w of workgroup b computes row pair p = 4b + w.  x is staged in
+// LDS -- optionally as RMSNorm(x (+ residual)) computed by the workgroup
+// itself with rms_norm_row, so the norm costs no launch (workgroup 0 stores
+// the new residual stream) -- and lane l streams 16-byte slices l, l+64, ...
+// of both rows, eight slices per row in flight, multiplying them on
+// v_dot2_f32_bf16; each row is then summed over the wave.  Row pairs and
+// epilogues, with torch's bf16 rounding points:
+//   mode 0  rows 2p, 2p+1:  y[r] = bf16(acc)
+//   mode 1  rows 2p, 2p+1:  y[r] = bf16(res[r] + bf16(acc))            (residual add)
+//   mode 2  rows p, N+p of the stacked [gate; up] weight:
+//           y[p] = bf16(bf16(silu(g)) * u), g = bf16(acc_gate), u = bf16(acc_up)
+//   mode 3  q/k/v rows (Hq + 2 Hkv heads of D): rows d and d + D/2 of a head;
+//           q and k heads rotated as apply_rotary_pos_emb rounds (see
+//           rope_kernel), v copied, all into y (the layout of W's rows), and
+//           the unrotated k into kraw (Hkv * D)
 constexpr int kGemvWaves = 4;
 constexpr int kGemvBatch = 8;  // slices per row and lane in flight
+static_assert(kGemvWaves * 64 == kNormThreads, "the GEMV prologue normalises with the RMSNorm thread mapping");
 
 struct GemvArgs {
   const uint16_t* w;
@@ -199,6 +222,17 @@ struct GemvArgs {
   uint16_t* y;
   const uint16_t* res;
   int N, K, mode;
+  // optional RMSNorm prologue: x <- norm_w * bf16(h * rsqrt(mean(h^2) + eps)),
+  // h = x (+ norm_res); workgroup 0 stores h to norm_res_out
+  const uint16_t* norm_w;
+  const uint16_t* norm_res;
+  uint16_t* norm_res_out;
+  float eps;
+  // mode 3
+  const uint16_t* cos;
+  const uint16_t* sin;
+  uint16_t* kraw;
+  int hq, hkv, hd;
 };
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2v_t;
@@ -208,12 +242,23 @@ WGKV_DEVICE float dot2(uint32_t a, uint32_t b, float c) {
 
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   extern __shared__ u32x4_t xs[];
+  __shared__ float s_sum[kGemvWaves];
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int pair = blockIdx.x * kGemvWaves + wid;
-  const int npairs = a.mode == 2 ? a.N : (a.N + 1) / 2;
+  const int half = a.hd / 2;
+  const int npairs = a.mode == 2 ? a.N : a.mode == 3 ? a.N / 2 : (a.N + 1) / 2;
   const int p = min(pair, npairs - 1);  // waves past the last pair compute it again and store nothing
-  const int r0 = a.mode == 2 ? p : 2 * p;
-  const int r1 = a.mode == 2 ? a.N + p : min(2 * p + 1, a.N - 1);
+  int r0, r1;
+  if (a.mode == 2) {
+    r0 = p;
+    r1 = a.N + p;
+  } else if (a.mode == 3) {
+    r0 = (p / half) * a.hd + p % half;
+    r1 = r0 + half;
+  } else {
+    r0 = 2 * p;
+    r1 = min(2 * p + 1, a.N - 1);
+  }
   const u32x4_t* w0 = (const u32x4_t*)(a.w + (int64_t)r0 * a.w_rs);
   const u32x4_t* w1 = (const u32x4_t*)(a.w + (int64_t)r1 * a.w_rs);
   const int ns = a.K / 8;
@@ -225,7 +270,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     b0[u] = __builtin_nontemporal_load(w0 + sl);
     b1[u] = __builtin_nontemporal_load(w1 + sl);
   }
-  for (int sl = threadIdx.x; sl < ns; sl += 64 * kGemvWaves) xs[sl] = ((const u32x4_t*)a.x)[sl];
+  if (a.norm_w) {
+    auto to_lds = [&](int ch, u32x4_t v) { xs[ch] = v; };
+    if (a.norm_res) {
+      rms_norm_row<true>(a.x, a.norm_res, a.norm_w, a.K, a.eps, s_sum, to_lds, [&](int ch, u32x4_t v) {
+        if (blockIdx.x == 0) ((u32x4_t*)a.norm_res_out)[ch] = v;
+      });
+    } else {
+      rms_norm_row<false>(a.x, nullptr, a.norm_w, a.K, a.eps, s_sum, to_lds, [](int, u32x4_t) {});
+    }
+  } else {
+    for (int sl = threadIdx.x; sl < ns; sl += 64 * kGemvWaves) xs[sl] = ((const u32x4_t*)a.x)[sl];
+  }
   __syncthreads();
   float acc0 = 0.f, acc1 = 0.f;
   for (int s0 = 0;;) {
@@ -259,6 +315,23 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     return;
   }
   const float v0 = rb(acc0), v1 = rb(acc1);
+  if (a.mode == 3) {
+    const int head = p / half, d = p % half;
+    if (head < a.hq + a.hkv) {
+      const float c0 = bf16lo(a.cos[d]), s0 = bf16lo(a.sin[d]);
+      const float c1 = bf16lo(a.cos[d + half]), s1 = bf16lo(a.sin[d + half]);
+      a.y[r0] = f32_to_bf16(rb(v0 * c0) + rb(-v1 * s0));
+      a.y[r1] = f32_to_bf16(rb(v1 * c1) + rb(v0 * s1));
+      if (head >= a.hq) {
+        a.kraw[r0 - a.hq * a.hd] = f32_to_bf16(v0);
+        a.kraw[r1 - a.hq * a.hd] = f32_to_bf16(v1);
+      }
+    } else {
+      a.y[r0] = f32_to_bf16(v0);
+      a.y[r1] = f32_to_bf16(v1);
+    }
+    return;
+  }
   if (a.mode == 1) {
     a.y[r0] = f32_to_bf16(bf16lo(a.res[r0]) + v0);
     if (r1 != r0) a.y[r1] = f32_to_bf16(bf16lo(a.res[r1]) + v1);
@@ -352,15 +425,52 @@ extern "C" int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const vo
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_gemv(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
-                         int32_t mode, const void* residual, void* stream) {
-  if (!w || !x || !y || n <= 0 || k <= 0 || mode < 0 || mode > 2) return WGKV_ERR_ARG;
+extern "C" int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+                            int32_t mode, const void* residual,
+                            const void* norm_weight, const void* norm_residual, void* norm_residual_out, float eps,
+                            const void* cos, const void* sin, void* k_raw,
+                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream) {
+  if (!w || !x || !y || n <= 0 || k <= 0 || mode < 0 || mode > 3) return WGKV_ERR_ARG;
   if (mode == 1 && !residual) return WGKV_ERR_ARG;
+  if ((norm_residual == nullptr) != (norm_residual_out == nullptr) || (norm_residual && !norm_weight))
+    return WGKV_ERR_ARG;
   if (k % 8 || k > 8 * 4096 || w_row_stride % 8 || misaligned(w) || misaligned(x)) return WGKV_ERR_UNSUPPORTED;
-  GemvArgs a = {(const uint16_t*)w, w_row_stride, (const uint16_t*)x, (uint16_t*)y, (const uint16_t*)residual,
-                n, k, mode};
-  const int npairs = mode == 2 ? n : (n + 1) / 2;
+  if (norm_weight && (k > 8 * kNormChunks * kNormThreads || misaligned(norm_weight) || misaligned(norm_residual) ||
+                      misaligned(norm_residual_out)))
+    return WGKV_ERR_UNSUPPORTED;
+  if (mode == 3) {
+    if (!cos || !sin || !k_raw || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || head_dim % 2)
+      return WGKV_ERR_ARG;
+    if (n != (num_q_heads + 2 * num_kv_heads) * head_dim) return WGKV_ERR_ARG;
+  }
+  GemvArgs a = {};
+  a.w = (const uint16_t*)w;
+  a.w_rs = w_row_stride;
+  a.x = (const uint16_t*)x;
+  a.y = (uint16_t*)y;
+  a.res = (const uint16_t*)residual;
+  a.N = n;
+  a.K = k;
+  a.mode = mode;
+  a.norm_w = (const uint16_t*)norm_weight;
+  a.norm_res = (const uint16_t*)norm_residual;
+  a.norm_res_out = (uint16_t*)norm_residual_out;
+  a.eps = eps;
+  a.cos = (const uint16_t*)cos;
+  a.sin = (const uint16_t*)sin;
+  a.kraw = (uint16_t*)k_raw;
+  a.hq = num_q_heads;
+  a.hkv = num_kv_heads;
+  a.hd = mode == 3 ? head_dim : 2;
+  const int npairs = mode == 2 ? n : mode == 3 ? n / 2 : (n + 1) / 2;
   const int blocks = (npairs + kGemvWaves - 1) / kGemvWaves;
   hipLaunchKernelGGL(gemv_kernel, dim3(blocks), dim3(64 * kGemvWaves), (size_t)k * 2, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_gemv(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+                         int32_t mode, const void* residual, void* stream) {
+  if (mode == 3) return WGKV_ERR_ARG;
+  return wgkv_gemv_ex(w, w_row_stride, n, k, x, y, mode, residual, nullptr, nullptr, nullptr, 0.f, nullptr, nullptr,
+                      nullptr, 0, 0, 0, stream);
 }

@@ -111,9 +111,30 @@ class LlamaAttention(nn.Module):
         self._qkv_weight = w
 
     def forward(self, gating_mode, hidden_states, position_embeddings, attention_mask=None, past_key_value=None,
-                cache_position=None, **kwargs):
+                cache_position=None, input_norm=None, **kwargs):
+        """input_norm (optional): the decoder's input RMSNorm module, applied
+        to hidden_states here; a decode step's single row then takes the
+        norm, the q/k/v product and RoPE in one launch (wgkv_gemv_ex)."""
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, self.head_dim)
+        cos, sin = position_embeddings
+        w = self._qkv_weight
+        nw = input_norm.weight if input_norm is not None else None
+        if (w is not None and w.device == hidden_states.device and not self.qk_norm and cos.dim() == 3
+                and model_ops.qkv_rope_usable(hidden_states, w, cos, sin, nw)):
+            Hq, Hkv = self.config.num_attention_heads, self.config.num_key_value_heads
+            buf, kraw = model_ops.qkv_rope(hidden_states, w, cos, sin, Hq, Hkv, self.head_dim, nw,
+                                           input_norm.eps if input_norm is not None else 1e-5)
+            q = buf[:, :, :Hq].transpose(1, 2)
+            k = buf[:, :, Hq:Hq + Hkv].transpose(1, 2)
+            v = buf[:, :, Hq + Hkv:].transpose(1, 2)
+            pre_key = kraw.transpose(1, 2) if "pre_k" in self.config.g_inputs else None
+            out, attn_weights, g_scores = self.self_attn_forward_patch(
+                self, gating_mode, attention_mask, past_key_value, input_shape, q, pre_key, k, v)
+            out = out.reshape(*input_shape, -1).to(hidden_states.dtype).contiguous()
+            return self.o_proj(out), attn_weights, g_scores
+        if input_norm is not None:
+            hidden_states = input_norm(hidden_states)
         if self._qkv_weight is not None and self._qkv_weight.device == hidden_states.device:
             nq, nk = self.q_proj.weight.shape[0], self.k_proj.weight.shape[0]
             qkv = model_ops.linear(hidden_states, self._qkv_weight)
@@ -130,7 +151,6 @@ class LlamaAttention(nn.Module):
         k = k.transpose(1, 2)
         v = (v_src if v_src is not None else self.v_proj(hidden_states)).view(hidden_shape).transpose(1, 2)
         pre_key = k if "pre_k" in self.config.g_inputs else None
-        cos, sin = position_embeddings
         if (model_ops.usable(q, k, v, cos, sin) and self.head_dim % 16 == 0 and q.stride(3) == 1
                 and k.stride(3) == 1 and v.stride(3) == 1 and cos.dim() == 3):
             q, k, v = model_ops.rope_qkv(q, k, v, cos, sin)  # one launch, the same bf16 rounding; v copied beside k

@@ -99,8 +99,10 @@ class DecoderLayer(nn.Module):
 
     def rmsnorm_and_self_attn(self, x, pos_emb, cache):
         """Input norm, attention, residual add and the post-attention norm
-        (src/modeling_llama.py:337-371): returns (residual, MLP input)."""
-        h, _, _ = self.self_attn(3, self.input_layernorm(x), pos_emb, None, cache)
+        (src/modeling_llama.py:337-371): returns (residual, MLP input).  The
+        attention module applies the input norm (for a decode step fused with
+        the q/k/v product and RoPE)."""
+        h, _, _ = self.self_attn(3, x, pos_emb, None, cache, input_norm=self.input_layernorm)
         mlp_in, x = self.post_attention_layernorm(h, residual=x)  # residual add fused into the norm
         return x, mlp_in
 

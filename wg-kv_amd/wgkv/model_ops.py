@@ -123,6 +123,47 @@ def swiglu_linear(x, gate_up_weight):
     return F.silu(g) * u
 
 
+def qkv_rope(x, w_qkv, cos, sin, num_q_heads, num_kv_heads, head_dim, norm_weight=None, eps=1e-5):
+    """One decode row's q/k/v projection with rotary embedding (wgkv_gemv_ex
+    mode 3), optionally after the input RMSNorm: x (1, 1, hidden) bf16 (the
+    residual stream when norm_weight is given), w_qkv the stacked (n, hidden)
+    weight, cos / sin (1, 1, head_dim).  Returns (buf (1, 1, Hq + 2 Hkv, D)
+    with rotated q, rotated k and v, the unrotated k (1, 1, Hkv, D)), the
+    values wgkv_rms_norm, the product and wgkv_rope_qkv give."""
+    n = (num_q_heads + 2 * num_kv_heads) * head_dim
+    buf = torch.empty(1, 1, num_q_heads + 2 * num_kv_heads, head_dim, dtype=x.dtype, device=x.device)
+    kraw = torch.empty(1, 1, num_kv_heads, head_dim, dtype=x.dtype, device=x.device)
+    c, s_ = cos.reshape(-1), sin.reshape(-1)
+    st = _lib.lib().wgkv_gemv_ex(_ptr(w_qkv), w_qkv.stride(0), n, w_qkv.shape[-1], _ptr(x), _ptr(buf), 3, None,
+                                 _ptr(norm_weight), None, None, float(eps), _ptr(c), _ptr(s_), _ptr(kraw),
+                                 num_q_heads, num_kv_heads, head_dim, _lib.stream_handle(x.device))
+    _lib.check(st, "wgkv_gemv_ex")
+    return buf, kraw
+
+
+def rms_norm_linear(x, norm_weight, eps, weight, residual=None, mode=0):
+    """weight @ RMSNorm(x (+ residual)) for one decode row in one launch
+    (wgkv_gemv_ex with the norm prologue; mode 0 plain, 2 the SwiGLU product
+    of a stacked [gate; up] weight).  Returns (y, h) with h = x + residual
+    (None without a residual), bit for bit rms_norm followed by linear /
+    swiglu_linear."""
+    n = weight.shape[0] // 2 if mode == 2 else weight.shape[0]
+    y = torch.empty(*x.shape[:-1], n, dtype=x.dtype, device=x.device)
+    h = torch.empty_like(x) if residual is not None else None
+    st = _lib.lib().wgkv_gemv_ex(_ptr(weight), weight.stride(0), n, weight.shape[-1], _ptr(x), _ptr(y), mode, None,
+                                 _ptr(norm_weight), _ptr(residual), _ptr(h), float(eps), None, None, None, 0, 0, 0,
+                                 _lib.stream_handle(x.device))
+    _lib.check(st, "wgkv_gemv_ex")
+    return y, h
+
+
+def qkv_rope_usable(x, w_qkv, cos, sin, norm_weight=None):
+    return (gemv_usable(x, w_qkv) and usable(cos, sin) and cos.numel() == sin.numel() == cos.shape[-1]
+            and cos.is_contiguous() and sin.is_contiguous()
+            and (norm_weight is None or (usable(norm_weight) and norm_weight.is_contiguous()
+                                         and norm_weight.data_ptr() % 16 == 0 and x.shape[-1] <= 8192)))
+
+
 class Linear(nn.Linear):
     """nn.Linear (same parameters and state-dict names) whose bias-free
     one-row products -- a decode step's -- run on wgkv_gemv."""
