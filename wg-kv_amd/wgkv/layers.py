@@ -299,6 +299,22 @@ def self_attn_forward_patch_inference(self, past_key_value, input_shape, query_s
     return out
 
 
+_ALL_ADMITTED = {}
+
+
+def _all_admitted(batch_size, num_kv_heads, kv_seq_len, device):
+    """The use_baseline mask (every token admitted, src/modeling_layers.py:1556),
+    made once per shape and device (it is only read) rather than filled in
+    every layer of every step; not cached while a graph is being captured."""
+    key = (batch_size, num_kv_heads, kv_seq_len, device)
+    m = _ALL_ADMITTED.get(key)
+    if m is None:
+        m = torch.ones(batch_size, num_kv_heads, kv_seq_len, dtype=torch.bool, device=device)
+        if not (device.type == "cuda" and torch.cuda.is_current_stream_capturing()):
+            _ALL_ADMITTED[key] = m
+    return m
+
+
 def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, input_shape, query_states,
                             pre_key, key_states, value_states):
     """src/modeling_layers.py:1534-1629, inference mode (gating_mode 3)."""
@@ -313,7 +329,7 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
     g_scores = None
     g_mask = None
     if cfg.use_baseline:
-        g_mask = torch.ones(batch_size, cfg.num_key_value_heads, kv_seq_len, dtype=torch.bool, device=device)
+        g_mask = _all_admitted(batch_size, cfg.num_key_value_heads, kv_seq_len, device)
     elif not (kv_seq_len == 1 and cfg.g_defer):
         if cfg.random_sparsity is not None:
             g_scores = get_random_g_scores(self, batch_size, kv_seq_len, device)
