@@ -11,10 +11,10 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def tiny_model(gated=True, S=1000, steps=8, W=128):
+def tiny_model(gated=True, S=1000, steps=8, W=128, **kw):
     from wgkv import e2e
     ec = e2e.E2EConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
-                       num_key_value_heads=2, vocab_size=1024, rope_theta=10000.0, local_window_size=W)
+                       num_key_value_heads=2, vocab_size=1024, rope_theta=10000.0, local_window_size=W, **kw)
     torch.manual_seed(0)
     prev = torch.get_default_dtype()
     torch.set_default_dtype(torch.bfloat16)
@@ -86,15 +86,17 @@ def test_run_reports():
     assert r.kv_mib > 0 and r.model_mib > 0
 
 
-@pytest.mark.parametrize("gated", [True, False])
-def test_graph_decode_matches_eager(gated):
+@pytest.mark.parametrize("gated,qwen3", [(True, False), (False, False), (True, True)])
+def test_graph_decode_matches_eager(gated, qwen3):
     """A captured decode step replayed 6 times (with eager host work and
     synchronisations between replays) gives the eager path's logits and
-    tokens bit for bit, and the device ring pointers track the host's."""
+    tokens bit for bit, and the device ring pointers track the host's.
+    qwen3: per-head q/k norms (the decode step's q/k/v product then runs
+    without the fused RoPE) and gate width g_expand = 1.5."""
     from wgkv import e2e
     from wgkv.cache import DualCache
-    print(f"[e2e] graph decode gated={gated}", flush=True)
-    m = tiny_model(gated)
+    print(f"[e2e] graph decode gated={gated} qwen3={qwen3}", flush=True)
+    m = tiny_model(gated, **({"qk_norm": True, "g_expand": 1.5} if qwen3 else {}))
     S, chunk, n = 640, 256, 8  # chunks 256, 256, 128 (each >= W)
     ids = torch.randint(0, 1000, (1, S), generator=torch.Generator().manual_seed(3)).to(DEV)
     if gated:
