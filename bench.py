@@ -42,6 +42,7 @@ def parse():
                         "chunked prefill of --e2e-prompt tokens then --e2e-steps greedy decode steps, "
                         "gated and all-admitted, on one GPU (several minutes)")
     p.add_argument("--e2e-prompt", type=int, default=400000)
+    p.add_argument("--e2e-chunk", type=int, default=4096, help="prompt tokens per prefill chunk")
     p.add_argument("--e2e-steps", type=int, default=256)
     p.add_argument("--e2e-layers", type=int, default=32)
     p.add_argument("--e2e-admit", type=float, default=0.30)
@@ -395,7 +396,7 @@ def e2e_section(args):
     tag = "qwen3_8b" if args.e2e_model == "qwen3-8b" else "llama8b"
     out = {"workload": f"e2e_{tag}_{S // 1000}k (BASELINE config 5): {ec.num_hidden_layers} layers, "
                        f"hidden {ec.hidden_size}, FFN {ec.intermediate_size}, vocab {ec.vocab_size}, "
-                       f"prompt {S} in 4096-token chunks, {steps} greedy decode steps, W {W}",
+                       f"prompt {S} in {args.e2e_chunk}-token chunks, {steps} greedy decode steps, W {W}",
            "data": "synthetic: random-init bf16 weights, uniform random token ids"}
     log("calibrating the gates")
     e2e.calibrate_gates(model, ids, args.e2e_admit)
@@ -408,7 +409,7 @@ def e2e_section(args):
         model.cfg.max_tokens_per_head = S + steps + 2 * W
         model.cfg.max_total_tokens = ec.num_hidden_layers * ec.num_key_value_heads * per_head
         log(f"{name}: prefill {S} tokens")
-        r = e2e.run(model, ids, steps, progress=log, graph=True)
+        r = e2e.run(model, ids, steps, chunk=args.e2e_chunk, progress=log, graph=True)
         torch.cuda.empty_cache()
         dm = sorted(r.decode_ms)
         tpot = sum(r.decode_ms) / len(r.decode_ms)
@@ -424,7 +425,7 @@ def e2e_section(args):
             log(f"{name}: eager run timing {args.e2e_profile}, MLP and LM head per phase")
             for key in timers.ms:
                 timers.ms[key] = 0.0
-            rp = e2e.run(model, ids, args.e2e_profile_steps, progress=log, timers=timers)
+            rp = e2e.run(model, ids, args.e2e_profile_steps, chunk=args.e2e_chunk, progress=log, timers=timers)
             torch.cuda.empty_cache()
             out[name]["profile"] = {"attn_granularity": args.e2e_profile, "decode_steps": args.e2e_profile_steps,
                                     "eager_prefill_ms": round(rp.prefill_ms, 1),

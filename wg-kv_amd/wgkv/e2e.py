@@ -80,8 +80,14 @@ class MLP(nn.Module):
         gu = self._gate_up
         if gu is not None and gu.device == x.device and model_ops.gemv_usable(x, gu):
             return model_ops.linear(model_ops.swiglu_linear(x, gu), self.down_proj.weight, residual=residual)
-        # prompts: separate GEMMs and the fused SwiGLU product
-        g, u = self.gate_proj(x), self.up_proj(x)
+        # prompts: one GEMM for gate and up (hipBLASLt at 4096 rows: 635 us
+        # against 2 x 365 us), then the fused SwiGLU product of its halves
+        if gu is not None and gu.device == x.device:
+            n = gu.shape[0] // 2
+            gup = F.linear(x, gu)
+            g, u = gup[..., :n], gup[..., n:]
+        else:
+            g, u = self.gate_proj(x), self.up_proj(x)
         if model_ops.usable(g, u) and g.shape[-1] % 8 == 0 and g.stride(-1) == 1 and u.stride(-1) == 1:
             out = self.down_proj(model_ops.silu_mul(g, u))
         else:
