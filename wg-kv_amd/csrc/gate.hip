@@ -235,7 +235,10 @@ __device__ __forceinline__ float reduce16_columns(const float (&v)[16], int lane
 }
 
 constexpr int kSmallTok = 4;
-constexpr int kSmallWaves = 4;
+#ifndef WGKV_GATE_SMALL_WAVES
+#define WGKV_GATE_SMALL_WAVES 4
+#endif
+constexpr int kSmallWaves = WGKV_GATE_SMALL_WAVES;
 constexpr int kSplitCols = 16 * kSmallWaves;  // hidden columns per workgroup and pass
 
 template <int K>
@@ -275,10 +278,9 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   const int c_first = split * kSplitCols + wid * 16;
   if (c_first < a.inner) load_rows(c_first);
 
-  // normalised inputs -> LDS: wave w handles token w; all its input loads
+  // normalised inputs -> LDS: wave w handles tokens w, w + waves, ...; all its input loads
   // are issued before the first reduction
-  if (wid < nt) {
-    const int s = wid;
+  for (int s = wid; s < nt; s += kSmallWaves) {
     float v[3][2];
 #pragma unroll
     for (int i = 0; i < 3; ++i)
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
         if (d < D) {
           float y = a.rms ? v[i][e] * scale : v[i][e];
           if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
-          xs[wid][i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+          xs[s][i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
         }
       }
     }
