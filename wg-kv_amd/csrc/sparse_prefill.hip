@@ -99,7 +99,7 @@ struct PrefillArgs {
   // are logical indices into each head's paged global cache (block table row
   // bt + h*bt_sh, already offset past the local pages), band keys below c0
   // come from the ring (pool row ring_row0 + h*W + p - (c0 - W)).
-  int c0, W, page;
+  int c0, W;  // pages of the global cache are kPage tokens
   const uint16_t* pool_k;
   const uint16_t* pool_v;
   const int32_t* bt;
@@ -477,7 +477,6 @@ extern "C" int wgkv_sparse_prefill_attn(
   a.scale_log2 = softmax_scale * kLog2e;
   a.c0 = 0;
   a.W = 0;
-  a.page = 16;
   a.pool_k = a.pool_v = nullptr;
   a.bt = nullptr;
   a.bt_sh = 0;
@@ -527,7 +526,6 @@ extern "C" int wgkv_chunk_prefill_attn(
   a.scale_log2 = softmax_scale * kLog2e;
   a.c0 = chunk_start;
   a.W = local_window;
-  a.page = page_size;
   a.pool_k = (const uint16_t*)pool_k;
   a.pool_v = (const uint16_t*)pool_v;
   a.bt = block_table + ((int64_t)layer * num_kv_heads) * max_pages_per_head + local_window / page_size;
