@@ -135,3 +135,24 @@ def test_packed_weights_follow_in_place_updates_and_misaligned_inputs_fall_back(
     kk_m.copy_(kk)
     third, mask3 = g.scores_and_mask(pk_m, kk_m, None, 0.5)
     compare(third, mask3, ref, 0.5, "misaligned inputs (fp32 path)", bf16_inputs=True)
+
+
+def test_packed_path_without_rms_matches_fp32_path():
+    """g_rms = False (no input norms, GatingPredictor's Identity norms): the
+    packed planes hold conv1.weight itself and the scores equal the fp32
+    MFMA path's to fp32 rounding (both multiply the bf16 inputs exactly)."""
+    from wgkv import gate as wgate
+    H, D, S = 8, 128, 1024
+    gen = torch.Generator().manual_seed(21)
+    g, params = make_gate(("pre_k", "post_k"), H, D, 4.0, gen, rms=False)
+    pre_k, post_k = (torch.randn(1, H, S, D, generator=gen).to(torch.bfloat16).cuda() for _ in range(2))
+    scores, mask = g.scores_and_mask(pre_k, post_k, None, 0.5)
+    assert g.__dict__.get("_packed_cache") is not None
+    s32, m32 = wgate.gate_scores_and_mask(pre_k, post_k, None, None, None, None, g.conv1.weight.detach(),
+                                          g.conv1.bias.detach(), g.conv2.weight.detach(), g.conv2.bias.detach(),
+                                          g.inner_dim, g.act, False, 0.0, 0.5, like=post_k)
+    d = (scores - s32).abs().max().item()
+    print(f"[gate packed, no rms] max|dg| vs fp32 path = {d:.2e}", flush=True)
+    assert d <= 2e-6
+    near = (s32 - 0.5).abs() < 1e-6
+    assert torch.equal(mask[~near], m32[~near])
