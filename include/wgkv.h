@@ -384,6 +384,12 @@ int wgkv_quest_select(
  *   copied alongside (v and v_out may be NULL), so the three outputs can
  *   share one buffer and its strides.  Every tensor has element strides
  *   (batch, seq, head) and a contiguous head_dim; D a multiple of 16.
+ * wgkv_rope_qkv_norm -- wgkv_rope_qkv after Qwen3's per-head q_norm / k_norm
+ *   (src/modeling_qwen3.py:235-239; weights of head_dim bf16, either may be
+ *   NULL): x = bf16(w * bf16(x * rsqrt(mean_head(x^2) + eps))) before the
+ *   rotation; k_pre (may be NULL; needs k_norm_weight) receives the
+ *   normalised, unrotated k (the gate's pre-RoPE key) with strides (batch,
+ *   seq, head).  head_dim <= 256 with a norm.
  * wgkv_silu_mul -- LlamaMLP's act_fn(gate) * up (:161): rows of `cols`
  *   bf16 (cols a multiple of 8), gate and up with their own row strides
  *   (e.g. the two halves of one fused projection), out contiguous.
@@ -420,6 +426,17 @@ int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                   void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
                   int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
                   int32_t head_dim, void* stream);
+
+int wgkv_rope_qkv_norm(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                       const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                       const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                       const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                       void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                       void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                       void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
+                       int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                       int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight, float eps,
+                       void* k_pre, int64_t kp_sb, int64_t kp_ss, int64_t kp_sh, void* stream);
 
 int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,
                   void* out, int64_t rows, int32_t cols, void* stream);

@@ -169,3 +169,42 @@ def test_qkv_rope_equals_product_then_rope(with_norm, Hq, Hkv, D):
     assert torch.equal(buf[:, :, Hq:Hq + Hkv].transpose(1, 2), fk)
     assert torch.equal(buf[:, :, Hq + Hkv:].transpose(1, 2), fv)
     assert torch.equal(kraw.transpose(1, 2), k)
+
+
+@pytest.mark.parametrize("S,D", [(1, 128), (300, 128), (77, 64)])
+def test_rope_with_qwen3_head_norms_matches_torch(S, D):
+    """Qwen3's per-head q_norm / k_norm fused into the RoPE launch against
+    HeadRMSNorm followed by wgkv_rope_qkv (itself bit-identical to
+    apply_rotary_pos_emb): the only difference allowed is the order of the
+    per-head sum of squares, which can move an element by one bf16 unit; the
+    normalised, unrotated k equals k_norm(k) to the same bound."""
+    from wgkv import model_ops
+    from wgkv.attention import HeadRMSNorm, LlamaRotaryEmbedding
+    print(f"[model_ops] rope + head norms S{S} D{D}", flush=True)
+    g = torch.Generator().manual_seed(S + D)
+    B, Hq, Hkv = 1, 8, 2
+    qkv = torch.randn(B, S, Hq + 2 * Hkv, D, generator=g).to(torch.bfloat16).to(DEV) * 3
+    q, k, v = (qkv[:, :, :Hq].transpose(1, 2), qkv[:, :, Hq:Hq + Hkv].transpose(1, 2),
+               qkv[:, :, Hq + Hkv:].transpose(1, 2))
+    qn, kn = HeadRMSNorm(D).to(DEV).to(torch.bfloat16), HeadRMSNorm(D).to(DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        qn.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+        kn.weight.copy_(1 + 0.1 * torch.randn(D, generator=g))
+    rot = LlamaRotaryEmbedding(D, 1e6, device=DEV)
+    cos, sin = rot(qkv, torch.arange(1000, 1000 + S, device=DEV)[None])
+    fq, fk, fv, fkp = model_ops.rope_qkv(q, k, v, cos, sin, qn.weight, kn.weight, qn.eps)
+    with torch.no_grad():
+        q2, k2 = qn(q), kn(k)
+    rq, rk, rv = model_ops.rope_qkv(q2, k2, v, cos, sin)
+
+    def ulps(a, b):
+        a, b = a.float(), b.float()
+        ulp = torch.exp2(torch.floor(torch.log2(b.abs().clamp_min(1e-30))) - 7)
+        return ((a - b).abs() / ulp)
+
+    for name, x, y in (("q", fq, rq), ("k", fk, rk), ("k_pre", fkp, k2)):
+        u = ulps(x, y)
+        frac = (u > 0).float().mean().item()
+        print(f"   {name}: max {u.max().item():.1f} ulp, {frac:.4%} elements differ", flush=True)
+        assert u.max().item() <= 2.0 and frac <= 0.002, name
+    assert torch.equal(fv, rv)

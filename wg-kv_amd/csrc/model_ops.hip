@@ -116,6 +116,10 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_kernel(NormArgs a) {
 // out[d] = bf16(bf16(x[d] cos[d]) + bf16(-x[d+h] sin[d])),
 // out[d+h] = bf16(bf16(x[d+h] cos[d+h]) + bf16(x[d] sin[d+h])), h = D/2;
 // v is copied, so the three outputs can share one buffer and strides.
+// Optionally q and k first get Qwen3's per-head RMSNorm (nw[0], nw[1]):
+// x <- bf16(w * bf16(x * rsqrt(mean_head(x^2) + eps))), the sum of squares
+// reduced over the D/16 threads of the head; the normalised k before the
+// rotation (the gate's pre-RoPE key) is also stored to kpre.
 struct RopeArgs {
   const uint16_t* in[3];
   int64_t is[3][3];
@@ -126,6 +130,10 @@ struct RopeArgs {
   const uint16_t* sin;
   int64_t cs_sb, cs_ss;
   int B, S, D;
+  const uint16_t* nw[2];
+  float eps;
+  uint16_t* kpre;
+  int64_t kp[3];
 };
 
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
@@ -162,6 +170,32 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   float x1[8], x2[8], c1[8], c2[8], s1[8], s2[8], o1[8], o2[8];
   unpack8(w1, x1);
   unpack8(w2, x2);
+  if (a.nw[ten]) {
+    // the head's D/16 threads are consecutive lanes (hch divides 64)
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(x1[e], x1[e], ss);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(x2[e], x2[e], ss);
+    if (hch >= 2) ss += dpp_f32<WGKV_DPP_QP_1032>(ss);
+    if (hch >= 4) ss += dpp_f32<WGKV_DPP_QP_2301>(ss);
+    if (hch >= 8) ss += dpp_f32<WGKV_DPP_ROW_HALF_MIRROR>(ss);
+    if (hch >= 16) ss += dpp_f32<WGKV_DPP_ROW_MIRROR>(ss);
+    const float scale = rsqrtf(ss / (float)a.D + a.eps);
+    float n1[8], n2[8];
+    unpack8(*(const u32x4_t*)(a.nw[ten] + d0), n1);
+    unpack8(*(const u32x4_t*)(a.nw[ten] + half + d0), n2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x1[e] = rb(n1[e] * rb(x1[e] * scale));
+      x2[e] = rb(n2[e] * rb(x2[e] * scale));
+    }
+    if (ten == 1 && a.kpre) {
+      uint16_t* kp = a.kpre + b * a.kp[0] + s * a.kp[1] + hh * a.kp[2];
+      *(u32x4_t*)(kp + d0) = pack8(x1);
+      *(u32x4_t*)(kp + half + d0) = pack8(x2);
+    }
+  }
   unpack8(*(const u32x4_t*)(cs + d0), c1);
   unpack8(*(const u32x4_t*)(cs + half + d0), c2);
   unpack8(*(const u32x4_t*)(sn + d0), s1);
@@ -365,7 +399,7 @@ extern "C" int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* re
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+extern "C" int wgkv_rope_qkv_norm(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
                              const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
                              const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
                              const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
@@ -373,10 +407,15 @@ extern "C" int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t 
                              void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
                              void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
                              int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
-                             int32_t head_dim, void* stream) {
+                             int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight, float eps,
+                             void* k_pre, int64_t kp_sb, int64_t kp_ss, int64_t kp_sh, void* stream) {
   if (!q || !k || !cos || !sin || !q_out || !k_out || (v == nullptr) != (v_out == nullptr)) return WGKV_ERR_ARG;
   if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0 || num_kv_heads <= 0) return WGKV_ERR_ARG;
   if (head_dim % 16) return WGKV_ERR_UNSUPPORTED;
+  if ((q_norm_weight || k_norm_weight) && head_dim > 256) return WGKV_ERR_UNSUPPORTED;
+  if (misaligned(q_norm_weight) || misaligned(k_norm_weight) || misaligned(k_pre)) return WGKV_ERR_UNSUPPORTED;
+  if (k_pre && !k_norm_weight) return WGKV_ERR_ARG;
+  if ((kp_sb | kp_ss | kp_sh) & 7) return WGKV_ERR_UNSUPPORTED;
   if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(cos) || misaligned(sin) || misaligned(q_out) ||
       misaligned(k_out) || misaligned(v_out))
     return WGKV_ERR_UNSUPPORTED;
@@ -407,9 +446,31 @@ extern "C" int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t 
   a.B = batch;
   a.S = seq_len;
   a.D = head_dim;
+  a.nw[0] = (const uint16_t*)q_norm_weight;
+  a.nw[1] = (const uint16_t*)k_norm_weight;
+  a.eps = eps;
+  a.kpre = (uint16_t*)k_pre;
+  a.kp[0] = kp_sb;
+  a.kp[1] = kp_ss;
+  a.kp[2] = kp_sh;
   const int64_t total = (int64_t)batch * seq_len * (a.H[0] + a.H[1] + a.H[2]) * (head_dim / 16);
   hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                             const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                             const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                             const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                             void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                             void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                             void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
+                             int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, void* stream) {
+  return wgkv_rope_qkv_norm(q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, v, v_sb, v_ss, v_sh, cos, sin, cs_sb, cs_ss,
+                            q_out, qo_sb, qo_ss, qo_sh, k_out, ko_sb, ko_ss, ko_sh, v_out, vo_sb, vo_ss, vo_sh,
+                            batch, seq_len, num_q_heads, num_kv_heads, head_dim, nullptr, nullptr, 0.f, nullptr,
+                            0, 0, 0, stream);
 }
 
 extern "C" int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const void* up, int64_t up_row_stride,

@@ -107,6 +107,11 @@ SIGNATURES = {
                                      c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64,
                                      c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,
                                      c_ptr, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr]),
+    "wgkv_rope_qkv_norm": (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,
+                                          c_ptr, c_i64, c_i64, c_i64, c_ptr, c_ptr, c_i64, c_i64,
+                                          c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,
+                                          c_ptr, c_i64, c_i64, c_i64, c_i32, c_i32, c_i32, c_i32, c_i32,
+                                          c_ptr, c_ptr, c_f32, c_ptr, c_i64, c_i64, c_i64, c_ptr]),
     "wgkv_silu_mul": (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_i32, c_ptr]),
     "wgkv_gemv": (ctypes.c_int, [c_ptr, c_i64, c_i32, c_i32, c_ptr, c_ptr, c_i32, c_ptr, c_ptr]),
     "wgkv_gemv_ex": (ctypes.c_int, [c_ptr, c_i64, c_i32, c_i32, c_ptr, c_ptr, c_i32, c_ptr,

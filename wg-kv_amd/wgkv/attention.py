@@ -145,14 +145,26 @@ class LlamaAttention(nn.Module):
             q = self.q_proj(hidden_states).view(hidden_shape)
             k = self.k_proj(hidden_states).view(hidden_shape)
             v_src = None
-        if self.qk_norm:
+        v = (v_src if v_src is not None else self.v_proj(hidden_states)).view(hidden_shape)
+        fused_rope = (model_ops.usable(q, k, v, cos, sin) and self.head_dim % 16 == 0 and q.stride(3) == 1
+                      and k.stride(3) == 1 and v.stride(3) == 1 and cos.dim() == 3)
+        # Qwen3's head norms go into the RoPE launch when its weights are bf16
+        fused_norm = (self.qk_norm and fused_rope and self.head_dim <= 256
+                      and model_ops.usable(self.q_norm.weight, self.k_norm.weight)
+                      and self.q_norm.eps == self.k_norm.eps)
+        if self.qk_norm and not fused_norm:
             q, k = self.q_norm(q), self.k_norm(k)
         q = q.transpose(1, 2)
         k = k.transpose(1, 2)
-        v = (v_src if v_src is not None else self.v_proj(hidden_states)).view(hidden_shape).transpose(1, 2)
+        v = v.transpose(1, 2)
         pre_key = k if "pre_k" in self.config.g_inputs else None
-        if (model_ops.usable(q, k, v, cos, sin) and self.head_dim % 16 == 0 and q.stride(3) == 1
-                and k.stride(3) == 1 and v.stride(3) == 1 and cos.dim() == 3):
+        if fused_norm:
+            # one launch: per-head norms, then the rotation; the normalised,
+            # unrotated k is the gate's pre-RoPE key (modeling_qwen3.py:235-239)
+            q, k, v, kn = model_ops.rope_qkv(q, k, v, cos, sin, self.q_norm.weight, self.k_norm.weight,
+                                             self.q_norm.eps)
+            pre_key = kn if "pre_k" in self.config.g_inputs else None
+        elif fused_rope:
             q, k, v = model_ops.rope_qkv(q, k, v, cos, sin)  # one launch, the same bf16 rounding; v copied beside k
         else:
             q, k = apply_rotary_pos_emb(q, k, cos, sin)

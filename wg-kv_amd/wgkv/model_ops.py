@@ -44,16 +44,19 @@ def rms_norm(x, weight, eps, residual=None):
     return out.view(x.shape), None if ores is None else ores.view(x.shape)
 
 
-def rope_qkv(q, k, v, cos, sin):
+def rope_qkv(q, k, v, cos, sin, q_norm_weight=None, k_norm_weight=None, eps=1e-6):
     """q (B,Hq,S,D), k / v (B,Hkv,S,D) views (d contiguous), cos/sin (B,S,D)
     -> (rotated q, rotated k, v) as (B,H,S,D) views of one contiguous
-    (B, S, Hq+2*Hkv, D) buffer, so k and v share strides."""
+    (B, S, Hq+2*Hkv, D) buffer, so k and v share strides.  With Qwen3's head
+    norm weights (both given) q and k are normalised per head first and the
+    normalised, unrotated k is returned as a fourth (B,Hkv,S,D) view."""
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     if cos.stride(-1) != 1:
         cos, sin = cos.contiguous(), sin.contiguous()
     buf = torch.empty(B, S, Hq + 2 * Hkv, D, dtype=q.dtype, device=q.device)
     qo, ko, vo = buf[:, :, :Hq], buf[:, :, Hq:Hq + Hkv], buf[:, :, Hq + Hkv:]
+    norm = q_norm_weight is not None
 
     def st(t):  # (batch, seq, head) strides of a (B, H, S, D) view
         return t.stride(0), t.stride(2), t.stride(1)
@@ -61,10 +64,15 @@ def rope_qkv(q, k, v, cos, sin):
     def so(t):  # of a (B, S, H, D) view
         return t.stride(0), t.stride(1), t.stride(2)
 
-    r = _lib.lib().wgkv_rope_qkv(
+    kp = torch.empty(B, S, Hkv, D, dtype=q.dtype, device=q.device) if norm else None
+    r = _lib.lib().wgkv_rope_qkv_norm(
         _ptr(q), *st(q), _ptr(k), *st(k), _ptr(v), *st(v), _ptr(cos), _ptr(sin), cos.stride(0), cos.stride(1),
-        _ptr(qo), *so(qo), _ptr(ko), *so(ko), _ptr(vo), *so(vo), B, S, Hq, Hkv, D, _lib.stream_handle(q.device))
-    _lib.check(r, "wgkv_rope_qkv")
+        _ptr(qo), *so(qo), _ptr(ko), *so(ko), _ptr(vo), *so(vo), B, S, Hq, Hkv, D,
+        _ptr(q_norm_weight), _ptr(k_norm_weight), float(eps), _ptr(kp), *(so(kp) if norm else (0, 0, 0)),
+        _lib.stream_handle(q.device))
+    _lib.check(r, "wgkv_rope_qkv_norm")
+    if norm:
+        return qo.transpose(1, 2), ko.transpose(1, 2), vo.transpose(1, 2), kp.transpose(1, 2)
     return qo.transpose(1, 2), ko.transpose(1, 2), vo.transpose(1, 2)
 
 
