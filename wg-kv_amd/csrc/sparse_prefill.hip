@@ -326,13 +326,17 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
         mx = fmax_ieee(mx, fmax_ieee(fmax_ieee(sc[kt][rt][0], sc[kt][rt][1]), fmax_ieee(sc[kt][rt][2], sc[kt][rt][3])));
-      mx = xor16_max(mx);
-      mx = xor32_max(mx);
-      mxs[rt] = mx * a.scale_log2;
+      mxs[rt] = mx;  // this lane's 16 keys of the row
     }
-    const bool need0 = mxs[0] > m_run[0] + kRescaleSlack;
-    const bool need1 = mxs[1] > m_run[1] + kRescaleSlack;
-    if (__builtin_amdgcn_ballot_w64(need0 || need1) != 0) {
+    // A row needs the rescale iff one of its four lanes' maxima exceeds
+    // m_run by the slack (the scale is positive, so scaling commutes with
+    // the max); only then are the row maxima reduced across the lanes.
+    if (__builtin_amdgcn_ballot_w64(mxs[0] * a.scale_log2 > m_run[0] + kRescaleSlack ||
+                                    mxs[1] * a.scale_log2 > m_run[1] + kRescaleSlack) != 0) {
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) mxs[rt] = xor32_max(xor16_max(mxs[rt])) * a.scale_log2;
+      const bool need0 = mxs[0] > m_run[0] + kRescaleSlack;
+      const bool need1 = mxs[1] > m_run[1] + kRescaleSlack;
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         const bool need = rt == 0 ? need0 : need1;
