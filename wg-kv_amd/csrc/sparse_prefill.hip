@@ -199,33 +199,39 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   // the row loads means no wait for an index also waits for the rows issued
   // before it (memory counters retire in order).
   struct Idx {
-    int k[KPT];     // per item: column position / page id / band position
+    // per item: one-shot mode, the column or band position of the lane's
+    // row; chunked mode, admitted columns, the page id of the wave's 1 KB
+    // block (uniform; band rows need no index in chunked mode)
+    int k[KPT];
   };
-  const int32_t* bt_h = CHUNK ? a.bt + (int64_t)h * a.bt_sh : nullptr;
+  // In chunked mode the 4 rows of a wave's 1 KB block are 4 consecutive
+  // logical entries of the head's global cache, aligned to 4, so they lie in
+  // one 16-token page: the page id is one scalar load per block and the row
+  // address is that page's (scalar) base plus a 32-bit lane offset.
+  const int32_t __attribute__((address_space(4)))* bt_h =
+      CHUNK ? (const int32_t __attribute__((address_space(4)))*)(a.bt + (int64_t)h * a.bt_sh) : nullptr;
   auto tile_idx = [&](int tl, Idx& ix) {
     if (tl < n_vtiles) {
       const int nval = min(kBlk, nv - tl * kBlk);
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
-        const int j = tl * kBlk + min(krow[i], nval - 1);
-        ix.k[i] = CHUNK ? bt_h[(unsigned)j / kPage] : cidx[j];  // j >= 0
+        if (CHUNK) {
+          const int first = (wid + i * NW) * RPB;  // first row of the block (uniform)
+          ix.k[i] = bt_h[(unsigned)(tl * kBlk + min(first, nval - 1)) / kPage];
+        } else {
+          ix.k[i] = cidx[tl * kBlk + min(krow[i], nval - 1)];
+        }
       }
-    } else {
-      const int b0 = CHUNK ? band_start + (tl - n_vtiles) * kBlk : bofs[r * a.bo_width + (tl - n_vtiles)];
+    } else if (!CHUNK) {
+      const int b0 = bofs[r * a.bo_width + (tl - n_vtiles)];
 #pragma unroll
       for (int i = 0; i < KPT; ++i) ix.k[i] = min(b0 + krow[i], a.S - 1);
     }
   };
-  // row start of key x of tile tl in the K (or V) source
-  auto row_ptr = [&](int tl, bool vertical, int x, int key_in_tile, const uint16_t* tensor_base,
-                     const uint16_t* pool) -> const uint16_t* {
-    if (vertical) {
-      if (CHUNK) {
-        const int j = tl * kBlk + key_in_tile;
-        return pool + ((int64_t)x * kPage + (unsigned)j % kPage) * D;  // j >= 0
-      }
-      return tensor_base + (int64_t)x * a.kv_ss;
-    }
+  // row start of key x of tile tl in the K (or V) source (not the chunked
+  // mode's admitted columns, which tile_load addresses by page)
+  auto row_ptr = [&](bool vertical, int x, const uint16_t* tensor_base, const uint16_t* pool) -> const uint16_t* {
+    if (vertical) return tensor_base + (int64_t)x * a.kv_ss;
     if (CHUNK && x < a.c0) return pool + (a.ring_row0 + (int64_t)h * a.W + (x - (a.c0 - a.W))) * D;
     return tensor_base + (int64_t)(x - (CHUNK ? a.c0 : 0)) * a.kv_ss;
   };
@@ -236,8 +242,17 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     for (int i = 0; i < KPT; ++i) {
       const int kt = min(krow[i], nval - 1);
       const int blk = (wid + i * NW) * 512;  // element offset of this wave's block (1 KB)
-      lds_dma16(row_ptr(tl, vertical, ix.k[i], kt, kbase, a.pool_k) + kcolK[i] * 8, dK + blk);
-      lds_dma16(row_ptr(tl, vertical, ix.k[i], kt, vbase, a.pool_v) + kcolV[i] * 8, dV + blk);
+      if (CHUNK && vertical) {
+        // tl * kBlk is a multiple of the page, so the slot is kt % kPage
+        const int64_t page_base = (int64_t)ix.k[i] * (kPage * D);
+        const int lane_row = (kt % kPage) * D;
+        lds_dma16(a.pool_k + page_base + (lane_row + kcolK[i] * 8), dK + blk);
+        lds_dma16(a.pool_v + page_base + (lane_row + kcolV[i] * 8), dV + blk);
+      } else {
+        const int x = CHUNK ? min(band_start + (tl - n_vtiles) * kBlk + krow[i], a.S - 1) : ix.k[i];
+        lds_dma16(row_ptr(vertical, x, kbase, a.pool_k) + kcolK[i] * 8, dK + blk);
+        lds_dma16(row_ptr(vertical, x, vbase, a.pool_v) + kcolV[i] * 8, dV + blk);
+      }
     }
   };
   // Per-lane LDS element offsets of the fragments (the slice permutations
