@@ -107,6 +107,7 @@ CASES = [
     (1, 3, 2, 128, 64, [64, 64, 128, 1000], 1.0, False),
     (1, 2, 1, 64, 128, [128, 256, 130], 0.0, False),
     (1, 4, 8, 128, 256, [2000], 0.2, False),
+    (1, 2, 8, 128, 256, [1024, 1024, 512], 0.3, False),  # two head groups per KV head, continued chunks
 ]
 
 
