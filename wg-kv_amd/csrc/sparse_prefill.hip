@@ -303,17 +303,23 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    // K fragments of k-step j+1 are read while the MFMAs of k-step j run
+    bf16x8_t kf[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+      kf[0][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[0]]));
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
-      bf16x8_t kf[4];
+      if (j + 1 < KS)
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        kf[kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[j]]));
+        for (int kt = 0; kt < 4; ++kt)
+          kf[(j + 1) & 1][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[j + 1]]));
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt)
-          sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kt], qb[rt][j], sc[kt][rt], 0, 0, 0);
+          sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j & 1][kt], qb[rt][j], sc[kt][rt], 0, 0, 0);
     }
     // tiles whose 64 keys are all visible to all 32 rows of the wave skip masking
     const bool full = vert ? nvalid == kBlk : (band0 + kBlk - 1 <= row0 && band0 + kBlk <= a.S);
