@@ -289,6 +289,13 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     // landed; the barrier publishes every wave's and frees the other buffer
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
     __syncthreads();
+    // K fragments of k-step j+1 are read while the MFMAs of k-step j run;
+    // those of k-step 0 before the next tile's loads are issued
+    bf16x8_t kf[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt)
+      kf[0][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[0]]));
+    __builtin_amdgcn_sched_barrier(0);
     // the next tile's rows stream into the other buffer under this tile's arithmetic
     if (tile + 1 < ntiles) {
       tile_load(tile + 1, idx_next, nK, nV);
@@ -303,11 +310,6 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     for (int kt = 0; kt < 4; ++kt)
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    // K fragments of k-step j+1 are read while the MFMAs of k-step j run
-    bf16x8_t kf[2][4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-      kf[0][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[0]]));
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
       if (j + 1 < KS)
