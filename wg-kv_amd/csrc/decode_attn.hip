@@ -369,8 +369,9 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   const int vq = i * NQ + t % NQ, grp = t / NQ;
 
   // Chunks are read in batches of kBatch with every load issued before the
-  // (branch-free) online update consumes them.
-  constexpr int kBatch = 8;
+  // (branch-free) online update consumes them; 16 covers the ~100 chunks of
+  // a head at batch 1 (8 groups) in one round of loads.
+  constexpr int kBatch = 16;
   float M = -INFINITY, L = 0.f;
   f32x4_t A = (f32x4_t){0.f, 0.f, 0.f, 0.f};
   for (int cb = c0 + grp; cb < c1; cb += GROUPS * kBatch) {
