@@ -61,7 +61,7 @@ def parse():
 # HBM bytes per config-3 decode call, from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes over `bench.py --traffic-probe`, each scaled by what the
 # counter reads for a 1 GiB device copy (profiles/decode_attn_traffic_b8_128k.md)
-DECODE_TRAFFIC_BYTES = 1415738794
+DECODE_TRAFFIC_BYTES = 1347666061
 
 
 def time_op(fn, steps, warmup):
