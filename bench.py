@@ -60,8 +60,24 @@ def parse():
 
 # HBM bytes per config-3 decode call, from rocprofv3 --pmc FETCH_SIZE and
 # WRITE_SIZE passes over `bench.py --traffic-probe`, each scaled by what the
-# counter reads for a 1 GiB device copy (profiles/decode_attn_traffic_b8_128k.md)
+# counter reads for a 1 GiB device copy in the same program; the summary with
+# the commands and raw counter values is DECODE_TRAFFIC_SOURCE
 DECODE_TRAFFIC_BYTES = 1347666061
+DECODE_TRAFFIC_SOURCE = "profiles/decode_attn_traffic_b8_128k.md"
+
+
+def host_cpu():
+    """The host's CPU model (from /proc/cpuinfo) and logical CPU count."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count()}
 
 
 def time_op(fn, steps, warmup):
@@ -118,6 +134,7 @@ def cpu_baseline(w, budget_s):
         "value": round(1.0 / per_seq, 3),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        **host_cpu(),
         "kind": "port",
         "sample": (f"oracle.attention.paged_decode (torch fp32 CPU): {done} sequence decodes cycling over the "
                    f"batch of {B} ({tokens} cached tokens attended, {t_total:.1f} s); one decode token per "
@@ -357,7 +374,7 @@ def layer_section(dev, cpu_budget):
                 "note": "whole layer incl. projections/RoPE/gate; includes host launch overhead"},
         "cpu_reference_path": {"prefill_ms": round(c_pre, 2), "decode_ms_per_step": round(c_dec, 3),
                                "decode_tokens_per_s": round(1e3 / c_dec, 1), "cores": torch.get_num_threads(),
-                               "kind": "port", "runs": len(cruns),
+                               **host_cpu(), "kind": "port", "runs": len(cruns),
                                "sample": "oracle.llama_layer.OracleLayer fp32 on the host cores; median of runs"},
     }
 
@@ -501,8 +518,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
             "traffic": DECODE_TRAFFIC_BYTES,
+            "traffic_source": DECODE_TRAFFIC_SOURCE,
             "bytes_per_launch": nbytes,
-            "launch": "wgkv_paged_decode_attn = decode_split_kernel + decode_merge_kernel",
+            "launch": "wgkv_paged_decode_attn = decode_split_kernel (split-K chunks, last arriver merges)",
         },
     }
     if not args.no_secondary:

@@ -135,3 +135,52 @@ def test_handle_matches_direct_call():
     b = wgkv.flash_attn_with_kvcache_wrapper(w.q, w.k_cache, w.v_cache, w.cache_seqlens, w.block_table, w.softmax_scale)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("heads", [(6, 2), (12, 4), (16, 2), (64, 8)])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("B", [1, 3])
+@pytest.mark.parametrize("max_len", [123, 4000])
+def test_grouped_heads_3_and_8(heads, D, B, max_len):
+    """G = 3 and G = 8 query heads per KV head (two MFMA head groups at G = 8)."""
+    q, k, v, sl, bt = reference_grid_case(heads, D, 16, B, max_len, seed=hash((heads, D, B, max_len, 38)) & 0xffff)
+    run_and_compare(q, k, v, sl, bt, D ** -0.5, f"G{heads[0] // heads[1]} {heads} D{D} B{B} L{max_len}")
+
+
+@pytest.mark.parametrize("B,Hkv", [(16, 8), (3, 32), (256, 8)])
+def test_block_planner_many_heads(B, Hkv):
+    """More than 64 (sequence, KV head) pairs: the plan is built by block
+    scans through LDS instead of per wave; a long head split into several
+    chunks; bit-identical on a second call."""
+    import wgkv
+    g = torch.Generator().manual_seed(B * 100 + Hkv)
+    D, P = 128, 16
+    Hq = Hkv * 4
+    max_len = 6000 if B * Hkv <= 128 else 600
+    sl = torch.randint(0, max_len + 1, (B, Hkv), generator=g, dtype=torch.int32)
+    sl[0, 0] = max_len  # one head long enough to need several chunks
+    maxb = (max_len + P - 1) // P
+    nb = B * Hkv * maxb + 1
+    bt = torch.randperm(nb, generator=g)[: B * Hkv * maxb].view(B, Hkv, maxb).to(torch.int32)
+    q = torch.randn(B, 1, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(nb, P, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(nb, P, D, generator=g).to(torch.bfloat16)
+    out = run_and_compare(q, k, v, sl, bt, D ** -0.5, f"block planner B{B} Hkv{Hkv}")
+    dev = torch.device("cuda:0")
+    again = wgkv.paged_decode_attn(q.to(dev), k.to(dev), v.to(dev), sl.to(dev), bt.to(dev), D ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+
+
+def test_many_chunks_batch1():
+    """Batch 1 at 128K context (Beta(2,8) admission, ~27K tokens per head):
+    dozens of chunks per head combined by the merge; bit-identical across
+    calls."""
+    import wgkv
+    from wgkv import workloads
+    w = workloads.decode_beta(ctx=131072, device="cuda", seed=11)
+    outs = [wgkv.paged_decode_attn(w.q, w.k_cache, w.v_cache, w.cache_seqlens, w.block_table, w.softmax_scale)
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
+    run_and_compare(w.q, w.k_cache, w.v_cache, w.cache_seqlens, w.block_table, w.softmax_scale, "beta 128k seed 11")

@@ -3,24 +3,29 @@
 // Work split: the logical sequence of every (batch row b, KV head h) is cut
 // into 16-token sub-pages; sub-pages are grouped into chunks of `cp`
 // sub-pages (cp a multiple of 16, chosen on the device so that the whole
-// batch, per-head remainders included, gives at most kRounds * slots chunks,
-// slots = resident workgroups = 3 per CU).  One workgroup (4 waves) owns one
-// chunk, and its waves take 64-token "quads" (4 sub-pages) in turn.  Every
-// K/V byte of the cache is read exactly once, for all G query heads of the
-// KV head together.
+// batch, per-head remainders included, gives about one chunk per resident
+// workgroup slot).  One workgroup (4 waves) owns one chunk, and its waves
+// take 64-token "quads" (4 sub-pages) in turn.  Every K/V byte of the cache
+// is read exactly once, for all G query heads of the KV head together.
 //
 // Per quad and wave:
 //   * K is read in the MFMA B-operand layout (lane n%16 = token row, lane/16
 //     = 16-byte slice of the row) and multiplied with the query heads on
-//     v_mfma_f32_16x16x32_bf16 (query head i replicated in rows 4r+i);
+//     v_mfma_f32_16x16x32_bf16 (query head 4*gi + i of group gi replicated
+//     in rows 4r+i of that group's A operand);
 //   * softmax runs in the log2 domain with one lazily moved running max per
 //     query head, uniform over the wave, and a per-lane running denominator;
-//   * P goes through a 1 KB LDS slot per wave and V is read fully coalesced
-//     (consecutive 16-byte slices of consecutive rows); P V runs on
-//     v_dot2_f32_bf16 over pairs of rows (P rounded to bf16, fp32 sums).
-// At the end of a chunk the 4 waves merge through LDS; a single-chunk head
-// writes its output directly, otherwise the chunk writes (m, l, acc) partials
-// that wgkv_decode_merge combines with the usual log-sum-exp rule.
+//   * P goes through a 1 KB LDS slot per wave and head group, and V is read
+//     fully coalesced (consecutive 16-byte slices of consecutive rows); P V
+//     runs on v_dot2_f32_bf16 over pairs of rows (P rounded to bf16, fp32
+//     sums).
+// At the end of a chunk the 4 waves merge through LDS.  A single-chunk head
+// writes its output directly; otherwise the chunk stores (m, l, acc)
+// partials that decode_merge_kernel combines with the log-sum-exp rule in
+// chunk order.  (Merging in the split kernel, by the last chunk of a head to
+// arrive, measured slower at batch 1: one workgroup then reads all ~80
+// partials of a head in three dependent rounds of loads, where the merge
+// launch spreads them over G*B*Hkv workgroups and one round.)
 #include "wgkv_common.h"
 
 namespace {
@@ -28,12 +33,16 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxBH = 2048;
-constexpr int kWgPerCu = 3;          // resident workgroups per CU at 158 VGPRs
-constexpr int kRounds = 1;           // chunks per resident workgroup slot
-constexpr int kMaxSlots = 1024;      // cap on CUs * kWgPerCu (workspace sizing)
-constexpr int kMaxChunks = kRounds * kMaxSlots + kMaxBH;
+constexpr int kWaveBH = 64;          // B*Hkv up to this: each wave plans alone, in registers
+constexpr int kMaxSlots = 1024;      // cap on CUs * resident workgroups per CU (workspace sizing)
+constexpr int kMaxChunks = kMaxSlots + kMaxBH;
+constexpr int kMaxG = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 units a running maximum may lag the scores
+
+// Resident workgroups per CU: G <= 4 fits three (158 VGPRs at D=128, G=4),
+// G = 8 (two head groups, 83 KB of LDS) one.
+constexpr int wg_per_cu(int G) { return G > 4 ? 1 : 3; }
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -51,9 +60,13 @@ struct DecodeArgs {
   int64_t out_sb, out_sh;
   int B, Hkv;
   float scale_log2;
-  int target_chunks;  // kRounds * slots - B*Hkv: the chunk count then fits kRounds full rounds
-  float* part;  // [kMaxChunks][4] m, then [kMaxChunks][4] l, then [kMaxChunks][4][D] acc
-  int* plan;    // [kMaxBH + 1] first chunk of each (b,h), written by the split kernel
+  int target_chunks;  // resident workgroup slots: the plan aims at one chunk per slot
+  // partials of chunk w, query head i (i < G): m at part_m[w*G+i], l at
+  // part_l[w*G+i], acc at part_acc[(w*G+i)*D ..]
+  float* part_m;
+  float* part_l;
+  float* part_acc;
+  int* plan;  // [B*Hkv + 1] first chunk of each (b,h) and the chunk count, written by the split kernel
 };
 
 __device__ __forceinline__ int clamped_tokens(const DecodeArgs& a, int bh) {
@@ -64,10 +77,57 @@ __device__ __forceinline__ int clamped_tokens(const DecodeArgs& a, int bh) {
   return T;
 }
 
-// Device-side split planner (replaces the host planner of the reference,
-// src/modeling_layers.py:1032-1055).  Leaves s_pref[bh] = first chunk of
-// (b,h) and s_pref[BH] = number of chunks; returns cp.
-__device__ int build_plan(const DecodeArgs& a, int* s_pref, int* s_tmp) {
+// This workgroup's share of the device-side split plan (replaces the host
+// planner of the reference, src/modeling_layers.py:1032-1055).
+struct Plan {
+  int n_chunks;  // chunks of the whole call
+  int bh;        // (b, h) this workgroup serves
+  int first;     // global index of that head's first chunk
+  int n_bh;      // chunks of that head
+  int cp;        // sub-pages per chunk
+};
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// B*Hkv <= 64: lane bh of every wave takes head bh; the plan is two wave
+// scans in registers, no LDS and no barrier.  Workgroup 0 stores the plan
+// (first chunk of each head, then the chunk count) for the merge.
+__device__ Plan plan_wave(const DecodeArgs& a, int w, int* plan_out) {
+  const int BH = a.B * a.Hkv;
+  const int lane = threadIdx.x & 63;
+  const int ns = lane < BH ? (clamped_tokens(a, lane) + 15) >> 4 : 0;
+  const int total = __builtin_amdgcn_readlane(wave_incl_scan(ns, lane), 63);
+  int cp = (total + a.target_chunks - 1) / a.target_chunks;
+  cp = max(16, (cp + 15) & ~15);
+  const int ch = lane < BH ? max(1, (ns + cp - 1) / cp) : 0;
+  const int incl = wave_incl_scan(ch, lane);
+  const int excl = incl - ch;
+  Plan p;
+  p.n_chunks = __builtin_amdgcn_readlane(incl, 63);
+  p.cp = cp;
+  // owner of chunk w: the largest head whose first chunk is <= w
+  const uint64_t own = __builtin_amdgcn_ballot_w64(lane < BH && excl <= w);
+  p.bh = own ? 63 - __builtin_clzll(own) : 0;
+  p.first = __builtin_amdgcn_readlane(excl, p.bh);
+  p.n_bh = __builtin_amdgcn_readlane(ch, p.bh);
+  if (w == 0 && threadIdx.x < 64) {
+    if (lane < BH) plan_out[lane] = excl;
+    if (lane == 0) plan_out[BH] = p.n_chunks;
+  }
+  return p;
+}
+
+// B*Hkv > 64: block scans over the heads through LDS (workgroup 0 stores
+// the plan for the merge).
+__device__ Plan plan_block(const DecodeArgs& a, int w, int* s_pref, int* s_tmp, int* plan_out) {
   const int BH = a.B * a.Hkv;
   const int t = threadIdx.x;
   const int per = (BH + kThreads - 1) / kThreads;
@@ -92,16 +152,20 @@ __device__ int build_plan(const DecodeArgs& a, int* s_pref, int* s_tmp) {
   }
   if (t == 0) s_pref[BH] = n_chunks;
   __syncthreads();
-  return cp;
-}
-
-__device__ __forceinline__ int find_owner(const int* s_pref, int BH, int w) {
-  int lo = 0, hi = BH - 1;  // largest bh with s_pref[bh] <= w
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (s_pref[mid] <= w) lo = mid; else hi = mid - 1;
+  if (w == 0)
+    for (int i = t; i <= BH; i += kThreads) plan_out[i] = s_pref[i];
+  int l = 0, h = BH - 1;  // largest bh with s_pref[bh] <= w
+  while (l < h) {
+    const int mid = (l + h + 1) >> 1;
+    if (s_pref[mid] <= w) l = mid; else h = mid - 1;
   }
-  return lo;
+  Plan p;
+  p.n_chunks = n_chunks;
+  p.cp = cp;
+  p.bh = l;
+  p.first = s_pref[l];
+  p.n_bh = s_pref[l + 1] - s_pref[l];
+  return p;
 }
 
 // First pool row (token slot) of sub-page `sp` of a head; page ids outside
@@ -151,34 +215,31 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 }
 
 template <int D, int G>
-// 158 registers at D=128, G=4: three waves per SIMD (measured faster than two).
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))) void decode_split_kernel(
-    DecodeArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(wg_per_cu(G), wg_per_cu(G))))
+void decode_split_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;       // MFMA k-steps per row
   constexpr int CH = D / 8;        // 16-byte slices per row
   constexpr int RPI = 64 / CH;     // rows per coalesced V load
   constexpr int NV = 64 / RPI;     // V loads per quad
+  constexpr int NG = (G + 3) / 4;  // groups of 4 query heads (MFMA A operands)
+  static_assert(G <= kMaxG, "query heads per KV head");
 
   __shared__ int s_pref[kMaxBH + 1];
   __shared__ int s_tmp[kThreads];
-  __shared__ f32x4_t s_p[kWaves][64];
-  __shared__ float s_acc[kWaves][RPI][G][D];
-  __shared__ float s_ml[kWaves][2][4];
+  __shared__ f32x4_t s_p[kWaves][NG][64];
+  __shared__ __attribute__((aligned(16))) float s_acc[kWaves][RPI][G][D];
+  __shared__ float s_ml[kWaves][2][G];
 
-  const int cp = build_plan(a, s_pref, s_tmp);
-  const int BH = a.B * a.Hkv;
-  if (blockIdx.x == 0)
-    for (int i = threadIdx.x; i <= BH; i += kThreads) a.plan[i] = s_pref[i];
   const int w = blockIdx.x;
-  if (w >= s_pref[BH]) return;
-  const int bh = find_owner(s_pref, BH, w);
-  const int ci = w - s_pref[bh];
-  const int n_chunks_bh = s_pref[bh + 1] - s_pref[bh];
+  const Plan pl = a.B * a.Hkv <= kWaveBH ? plan_wave(a, w, a.plan) : plan_block(a, w, s_pref, s_tmp, a.plan);
+  if (w >= pl.n_chunks) return;
+  const int bh = pl.bh;
+  const int ci = w - pl.first;
   const int b = bh / a.Hkv, h = bh - b * a.Hkv;
   const int T = clamped_tokens(a, bh);
   const int nsub = (T + 15) >> 4;
-  const int s0 = ci * cp;
-  const int s1 = min(nsub, s0 + cp);
+  const int s0 = ci * pl.cp;
+  const int s1 = min(nsub, s0 + pl.cp);
   const int tok_end = min(T, s1 * 16);
 
   // wid is wave-uniform: the quad bookkeeping, page-table reads and row
@@ -187,16 +248,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   const int n = lane & 15, g = lane >> 4;
   const int32_t* bt_row = a.bt + (int64_t)b * a.bt_sb + (int64_t)h * a.bt_sh;
 
-  // Query heads as the MFMA A operand: row m holds head m%4 (zero if >= G).
-  bf16x8_t qa[KS];
-  {
-    const int qh = n & 3;
+  // Query heads as the MFMA A operands: row m of group gi holds head
+  // 4*gi + m%4 (zero if >= G).
+  bf16x8_t qa[NG][KS];
+#pragma unroll
+  for (int gi = 0; gi < NG; ++gi) {
+    const int qh = 4 * gi + (n & 3);
     const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)(h * G + (qh < G ? qh : 0)) * a.q_sh;
 #pragma unroll
     for (int j = 0; j < KS; ++j) {
       u32x4_t v = *(const u32x4_t*)(qrow + (j * 4 + g) * 8);
       if (qh >= G) v = (u32x4_t){0u, 0u, 0u, 0u};
-      qa[j] = __builtin_bit_cast(bf16x8_t, v);
+      qa[gi][j] = __builtin_bit_cast(bf16x8_t, v);
     }
   }
 
@@ -220,25 +283,30 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
     load_k<D>(a, kr, off, n, g);
     load_v<D>(a, vr, off, lane);
 
-    f32x4_t c[4];
+    f32x4_t c[NG][4];
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      c[p] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int gi = 0; gi < NG; ++gi)
 #pragma unroll
-      for (int j = 0; j < KS; ++j)
-        c[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[j], __builtin_bit_cast(bf16x8_t, kr[p][j]), c[p], 0, 0, 0);
-    }
+      for (int p = 0; p < 4; ++p) {
+        c[gi][p] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < KS; ++j)
+          c[gi][p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[gi][j], __builtin_bit_cast(bf16x8_t, kr[p][j]),
+                                                             c[gi][p], 0, 0, 0);
+      }
 
     // Softmax in the log2 domain with a lazy running maximum: m_run of a
     // head moves only when a score of the quad exceeds it by more than
     // kRescaleSlack (then to the quad's maximum, rescaling l and acc), so
     // p <= 2^kRescaleSlack and most quads need neither a maximum nor a
-    // rescale -- one compare and ballot per head.
+    // rescale -- one compare and ballot per head.  Lane (n, g) holds token n
+    // of sub-page g (rows 4g..4g+3 of its MFMA are the group's heads).
     const bool ok = (sp0 + g) * 16 + n < tok_end;
-    float s[G], pr[4];
+    float s[G], pr[NG][4];
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      const float x = g == 0 ? c[0][i] : g == 1 ? c[1][i] : g == 2 ? c[2][i] : c[3][i];
+      const f32x4_t* cg = c[i / 4];
+      const float x = g == 0 ? cg[0][i % 4] : g == 1 ? cg[1][i % 4] : g == 2 ? cg[2][i % 4] : cg[3][i % 4];
       s[i] = ok ? x * a.scale_log2 : -INFINITY;
     }
     uint64_t up_any = 0;
@@ -257,14 +325,18 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) pr[i] = 0.f;
+    for (int gi = 0; gi < NG; ++gi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pr[gi][i] = 0.f;
 #pragma unroll
     for (int i = 0; i < G; ++i) {
       // m_run is -inf only while every score seen is -inf: p = 0 then
-      pr[i] = fast_exp2(s[i] - (m_run[i] == -INFINITY ? 0.f : m_run[i]));
-      l_lane[i] += pr[i];
+      pr[i / 4][i % 4] = fast_exp2(s[i] - (m_run[i] == -INFINITY ? 0.f : m_run[i]));
+      l_lane[i] += pr[i / 4][i % 4];
     }
-    s_p[wid][g * 16 + n] = (f32x4_t){pr[0], pr[1], pr[2], pr[3]};
+#pragma unroll
+    for (int gi = 0; gi < NG; ++gi)
+      s_p[wid][gi][g * 16 + n] = (f32x4_t){pr[gi][0], pr[gi][1], pr[gi][2], pr[gi][3]};
     wave_lds_sync();
 
     // P V on v_dot2_f32_bf16: the lane's rows are paired (load i, load i+1)
@@ -275,14 +347,17 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
 #pragma unroll
     for (int i = 0; i < NV; i += 2) {
       const int r0 = i * RPI + lane / CH, r1 = r0 + RPI;
-      const f32x4_t p0 = s_p[wid][r0];
-      const f32x4_t p1 = s_p[wid][r1];
       u32x4_t v0 = vr[i], v1 = vr[i + 1];
       if (!full && sp0 * 16 + r0 >= tok_end) v0 = (u32x4_t){0u, 0u, 0u, 0u};
       if (!full && sp0 * 16 + r1 >= tok_end) v1 = (u32x4_t){0u, 0u, 0u, 0u};
       uint32_t pp[G];
 #pragma unroll
-      for (int qi = 0; qi < G; ++qi) pp[qi] = pack_bf16x2(p0[qi], p1[qi]);
+      for (int gi = 0; gi < NG; ++gi) {
+        const f32x4_t p0 = s_p[wid][gi][r0];
+        const f32x4_t p1 = s_p[wid][gi][r1];
+#pragma unroll
+        for (int qi = 4 * gi; qi < G && qi < 4 * gi + 4; ++qi) pp[qi] = pack_bf16x2(p0[qi % 4], p1[qi % 4]);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         // (v0.d, v1.d) for d = 2e (low halves) and d = 2e+1 (high halves)
@@ -316,9 +391,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
   }
   __syncthreads();
 
-  float* part_m = a.part;
-  float* part_l = a.part + kMaxChunks * 4;
-  float* part_acc = a.part + kMaxChunks * 8;
+  const bool single = pl.n_bh == 1;
   for (int v = threadIdx.x; v < G * D; v += kThreads) {
     const int i = v / D, d = v - i * D;
     float M = -INFINITY;
@@ -336,27 +409,28 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(3, 3))
       L = fmaf(sc, s_ml[ww][1][i], L);
       A = fmaf(sc, sum, A);
     }
-    if (n_chunks_bh == 1) {
+    if (single) {
       const float o = L > 0.f ? A / L : 0.f;
       a.out[(int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d] = f32_to_bf16(o);
     } else {
       if (d == 0) {
-        part_m[w * 4 + i] = M;
-        part_l[w * 4 + i] = L;
+        a.part_m[w * G + i] = M;
+        a.part_l[w * G + i] = L;
       }
-      part_acc[((int64_t)w * 4 + i) * D + d] = A;
+      a.part_acc[((int64_t)w * G + i) * D + d] = A;
     }
   }
 }
 
-// Log-sum-exp merge of a head's chunk partials in one pass: each thread keeps
-// a running (max, sum, acc) over its share of the chunks (all loads of the
-// pass are independent), then the shares are combined through LDS.  The plan
-// comes from the split kernel, which ran before on the same stream.
+// Log-sum-exp merge of a head's chunk partials in one pass, one workgroup
+// per (b, h, query head i): the float4 quads of head i's row are summed by
+// GROUPS thread groups over disjoint chunk subsets, each thread keeping a
+// running (max, sum, acc) with all loads of a batch issued before the
+// (branch-free) update consumes them; the groups are then combined through
+// LDS in group order.  The plan comes from the split kernel, which ran
+// before on the same stream.
 template <int D, int G>
 __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
-  // one workgroup per (b, h, query head i): the float4 quads of head i's row
-  // are summed by GROUPS thread groups over disjoint chunk subsets
   constexpr int NQ = D / 4;
   constexpr int GROUPS = kThreads / NQ;
   __shared__ f32x4_t s_a[kThreads];
@@ -365,16 +439,11 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   const int c0 = a.plan[bh], c1 = a.plan[bh + 1];
   if (c1 - c0 <= 1) return;  // written directly by the split kernel
   const int b = bh / a.Hkv, h = bh - b * a.Hkv;
-  const float* part_m = a.part;
-  const float* part_l = a.part + kMaxChunks * 4;
-  const float* part_acc = a.part + kMaxChunks * 8;
   const int t = threadIdx.x;
   const int i = blockIdx.y;
-  const int vq = i * NQ + t % NQ, grp = t / NQ;
-
-  // Chunks are read in batches of kBatch with every load issued before the
-  // (branch-free) online update consumes them; 16 covers the ~100 chunks of
-  // a head at batch 1 (8 groups) in one round of loads.
+  const int vq = t % NQ, grp = t / NQ;
+  // 16 chunks per batch and 8 groups (D = 128) read the ~80-100 chunks of
+  // a head at batch 1 in one round of loads
   constexpr int kBatch = 16;
   float M = -INFINITY, L = 0.f;
   f32x4_t A = (f32x4_t){0.f, 0.f, 0.f, 0.f};
@@ -384,9 +453,9 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int c = min(cb + k * GROUPS, c1 - 1);
-      mc[k] = part_m[c * 4 + i];
-      lc[k] = part_l[c * 4 + i];
-      ac[k] = *(const f32x4_t*)(part_acc + (int64_t)c * 4 * D + vq * 4);
+      mc[k] = a.part_m[c * G + i];
+      lc[k] = a.part_l[c * G + i];
+      ac[k] = *(const f32x4_t*)(a.part_acc + ((int64_t)c * G + i) * D + vq * 4);
     }
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
@@ -416,8 +485,7 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
       At += sc * s_a[gg * NQ + t];
     }
     const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
-    const int d = vq * 4 - i * D;
-    uint16_t* o = a.out + (int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d;
+    uint16_t* o = a.out + (int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + vq * 4;
 #pragma unroll
     for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(Lt > 0.f ? At[e] * inv : 0.f);
   }
@@ -438,22 +506,35 @@ int cu_count() {
 template <int D, int G>
 hipError_t launch(DecodeArgs a, hipStream_t st) {
   const int BH = a.B * a.Hkv;
-  const int slots = min(kMaxSlots, cu_count() * kWgPerCu);
-  a.target_chunks = max(slots, kRounds * slots - BH);
+  const int slots = min(kMaxSlots, cu_count() * wg_per_cu(G));
+  a.target_chunks = slots;
+  // the plan makes at most target_chunks + BH chunks (one remainder per head)
   hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(a.target_chunks + BH), dim3(kThreads), 0, st, a);
-  hipError_t e = hipGetLastError();
+  const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH, G), dim3(kThreads), 0, st, a);
   return hipGetLastError();
 }
+
+template <int D>
+hipError_t launch_g(const DecodeArgs& a, int G, hipStream_t st) {
+  switch (G) {
+    case 1: return launch<D, 1>(a, st);
+    case 2: return launch<D, 2>(a, st);
+    case 3: return launch<D, 3>(a, st);
+    case 4: return launch<D, 4>(a, st);
+    default: return launch<D, 8>(a, st);
+  }
+}
+
+size_t part_floats(int head_dim) { return (size_t)kMaxChunks * kMaxG * (2 + (size_t)head_dim); }
 
 }  // namespace
 
 extern "C" size_t wgkv_paged_decode_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t head_dim) {
   (void)batch;
   (void)num_kv_heads;
-  return (size_t)kMaxChunks * 4 * (2 + (size_t)(head_dim > 0 ? head_dim : 0)) * sizeof(float) +
-         (size_t)(kMaxBH + 1) * sizeof(int);
+  return part_floats(head_dim > 0 ? head_dim : 0) * sizeof(float) + (size_t)(kMaxBH + 1) * sizeof(int);
 }
 
 extern "C" int wgkv_paged_decode_attn(
@@ -472,7 +553,7 @@ extern "C" int wgkv_paged_decode_attn(
   if ((int64_t)batch * num_kv_heads > kMaxBH) return WGKV_ERR_UNSUPPORTED;
   const int G = num_q_heads / num_kv_heads;
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
-  if (G != 1 && G != 2 && G != 4) return WGKV_ERR_UNSUPPORTED;
+  if (G != 1 && G != 2 && G != 3 && G != 4 && G != 8) return WGKV_ERR_UNSUPPORTED;
   int shift;
   if (page_size == 16) shift = 0;
   else if (page_size == 32) shift = 1;
@@ -481,7 +562,8 @@ extern "C" int wgkv_paged_decode_attn(
   // 16-byte vector loads: rows and bases must be 16-byte aligned.
   if (((uintptr_t)q | (uintptr_t)k_cache | (uintptr_t)v_cache) & 15) return WGKV_ERR_UNSUPPORTED;
   if ((q_stride_b | q_stride_h) & 7) return WGKV_ERR_UNSUPPORTED;
-  if (!workspace || workspace_bytes < wgkv_paged_decode_workspace_bytes(batch, num_kv_heads, head_dim))
+  if (!workspace || workspace_bytes < wgkv_paged_decode_workspace_bytes(batch, num_kv_heads, head_dim) ||
+      ((uintptr_t)workspace & 15))
     return WGKV_ERR_WORKSPACE;
 
   DecodeArgs a;
@@ -505,15 +587,13 @@ extern "C" int wgkv_paged_decode_attn(
   a.B = batch;
   a.Hkv = num_kv_heads;
   a.scale_log2 = softmax_scale * kLog2e;
-  a.part = (float*)workspace;
-  a.plan = (int*)((char*)workspace + (size_t)kMaxChunks * 4 * (2 + head_dim) * sizeof(float));
+  float* ws = (float*)workspace;
+  a.part_m = ws;
+  a.part_l = ws + (size_t)kMaxChunks * kMaxG;
+  a.part_acc = ws + (size_t)kMaxChunks * kMaxG * 2;
+  a.plan = (int*)(ws + part_floats(head_dim));
 
   hipStream_t st = (hipStream_t)stream;
-  hipError_t e;
-  if (head_dim == 128) {
-    e = G == 4 ? launch<128, 4>(a, st) : G == 2 ? launch<128, 2>(a, st) : launch<128, 1>(a, st);
-  } else {
-    e = G == 4 ? launch<64, 4>(a, st) : G == 2 ? launch<64, 2>(a, st) : launch<64, 1>(a, st);
-  }
+  const hipError_t e = head_dim == 128 ? launch_g<128>(a, G, st) : launch_g<64>(a, G, st);
   return e == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

@@ -14,7 +14,7 @@ import torch
 import torch.nn as nn
 
 from . import _lib
-from .ops import _ptr, _require_cuda
+from .ops import _ptr, _require_cuda, _retired
 
 _INPUT_BITS = {"pre_k": 1, "post_k": 2, "v": 4}
 
@@ -207,6 +207,8 @@ def _decode_workspace(device, B, H, inner):
     need = int(_lib.lib().wgkv_gate_workspace_bytes(B, H, inner))
     ws = _DECODE_WS.get(device)
     if ws is None or ws.numel() < need:
+        if ws is not None:
+            _retired.append(ws)  # a captured graph may still hold its address
         ws = torch.zeros(max(need, 65536), dtype=torch.uint8, device=device)
         _DECODE_WS[device] = ws
     return ws

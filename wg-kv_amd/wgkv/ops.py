@@ -3,22 +3,46 @@
 Each wrapper validates shapes/dtypes on the host, passes raw pointers and
 strides to the C ABI and raises on a non-zero status.  Scratch memory is a
 per-device workspace tensor allocated once and reused; calls on one device
-are ordered by the stream, so sharing it is safe.
+are ordered by the stream, so sharing it is safe.  A workspace that is
+replaced by a larger one is kept alive (not returned to the caching
+allocator), because a captured HIP graph may still hold its address.
 """
 import torch
 
 from . import _lib
 
 _workspaces = {}
+_decode_workspaces = {}
+_retired = []  # replaced workspaces, kept for graphs captured with their addresses
+
+
+def _dev_key(device):
+    dev = torch.device(device)
+    return dev, (dev.index if dev.index is not None else torch.cuda.current_device())
 
 
 def workspace(device, nbytes):
-    dev = torch.device(device)
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    """Uninitialised per-device scratch of at least ``nbytes`` bytes."""
+    dev, key = _dev_key(device)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _retired.append(ws)
         ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
         _workspaces[key] = ws
+    return ws
+
+
+def decode_workspace(device):
+    """The decode attention's per-device workspace (split partials and the
+    split plan), sized for the largest head_dim so that it never grows and a
+    captured graph's address stays valid."""
+    dev, key = _dev_key(device)
+    ws = _decode_workspaces.get(key)
+    if ws is None:
+        nbytes = int(_lib.lib().wgkv_paged_decode_workspace_bytes(1, 1, 128))
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _decode_workspaces[key] = ws
     return ws
 
 
@@ -71,8 +95,7 @@ def paged_decode_attn(q, k_cache, v_cache, cache_seqlens, block_table, softmax_s
         out = torch.empty(B, 1, Hq, D, dtype=torch.bfloat16, device=q.device)
     o3 = out[:, 0]
     L = _lib.lib()
-    nbytes = L.wgkv_paged_decode_workspace_bytes(B, Hkv, D)
-    ws = workspace(q.device, nbytes)
+    ws = decode_workspace(q.device)
     st = L.wgkv_paged_decode_attn(
         _ptr(q3), q3.stride(0), q3.stride(1),
         _ptr(k_cache), _ptr(v_cache), k_cache.shape[0], k_cache.shape[1],
