@@ -52,7 +52,7 @@ const char* wgkv_status_string(int status);
  * sequence (page i of the head = block_table[b,h,i]) are attended by the
  * Hq/Hkv query heads h_kv*G .. h_kv*G+G-1 with softmax(q.k * scale) v.  A head
  * with zero tokens yields zeros.  Supported: D in {64,128}, page_size in
- * {16,32,64}, G = Hq/Hkv in {1,2,4}, B*Hkv <= 2048.  Split planning happens
+ * {16,32,64}, G = Hq/Hkv in {1,2,3,4,8}, B*Hkv <= 2048.  Split planning happens
  * on the device; out-of-range lengths are clamped to max_pages*page_size and
  * out-of-range page ids to the pool, so no access leaves the buffers.
  * ---------------------------------------------------------------------- */
@@ -68,6 +68,27 @@ int wgkv_paged_decode_attn(
     float softmax_scale,
     void* workspace, size_t workspace_bytes,
     void* stream);
+
+/* Allocation-free form of wgkv_paged_decode_attn.  It has no counterpart in
+ * the reference: it is for callers that cannot allocate device memory or
+ * pass a workspace (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments and results as
+ * wgkv_paged_decode_attn minus the workspace; the split partials and plan
+ * live in a static device array of the library (12.2 MiB per device, held
+ * until the process ends) that covers every supported call (head_dim <= 128,
+ * G <= 8, batch*num_kv_heads <= 2048; larger sizes return
+ * WGKV_ERR_UNSUPPORTED).  The array's device address is looked up on the
+ * first call on each device.  No entry state needs clearing between calls,
+ * but all calls on one device share the array: calls that overlap on one GPU
+ * (different streams, no ordering between them) race and must not be made. */
+int wgkv_paged_decode_attn_noalloc(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h,
+    const void* k_cache, const void* v_cache, int64_t num_pages, int32_t page_size,
+    const int32_t* cache_seqlens, int64_t sl_stride_b,
+    const int32_t* block_table, int64_t bt_stride_b, int64_t bt_stride_h, int32_t max_pages,
+    void* out, int64_t out_stride_b, int64_t out_stride_h,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, void* stream);
 
 /* ------------------------------------------------------------------------
  * Vertical-slash metadata of the sparse prefill, built on the device.

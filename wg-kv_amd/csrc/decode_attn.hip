@@ -26,6 +26,8 @@
 // arrive, measured slower at batch 1: one workgroup then reads all ~80
 // partials of a head in three dependent rounds of loads, where the merge
 // launch spreads them over G*B*Hkv workgroups and one round.)
+#include <mutex>
+
 #include "wgkv_common.h"
 
 namespace {
@@ -529,6 +531,45 @@ hipError_t launch_g(const DecodeArgs& a, int G, hipStream_t st) {
 
 size_t part_floats(int head_dim) { return (size_t)kMaxChunks * kMaxG * (2 + (size_t)head_dim); }
 
+// ---- scratch of the allocation-free entry point ------------------------------
+// The partials and the plan of the largest supported call (head_dim 128, G 8,
+// B*Hkv 2048): 12.2 MiB per device, held until the process ends.  In host
+// code `scratch` names a host-side stand-in; its device address is looked up
+// once per device with hipGetSymbolAddress and only that address is used.
+constexpr size_t kScratchBytes =
+    ((size_t)kMaxChunks * kMaxG * (2 + 128) * sizeof(float) + (size_t)(kMaxBH + 1) * sizeof(int) + 255) & ~(size_t)255;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on the device that owns `stream` (the current
+// device for the null stream), resolved on the first call for that device
+// with the device made current for the lookup.
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (stream) {
+    if (hipStreamGetDevice(stream, &dev) != hipSuccess) return WGKV_ERR_HIP;
+  } else if (hipGetDevice(&dev) != hipSuccess) {
+    return WGKV_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) return WGKV_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return WGKV_ERR_HIP;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return WGKV_ERR_HIP;
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return WGKV_ERR_HIP;
+    if (e != hipSuccess || !p) return WGKV_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return WGKV_OK;
+}
+
 }  // namespace
 
 extern "C" size_t wgkv_paged_decode_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t head_dim) {
@@ -596,4 +637,24 @@ extern "C" int wgkv_paged_decode_attn(
   hipStream_t st = (hipStream_t)stream;
   const hipError_t e = head_dim == 128 ? launch_g<128>(a, G, st) : launch_g<64>(a, G, st);
   return e == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+extern "C" int wgkv_paged_decode_attn_noalloc(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h,
+    const void* k_cache, const void* v_cache, int64_t num_pages, int32_t page_size,
+    const int32_t* cache_seqlens, int64_t sl_stride_b,
+    const int32_t* block_table, int64_t bt_stride_b, int64_t bt_stride_h, int32_t max_pages,
+    void* out, int64_t out_stride_b, int64_t out_stride_h,
+    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, void* stream) {
+  if (batch <= 0 || num_kv_heads <= 0 || head_dim <= 0) return WGKV_ERR_ARG;
+  if ((int64_t)batch * num_kv_heads > kMaxBH || head_dim > 128) return WGKV_ERR_UNSUPPORTED;
+  if (wgkv_paged_decode_workspace_bytes(batch, num_kv_heads, head_dim) > kScratchBytes) return WGKV_ERR_WORKSPACE;
+  void* ws = nullptr;
+  const int st = scratch_for_stream((hipStream_t)stream, &ws);
+  if (st != WGKV_OK) return st;
+  return wgkv_paged_decode_attn(q, q_stride_b, q_stride_h, k_cache, v_cache, num_pages, page_size, cache_seqlens,
+                                sl_stride_b, block_table, bt_stride_b, bt_stride_h, max_pages, out, out_stride_b,
+                                out_stride_h, batch, num_q_heads, num_kv_heads, head_dim, softmax_scale, ws,
+                                kScratchBytes, stream);
 }

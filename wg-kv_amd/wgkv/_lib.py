@@ -42,6 +42,15 @@ SIGNATURES = {
         c_f32,
         c_ptr, c_size,
         c_ptr]),
+    "wgkv_paged_decode_attn_noalloc": (ctypes.c_int, [
+        c_ptr, c_i64, c_i64,
+        c_ptr, c_ptr, c_i64, c_i32,
+        c_ptr, c_i64,
+        c_ptr, c_i64, c_i64, c_i32,
+        c_ptr, c_i64, c_i64,
+        c_i32, c_i32, c_i32, c_i32,
+        c_f32,
+        c_ptr]),
     "wgkv_build_prefill_meta": (ctypes.c_int, [
         c_ptr, c_i64, c_i64,
         c_i32, c_i32, c_i32, c_i32, c_i32,
