@@ -183,12 +183,15 @@ int wgkv_decode_append(
     void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream);
 
-/* wgkv_decode_append with the ring state (local_ptr, local_length) in device
- * memory (int32[2]) instead of host arguments, for decode steps replayed from
- * a captured HIP graph: promotion runs only if the device local_length equals
- * W (the host condition of :1470), and with advance != 0 (the last layer's
- * call) the kernel advances the ring state as decode_wrapper's host update
- * does (:1409-1413).  Same arguments otherwise. */
+/* wgkv_decode_append with the ring state in device memory, int32[3] =
+ * (local_ptr, local_length, slot of the last ring write), instead of host
+ * arguments, for decode steps replayed from a captured HIP graph: promotion
+ * runs only if the device local_length equals W (the host condition of
+ * :1470); a ring write stores its slot in ring_state[2] (deferred gating
+ * re-gates the window when that slot is W-1, :1402-1405); with advance != 0
+ * (the last layer's call) the kernel advances the ring state as
+ * decode_wrapper's host update does (:1409-1413).  Same arguments
+ * otherwise. */
 int wgkv_decode_append_ring(
     const void* key, const void* value, int64_t kv_stride_h,
     const void* pre_key, int64_t pk_stride_h,
@@ -224,6 +227,10 @@ int wgkv_decode_append_ring(
  * product split into three bf16 planes that carry all its bits, so the
  * result equals the fp32 layer up to rounding order.  Otherwise ignored
  * (w1 and the norm weights are always read by the other paths).
+ * active_flag (may be NULL): a device int32; when given, the launch does
+ * nothing unless *active_flag == active_value -- the condition is read on the
+ * device, so a captured decode step can re-gate its window only on the step
+ * that fills the ring's last slot (deferred gating, :1402-1405).
  * workspace (may be NULL): for seq_len <= 4 (decode steps) the hidden
  * columns of each head are split over several workgroups whose partial
  * logits meet in the workspace; it must hold wgkv_gate_workspace_bytes()
@@ -244,6 +251,7 @@ int wgkv_gate_scores(
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
     const void* w1_packed,
+    const int32_t* active_flag, int32_t active_value,
     void* workspace, int64_t workspace_bytes,
     void* stream);
 

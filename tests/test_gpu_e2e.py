@@ -124,9 +124,61 @@ def test_graph_decode_matches_eager(gated, qwen3):
         _ = torch.randn(1000, device=DEV).sum().item()  # eager work between replays
         assert int(t.item()) == eager_toks[i], i
         assert torch.equal(gd.logits.float(), eager_logits[i]), (i, (gd.logits.float() - eager_logits[i]).abs().max())
-        assert cb.ring_state.tolist() == [cb.local_ptr, cb.local_length]
+        assert cb.ring_state[:2].tolist() == [cb.local_ptr, cb.local_length]
     assert torch.equal(ca.global_lengths, cb.global_lengths)
     assert ca.local_ptr == cb.local_ptr and ca.local_length == cb.local_length
+
+
+@pytest.mark.parametrize("defer", [True, False])
+def test_graph_decode_deferred_gating(defer):
+    """Deferred gating (the reference profiling harness's mode): 150 captured
+    decode steps with a 64-token window re-gate each layer's window twice (on
+    the steps that write slot 63, decided on the device) and equal the eager
+    path -- which tests the slot on the host -- bit for bit: logits, tokens,
+    flags, block tables and lengths.  With immediate gating the same run
+    gates every token."""
+    from wgkv import e2e
+    from wgkv.cache import DualCache
+    print(f"[e2e] graph decode, g_defer={defer}, 150 steps, W=64", flush=True)
+    W, S, chunk, n = 64, 640, 256, 150
+    m = tiny_model(True, S=S, steps=n, W=W, g_defer=defer)
+    ids = torch.randint(0, 1000, (1, S), generator=torch.Generator().manual_seed(5)).to(DEV)
+    e2e.calibrate_gates(m, ids, 0.3, chunk=256)
+
+    def prefill():
+        c = DualCache()
+        logits = None
+        for c0 in range(0, S, chunk):
+            logits = m.forward_tokens(ids[:, c0:c0 + chunk], c0, c)
+        return c, e2e.greedy_token(logits)
+
+    ca, tok = prefill()
+    assert (ca.local_pre_key is not None) == defer
+    flags0 = ca.local_is_global.clone()
+    eager_logits, eager_toks, refreshed = [], [], 0
+    for i in range(n):
+        before = ca.local_is_global.clone()
+        lg = m.forward_tokens(tok, S + i, ca)
+        tok = e2e.greedy_token(lg)
+        eager_logits.append(lg.float().clone())
+        eager_toks.append(int(tok.item()))
+        if defer and not torch.equal(before, ca.local_is_global):
+            refreshed += 1
+            assert ca.local_ptr == 0, "flags may only change when slot W-1 was written"
+    if defer:
+        assert refreshed == 2 and not torch.equal(flags0, ca.local_is_global)
+    cb, tok_b = prefill()
+    gd = e2e.GraphDecoder(m, cb, tok_b, S, warmup=2)
+    for i in range(2, n):
+        t = gd.step()
+        if i % 16 == 0:
+            _ = torch.randn(1000, device=DEV).sum().item()  # eager work between replays
+        assert int(t.item()) == eager_toks[i], i
+        assert torch.equal(gd.logits.float(), eager_logits[i]), (i, (gd.logits.float() - eager_logits[i]).abs().max())
+    torch.cuda.synchronize()
+    assert torch.equal(ca.local_is_global, cb.local_is_global)
+    assert torch.equal(ca.global_lengths, cb.global_lengths) and torch.equal(ca.block_table, cb.block_table)
+    assert cb.ring_state[:2].tolist() == [cb.local_ptr, cb.local_length]
 
 
 @pytest.mark.parametrize("granularity", ["rms_linear_attn", "kernel", "predictor"])
@@ -134,11 +186,13 @@ def test_timed_run_matches_untimed(granularity):
     """With the per-granularity timers installed (profiling.py
     --profile_attn_mlp), an eager run decodes the same tokens as without
     them, and attention, MLP and LM head each accumulate time in both the
-    prefill and the decode phase (nothing in warm-up)."""
+    prefill and the decode phase (nothing in warm-up).  The predictor case
+    gates every decode token (with deferred gating a 4-step decode calls no
+    predictor, as in the reference)."""
     from wgkv import e2e
     print(f"[e2e] timed run {granularity}", flush=True)
     ids = torch.randint(0, 1000, (1, 640), generator=torch.Generator().manual_seed(4)).to(DEV)
-    m = tiny_model(True)
+    m = tiny_model(True, g_defer=granularity != "predictor")
     e2e.calibrate_gates(m, ids, 0.3, chunk=256)
     plain = e2e.run(m, ids, steps=4, chunk=256, warmup_steps=1)
     t = e2e.install_timing(m, granularity)

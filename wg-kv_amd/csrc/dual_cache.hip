@@ -197,7 +197,7 @@ struct AppendArgs {
   int layer, L, H, D, W, page, max_tokens_per_head;
   int64_t total_pages;
   int local_ptr, local_length, do_migrate, do_write;
-  int32_t* ring;  // device (local_ptr, local_length), replacing the two above when set
+  int32_t* ring;  // device (local_ptr, local_length, last slot written), replacing the two above when set
   uint16_t* qmin;  // QUEST page key bounds (total_pages, D) or NULL
   uint16_t* qmax;
   int32_t* free_ids;    // SnapKV free page list (ids in release order) or NULL
@@ -346,6 +346,10 @@ __global__ __launch_bounds__(kThreads) void decode_append_kernel(AppendArgs a) {
     if (a.mask) a.local_is_global[row] = a.mask[h] ? 1 : 0;
     if (a.cache_seqlens) a.cache_seqlens[h] = cur + a.global_lengths[a.layer * a.H + h];
   }
+  // the slot this step wrote, for decisions later in the step (the deferred
+  // gate's window refresh when it is W-1, :1402-1405); ring[0..1] are not
+  // touched here, so no thread's read of them races with this store
+  if (a.ring && t == 0) a.ring[2] = slot;
   if (a.ring && a.advance) {
     // every thread has read the pointers above; advance them for the next step
     // (decode_wrapper's host update after the last layer, :1409-1413)

@@ -41,7 +41,15 @@ struct GateArgs {
   int nsplit;
   float* part;
   int32_t* counter;
+  // when set, the launch does nothing unless *active == active_value (a
+  // condition decided on the device, e.g. by a captured decode step)
+  const int32_t* active;
+  int active_value;
 };
+
+__device__ __forceinline__ bool inactive(const GateArgs& a) {
+  return a.active != nullptr && *a.active != a.active_value;
+}
 
 __device__ __forceinline__ float load_in(const GateArgs& a, int i, int b, int h, int s, int d) {
   const int64_t off = (int64_t)b * a.sb[i] + (int64_t)h * a.sh[i] + (int64_t)s * a.ss[i] + d;
@@ -88,6 +96,7 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
   constexpr int LDX = K + 4;  // padded row (floats)
   __shared__ float xs[kTok * LDX];
   __shared__ float s_part[4][kTok];
+  if (inactive(a)) return;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   // XCD-aware order: workgroups are dealt to the 8 XCDs round-robin by linear
   // id, so taking (batch, head) = id mod B*H keeps each head's workgroups on
@@ -247,6 +256,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   constexpr int CPL = (KC + 63) / 64;       // chunks per lane
   __shared__ __attribute__((aligned(16))) float xs[kSmallTok][K];
   __shared__ float s_part[kSmallWaves][kSmallTok];
+  if (inactive(a)) return;  // before any arrival is counted
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int split = blockIdx.x, bh = blockIdx.y;
   const int b = bh / a.H, h = bh - b * a.H;
@@ -464,6 +474,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int NLD = 16 / RPL;  // wave loads per input for the wave's 16 tokens
   __shared__ __attribute__((aligned(16))) uint16_t ys[kTok * LDY];
   __shared__ float s_part[4][kTok];
+  if (inactive(a)) return;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int nbh = a.B * a.H;
   const int lid = blockIdx.x + blockIdx.y * gridDim.x;  // XCD-aware order, as gate_kernel
@@ -612,6 +623,7 @@ extern "C" int wgkv_gate_scores(
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
     const void* w1_packed,
+    const int32_t* active_flag, int32_t active_value,
     void* workspace, int64_t workspace_bytes,
     void* stream) {
   if (batch <= 0 || num_kv_heads <= 0 || seq_len <= 0) return WGKV_ERR_ARG;
@@ -656,6 +668,8 @@ extern "C" int wgkv_gate_scores(
   a.mask = mask;
   a.mk_sb = mk_sb;
   a.mk_sh = mk_sh;
+  a.active = active_flag;
+  a.active_value = active_value;
   a.nsplit = 1;
   if (workspace && seq_len <= kSmallTok) {
     const int nsplit = (inner + kSplitCols - 1) / kSplitCols;

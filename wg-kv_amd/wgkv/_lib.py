@@ -104,6 +104,7 @@ SIGNATURES = {
         c_ptr, c_i64, c_i64,
         c_ptr, c_i64, c_i64,
         c_ptr,
+        c_ptr, c_i32,
         c_ptr, c_i64,
         c_ptr]),
     "wgkv_gate_workspace_bytes": (ctypes.c_int64, [c_i32, c_i32, c_i32]),

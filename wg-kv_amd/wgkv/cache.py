@@ -79,8 +79,9 @@ class DualCache:
         self.local_length = 0
         self.prefill_length = 0  # prompt tokens in the cache (all layers); chunks continue from here
         self.decode_started = False
-        # (local_ptr, local_length) on the device for graph-captured decode steps
-        self.ring_state = torch.zeros(2, **i32)
+        # (local_ptr, local_length, slot of the last ring write) on the device
+        # for graph-captured decode steps
+        self.ring_state = torch.zeros(3, **i32)
         self.device_ring = False
         self.next_free_block_dev = torch.full((1,), n_local, **i32)
         self.status = torch.zeros(1, **i32)
@@ -94,7 +95,7 @@ class DualCache:
         Python decode path; a caller replaying a captured step advances them
         with ``advance_host_ring``."""
         if on:
-            self.ring_state.copy_(torch.tensor([self.local_ptr, self.local_length], dtype=torch.int32))
+            self.ring_state.copy_(torch.tensor([self.local_ptr, self.local_length, -1], dtype=torch.int32))
         self.device_ring = on
 
     def advance_host_ring(self):

@@ -132,6 +132,10 @@ class E2EConfig:
     g_threshold: float = 0.1
     qk_norm: bool = False
     g_expand: float = 4.0
+    # deferred gating, as the reference's profiling harness forces
+    # (scripts/profiling.py:212-213): decode steps store the pre-RoPE key and
+    # re-gate the whole window when its last slot is written
+    g_defer: bool = True
 
     @staticmethod
     def qwen3_8b(**kw):
@@ -151,7 +155,8 @@ class LlamaLite(nn.Module):
         self.cfg = WGKVConfig(hidden_size=ec.hidden_size, num_hidden_layers=ec.num_hidden_layers,
                               num_attention_heads=ec.num_attention_heads, num_key_value_heads=ec.num_key_value_heads,
                               rope_theta=ec.rope_theta, local_window_size=ec.local_window_size,
-                              g_threshold=ec.g_threshold, g_expand=ec.g_expand, use_baseline=not gated,
+                              g_threshold=ec.g_threshold, g_expand=ec.g_expand, g_defer=ec.g_defer,
+                              use_baseline=not gated,
                               max_tokens_per_head=max_tokens_per_head, max_total_tokens=max_total_tokens,
                               check_capacity=False)
         self.embed_tokens = nn.Embedding(ec.vocab_size, ec.hidden_size)
@@ -210,8 +215,9 @@ class GraphDecoder:
     and the argmax) captured in a HIP graph and replayed.  The cache runs on
     its device ring pointers; the token and the position live in device
     tensors the step itself advances.  The ring must already be full (any
-    prompt of at least W tokens) and gating immediate (deferred gating
-    re-gates on a host condition)."""
+    prompt of at least W tokens).  With deferred gating every layer's window
+    re-gate is in the graph and runs only on the step that writes the ring's
+    last slot (decided on the device from the ring state)."""
 
     def __init__(self, model, cache, token, pos, warmup=2):
         dev = token.device

@@ -93,8 +93,11 @@ class GatingPredictor(nn.Module):
         self.__dict__["_packed_cache"] = (key, packed)
         return packed
 
-    def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True):
-        """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S))."""
+    def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True,
+                        active=None):
+        """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S)).
+        ``active`` = (device int32 tensor, value): the kernel runs only if
+        the tensor's first element equals value (decided on the device)."""
         B, H, S, D = post_key.shape
         if H != self.num_kv_heads or D != self.head_dim:
             raise AssertionError("gate input shape does not match the predictor")
@@ -109,7 +112,8 @@ class GatingPredictor(nn.Module):
             w1, self._f32(self.conv1.bias), self._f32(self.conv2.weight),
             self._f32(self.conv2.bias), self.inner_dim, self.act, self.g_rms,
             0.0 if self.g_fast_path else float(self.g_epsilon), threshold,
-            like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores, w1_packed=packed)
+            like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores, w1_packed=packed,
+            active=active)
 
     def forward(self, pre_key, post_key, value):
         """Scores (B, H, S) float32, as the reference's forward returns."""
@@ -142,15 +146,17 @@ def pack_weights(w_pre, w_post, w_v, w1, g_inputs, rms, num_kv_heads, head_dim, 
 
 def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
                          clamp_min, threshold, like=None, scores_out=None, mask_out=None, want_scores=True,
-                         w1_packed=None):
+                         w1_packed=None, active=None):
     """The gate kernel on explicit fp32 parameters (GatingPredictor.forward,
     src/modeling_layers.py:170-205, with the admission of :1465): inputs
     (B, H, S, D) bf16 or fp32 (None for inputs not used), RMS-norm weights (D)
     or None, conv1 weight (H*inner, n_in*D, 1) / bias, conv2 weight
     (H, inner, 1) / bias, act 0 = GELU (erf) / 1 = SiLU, clamp_min > 0 for the
     conv path's clamp; w1_packed (optional) = pack_weights() of the same
-    weights, used for bf16 inputs of more than four tokens.  Returns (scores
-    f32 (B,H,S) or None, mask bool (B,H,S))."""
+    weights, used for bf16 inputs of more than four tokens; active (optional)
+    = (int32 device tensor, value): the launch computes and writes nothing
+    unless the tensor's first element equals value.  Returns (scores f32
+    (B,H,S) or None, mask bool (B,H,S))."""
     ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
     ref = like if like is not None else next(t for t in (post_key, pre_key, value) if t is not None)
     B, H, S, D = ref.shape
@@ -180,6 +186,8 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         scores = scores_out if scores_out is not None else torch.empty(B, H, S, dtype=torch.float32, device=dev)
     mask = mask_out if mask_out is not None else torch.empty(B, H, S, dtype=torch.bool, device=dev)
     mk = mask.view(torch.uint8)
+    if active is not None and (active[0].dtype != torch.int32 or not active[0].is_cuda):
+        raise TypeError("active must be a device int32 tensor")
     ws = _decode_workspace(dev, B, H, int(inner)) if S <= 4 else None
     st = _lib.lib().wgkv_gate_scores(
         *args,
@@ -191,6 +199,7 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
         _ptr(mk), mk.stride(0), mk.stride(1),
         _ptr(w1_packed),
+        _ptr(active[0]) if active is not None else None, int(active[1]) if active is not None else 0,
         _ptr(ws), 0 if ws is None else ws.numel(),
         _lib.stream_handle(dev))
     _lib.check(st, "wgkv_gate_scores")

@@ -153,13 +153,19 @@ def snapkv_evict(self, past_key_value, device, local_blocks_per_head):
     c.free_count_dev.fill_(free_n)
 
 
-def refresh_local_is_global(self, past_key_value, device):
+def refresh_local_is_global(self, past_key_value, device, on_device=False):
     """src/modeling_layers.py:1169-1180: re-gate the whole local window of this
-    layer (deferred gating) and store the flags."""
+    layer (deferred gating) and store the flags.  With ``on_device`` the
+    caller has not tested the condition (slot W-1 just written, :1404): the
+    gate launch reads the slot from the cache's device ring state and does
+    nothing on other steps, so a captured decode step can include it."""
     c = past_key_value
     layer = self.layer_idx
     H, W, D = c.num_kv_heads, c.local_window_size, c.head_dim
     if self.config.random_sparsity is not None:
+        if on_device:
+            raise NotImplementedError("deferred gating with random_sparsity draws on the host; "
+                                      "it cannot run with device_ring")
         g = get_random_g_scores(self, 1, W, device)
         c.local_is_global[layer] = g[0] > self.config.g_threshold
         return
@@ -168,7 +174,8 @@ def refresh_local_is_global(self, past_key_value, device):
         k = c.block_pool_k[start:start + H * W].view(1, H, W, D)
         v = c.block_pool_v[start:start + H * W].view(1, H, W, D)
         self.g_predictors.scores_and_mask(c.local_pre_key[layer].unsqueeze(0), k, v, self.config.g_threshold,
-                                          mask_out=c.local_is_global[layer].unsqueeze(0))
+                                          mask_out=c.local_is_global[layer].unsqueeze(0), want_scores=False,
+                                          active=(c.ring_state[2:], W - 1) if on_device else None)
 
 
 def migrate_local_kv_to_global(self, past_key_value, device, local_blocks_per_head):
@@ -244,10 +251,11 @@ def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, valu
                       g_mask=None if g_mask is None else g_mask[0, :, 0],
                       pre_key=pre_key[0, :, 0] if g_mask is None else None,
                       migrate=False, write=True, cache_seqlens=seqlens[0], advance=last)
-    if g_mask is None and insert_pos == W - 1:
+    if g_mask is None:
         if c.device_ring:
-            raise AssertionError("deferred gating re-gates on a host condition; it cannot run with device_ring")
-        refresh_local_is_global(self, c, device)
+            refresh_local_is_global(self, c, device, on_device=True)  # runs only if slot W-1 was written
+        elif insert_pos == W - 1:
+            refresh_local_is_global(self, c, device)
     if self.config.use_quest:  # :1419-1427
         if c.device_ring:
             raise AssertionError("QUEST selection takes the host ring length; it cannot run with device_ring")
