@@ -66,6 +66,31 @@ def gate_scores(pre_key, post_key, value, params, g_inputs=("pre_k", "post_k"),
     return g
 
 
+def bf16_midpoint_distance(y):
+    """Distance of each float64 value from the nearest bf16 rounding boundary
+    (the midpoint of two adjacent bf16 values), in float32 ulps of the
+    value's binade.  With frexp, y = m * 2**e, 0.5 <= |m| < 1: bf16 values
+    are the integers of |m| * 256 (8 significant bits) and one float32 ulp
+    (24 bits) is 2**-16 of their spacing.  Zero is a bf16 value (distance
+    2**15)."""
+    m, _ = torch.frexp(y.to(torch.float64))
+    t = m.abs() * 256.0
+    return (t - torch.floor(t) - 0.5).abs() * 65536.0
+
+
+def bf16_cast_ambiguous(x, ulps=4.0):
+    """Per row of x (..., D): True if an element of the normalised row
+    x * rsqrt(mean(x^2) + 1e-6), computed in float64, lies within ``ulps``
+    float32 ulps of a bf16 rounding boundary.  Only there can a float32
+    evaluation in another summation order (or with another rsqrt) round the
+    element to the other bf16 neighbour when the reference casts it back to
+    bf16 (src/modeling_layers.py:128); every other row's bf16 values are
+    fixed by the mathematics."""
+    xd = x.to(torch.float64)
+    y = xd * torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + RMS_EPS)
+    return (bf16_midpoint_distance(y) < ulps).any(-1)
+
+
 def gate_logits(pre_key, post_key, value, params, **kw):
     """Pre-sigmoid logits (used to place the threshold at a quantile)."""
     g = gate_scores(pre_key, post_key, value, params, **kw).double()

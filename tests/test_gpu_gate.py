@@ -2,7 +2,9 @@
 
 Scores agree to float32 rounding (summation order differs); admission flags
 are bit-exact except tokens whose oracle score lies within 1e-6 of the
-threshold, which are counted and reported separately."""
+threshold and, with bf16 inputs, tokens whose normalised inputs sit within a
+few float32 ulps of a bf16 rounding boundary -- two sets counted and
+reported separately."""
 import os
 
 import numpy as np
@@ -24,30 +26,41 @@ def product_gate(params, H, D, g_expand, fast=True):
     return g.cuda()
 
 
-def compare(scores, mask, ref, thr, label, bf16_inputs=False):
-    """fp32 inputs: |dg| <= 2e-6 everywhere and admission exact except tokens
-    within 1e-6 of the threshold.  bf16 inputs: the reference casts each
-    normalised input back to bf16 (src/modeling_layers.py:128), so a 1-ulp
-    difference of the fp32 mean of squares (summation order) can move one
-    element by one bf16 ulp; such tokens (|dg| > 2e-6) must stay below 1 %,
-    and admission is exact except tokens within max(1e-6, max|dg|) of the
-    threshold, which are reported."""
+def compare(scores, mask, ref, thr, label, ambiguous=None):
+    """|dg| <= 2e-6 and admission exact for every token except (a) tokens
+    whose oracle score lies within 1e-6 of the threshold and (b) with bf16
+    inputs, ``ambiguous`` tokens: an element of a normalised input lies
+    within 4 float32 ulps of a bf16 rounding boundary, so the reference's
+    cast back to bf16 (src/modeling_layers.py:128) may round it either way
+    under another float32 summation order (oracle.gate.bf16_cast_ambiguous).
+    Both sets are counted and reported separately; an ambiguous token may
+    move by at most one bf16 step of one input element (|dg| <= 1e-3)."""
     s = scores.cpu().double().numpy()
     r = ref.double().numpy()
     d = np.abs(s - r)
-    diff = d.max()
-    off = (d > 2e-6).mean()
-    band = max(NEAR, diff) if bf16_inputs else NEAR
-    near = np.abs(r - thr) < band
-    flips = int(((mask.cpu().numpy()) != (r > thr)).sum())
-    far_equal = np.array_equal(mask.cpu().numpy()[~near], (r > thr)[~near])
-    print(f"[gate parity] {label}: max|dg|={diff:.2e}, tokens |dg|>2e-6: {off:.4%}, "
-          f"near-threshold (|g-tau|<{band:.1e}) tokens={int(near.sum())}, admission flips={flips}", flush=True)
-    if bf16_inputs:
-        assert off <= 0.01 and diff <= 1e-3
-    else:
-        assert diff <= 2e-6
-    assert far_equal
+    amb = np.zeros(r.shape, dtype=bool) if ambiguous is None else ambiguous.cpu().numpy().reshape(r.shape)
+    near = np.abs(r - thr) < NEAR
+    got, want = mask.cpu().numpy(), r > thr
+    flips = got != want
+    clean = ~amb
+    dmax_clean = d[clean].max() if clean.any() else 0.0
+    dmax_amb = d[amb].max() if amb.any() else 0.0
+    print(f"[gate parity] {label}: max|dg| {dmax_clean:.2e} (ambiguous tokens {dmax_amb:.2e}); "
+          f"near-threshold (|g-tau|<1e-6) {int(near.sum())}; bf16-ambiguous {int(amb.sum())}; "
+          f"flips among near {int((flips & near).sum())}, ambiguous {int((flips & amb & ~near).sum())}, "
+          f"other {int((flips & ~near & ~amb).sum())}", flush=True)
+    assert dmax_clean <= 2e-6
+    assert dmax_amb <= 1e-3
+    assert not (flips & ~near & ~amb).any()
+
+
+def bf16_ambiguous(*inputs):
+    """Tokens (B, H, S) with a bf16-rounding-ambiguous normalised input row."""
+    amb = None
+    for x in inputs:
+        a = ogate.bf16_cast_ambiguous(x)
+        amb = a if amb is None else amb | a
+    return amb
 
 
 @pytest.mark.parametrize("name", list(scenarios.GATE_SCENARIOS))
@@ -80,7 +93,8 @@ def test_gate_matches_oracle(D, g_expand, S, H, dtype):
     pk = pre_k.transpose(1, 2).contiguous().cuda().transpose(1, 2)
     kk = post_k.transpose(1, 2).contiguous().cuda().transpose(1, 2)
     scores, mask = g.scores_and_mask(pk, kk, None, thr)
-    compare(scores, mask, ref, thr, f"D{D} x{g_expand} S{S} {dtype}", bf16_inputs=dtype == torch.bfloat16)
+    amb = bf16_ambiguous(pre_k, post_k) if dtype == torch.bfloat16 else None
+    compare(scores, mask, ref, thr, f"D{D} x{g_expand} S{S} {dtype}", ambiguous=amb)
 
 
 def test_gate_forward_returns_scores_and_bf16_params():

@@ -14,7 +14,7 @@ import torch
 
 import scenarios
 from oracle import gate as ogate
-from test_gpu_gate import compare
+from test_gpu_gate import bf16_ambiguous, compare
 
 pytestmark = pytest.mark.gpu
 
@@ -93,7 +93,9 @@ def test_packed_path_matches_oracle_and_fp32_path(g_inputs, D, g_expand, S):
     dev = [t.transpose(1, 2).contiguous().cuda().transpose(1, 2) for t in (pre_k, post_k, value)]
     scores, mask = g.scores_and_mask(dev[0], dev[1], dev[2], thr)
     assert g.__dict__.get("_packed_cache") is not None, "bf16 inputs of more than 4 tokens take the packed path"
-    compare(scores, mask, ref, thr, f"packed {'+'.join(g_inputs)} D{D} S{S}", bf16_inputs=True)
+    used = {"pre_k": pre_k, "post_k": post_k, "v": value}
+    amb = bf16_ambiguous(*(used[n] for n in g_inputs))
+    compare(scores, mask, ref, thr, f"packed {'+'.join(g_inputs)} D{D} S{S}", ambiguous=amb)
     # the fp32 MFMA path on the same inputs (no packed weights)
     norms = [g.pre_key_norm, g.post_key_norm, g.value_norm]
     wn = [m.weight.detach() if isinstance(m, wgate.GatingRMSNorm) else None for m in norms]
@@ -103,7 +105,7 @@ def test_packed_path_matches_oracle_and_fp32_path(g_inputs, D, g_expand, S):
         use["v"] if "v" in g_inputs else None, wn[0], wn[1], wn[2],
         g.conv1.weight.detach(), g.conv1.bias.detach(), g.conv2.weight.detach(), g.conv2.bias.detach(),
         g.inner_dim, g.act, True, 0.0, thr, like=dev[1])
-    compare(s32, m32, ref, thr, f"fp32 path {'+'.join(g_inputs)} D{D} S{S}", bf16_inputs=True)
+    compare(s32, m32, ref, thr, f"fp32 path {'+'.join(g_inputs)} D{D} S{S}", ambiguous=amb)
     d = (scores - s32).abs()
     print(f"[gate packed vs fp32 path] max|dg|={d.max().item():.2e} tokens |dg|>2e-6: "
           f"{(d > 2e-6).float().mean().item():.4%}", flush=True)
@@ -126,7 +128,8 @@ def test_packed_weights_follow_in_place_updates_and_misaligned_inputs_fall_back(
     ref = ogate.gate_scores(pre_k, post_k, None, p2)
     second, mask = g.scores_and_mask(pk, kk, None, 0.5)
     assert not torch.equal(first, second)
-    compare(second, mask, ref, 0.5, "packed after in-place updates", bf16_inputs=True)
+    amb = bf16_ambiguous(pre_k, post_k)
+    compare(second, mask, ref, 0.5, "packed after in-place updates", ambiguous=amb)
     # rows starting 2 bytes past a 16-byte boundary: no packed read, same results
     buf = torch.empty(2, H * S * D + 1, dtype=torch.bfloat16, device="cuda")
     pk_m = buf[0, 1:].view(1, H, S, D)
@@ -134,7 +137,7 @@ def test_packed_weights_follow_in_place_updates_and_misaligned_inputs_fall_back(
     pk_m.copy_(pk)
     kk_m.copy_(kk)
     third, mask3 = g.scores_and_mask(pk_m, kk_m, None, 0.5)
-    compare(third, mask3, ref, 0.5, "misaligned inputs (fp32 path)", bf16_inputs=True)
+    compare(third, mask3, ref, 0.5, "misaligned inputs (fp32 path)", ambiguous=amb)
 
 
 def test_packed_path_without_rms_matches_fp32_path():

@@ -4,9 +4,10 @@ prefill then 32 decode steps at positions 2048..2079, against the oracle layer.
 
 Checked: the dual-cache state after prefill and after decoding (block tables,
 global lengths, local flags, bump pointer) is bit-exact -- i.e. admission and
-compaction match -- with any oracle score within 1e-6 of the threshold
-reported (none occur for this seed); layer outputs agree within max-abs 2e-2 /
-mean-abs 2e-3.  Both immediate and deferred gating (g_defer)."""
+compaction match; a head with an oracle score within 1e-6 of the threshold
+would be left out of the comparison and reported (none occur for these
+seeds); layer outputs agree within max-abs 2e-2 / mean-abs 2e-3.  Both
+immediate and deferred gating (g_defer)."""
 import numpy as np
 import pytest
 import torch
@@ -52,6 +53,40 @@ def assert_same_state(a, b, label):
         assert np.array_equal(np.asarray(x), np.asarray(y)), f"{label}: {name} differs"
 
 
+def _logical_global_k(table, lengths, pool_k, h, lb):
+    n = int(lengths[0, h])
+    ids = torch.as_tensor(np.asarray(table[0, h, lb:lb + (n + 15) // 16])).long()
+    rows = (ids[:, None] * 16 + torch.arange(16)[None]).reshape(-1)[:n]
+    return pool_k[rows].float()
+
+
+def compare_state(cache, orc, near_heads, label, lb=128 // 16):
+    """The cache state against the oracle's.  Heads with a token whose oracle
+    score lies within 1e-6 of the threshold are left out (their admission may
+    legitimately differ); for every other head the global length, local flags
+    and logical global keys are compared, and the block table for the heads
+    allocated before the first such head (pages are handed out in head
+    order).  With no such head everything is compared, bump pointer included."""
+    a, b = cache_state(cache), oracle_state(orc)
+    if not near_heads:
+        assert_same_state(a, b, label)
+        print(f"[layer e2e] {label}: whole cache state bit-exact", flush=True)
+        return
+    H = a[1].shape[1]
+    keep = [h for h in range(H) if h not in near_heads]
+    first = min(near_heads)
+    for h in keep:
+        assert a[1][0, h] == b[1][0, h], f"{label}: global length of head {h}"
+        assert np.array_equal(a[2][0, h], b[2][0, h]), f"{label}: local flags of head {h}"
+        ka = _logical_global_k(a[0], a[1], cache.block_pool_k.cpu(), h, lb)
+        kb = _logical_global_k(b[0], b[1], orc.cache.block_pool_k, h, lb)
+        assert torch.equal(ka, kb), f"{label}: global keys of head {h}"
+    for h in range(first):
+        assert np.array_equal(a[0][0, h], b[0][0, h]), f"{label}: block table of head {h}"
+    print(f"[layer e2e] {label}: heads {sorted(near_heads)} left out (near-threshold); "
+          f"heads {keep} bit-exact", flush=True)
+
+
 @pytest.mark.parametrize("g_defer,qwen3", [(False, False), (True, False), (False, True), (True, True)])
 def test_config1_layer_end_to_end(g_defer, qwen3):
     """qwen3: Qwen3's layer variant (per-head q/k norms before the pre-RoPE
@@ -65,7 +100,9 @@ def test_config1_layer_end_to_end(g_defer, qwen3):
     orc = OracleLayer(w, 512, 8, 2, 64, 128, cfg["max_tokens_per_head"], g_defer=g_defer, kv_dtype=torch.bfloat16,
                       qk_norm=qwen3)
     o_out, o_mask, o_g = orc.prefill(x, torch.arange(S))
-    near = int((o_g - 0.1).abs().lt(1e-6).sum())
+    near_t = (o_g - 0.1).abs().lt(1e-6)  # (H, S)
+    near = int(near_t.sum())
+    near_heads = set(torch.nonzero(near_t.any(-1)).flatten().tolist())
     admitted = o_mask.float().mean().item()
     layer, rope = product_layer(cfg, w, qk_norm=qwen3)
     cache = DualCache()
@@ -78,14 +115,15 @@ def test_config1_layer_end_to_end(g_defer, qwen3):
     print(f"[layer e2e] prefill: admitted {admitted:.3f}, near-threshold {near}, "
           f"max_abs {err.max().item():.2e} mean_abs {err.mean().item():.2e}", flush=True)
     assert 0.1 < admitted < 0.3
-    if near == 0:
-        assert_same_state(cache_state(cache), oracle_state(orc), "after prefill")
+    compare_state(cache, orc, near_heads, "after prefill")
     assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
     worst = 0.0
     for i, xi in enumerate(xs):
         o_o, o_m, o_gi = orc.decode(xi, S + i)
         if o_gi is not None:
-            near += int((o_gi - 0.1).abs().lt(1e-6).sum())
+            ni = (o_gi - 0.1).abs().lt(1e-6)  # (H,)
+            near += int(ni.sum())
+            near_heads |= set(torch.nonzero(ni).flatten().tolist())
         xgi = xi.cuda()
         with torch.no_grad():
             oi, _, _ = layer(3, xgi, rope(xgi, torch.tensor([[S + i]], device="cuda")), None, cache)
@@ -95,5 +133,4 @@ def test_config1_layer_end_to_end(g_defer, qwen3):
     torch.cuda.synchronize()
     print(f"[layer e2e] decode: worst max_abs {worst:.2e}, near-threshold total {near}", flush=True)
     assert (cache.local_ptr, cache.local_length) == (orc.cache.local_ptr, orc.cache.local_length)
-    if near == 0:
-        assert_same_state(cache_state(cache), oracle_state(orc), "after decode")
+    compare_state(cache, orc, near_heads, "after decode")
