@@ -40,7 +40,9 @@ def parse():
     p.add_argument("--e2e", action="store_true",
                    help="only the BASELINE config-5 end-to-end run: a 32-layer Llama-3.1-8B-shaped model, "
                         "chunked prefill of --e2e-prompt tokens then --e2e-steps greedy decode steps, "
-                        "gated and all-admitted, on one GPU (several minutes)")
+                        "gated and all-admitted, on one GPU (about 1.5 minutes at 400K)")
+    p.add_argument("--no-e2e", action="store_true",
+                   help="leave the config-5 end-to-end run out of the default line")
     p.add_argument("--e2e-prompt", type=int, default=400000)
     p.add_argument("--e2e-chunk", type=int, default=4096, help="prompt tokens per prefill chunk")
     p.add_argument("--e2e-steps", type=int, default=256)
@@ -414,7 +416,10 @@ def e2e_section(args):
     out = {"workload": f"e2e_{tag}_{S // 1000}k (BASELINE config 5): {ec.num_hidden_layers} layers, "
                        f"hidden {ec.hidden_size}, FFN {ec.intermediate_size}, vocab {ec.vocab_size}, "
                        f"prompt {S} in {args.e2e_chunk}-token chunks, {steps} greedy decode steps, W {W}",
-           "data": "synthetic: random-init bf16 weights, uniform random token ids"}
+           "data": "synthetic: random-init bf16 weights, uniform random token ids",
+           "gating": ("deferred (g_defer, as scripts/profiling.py:212-213): decode steps re-gate the window "
+                      "when its last slot is written" if ec.g_defer else "every token"),
+           "decode": "each step one replay of a captured HIP graph of the whole model's step"}
     log("calibrating the gates")
     e2e.calibrate_gates(model, ids, args.e2e_admit)
     # pass-through (phase "warmup") until a run switches them on; graph runs never do
@@ -520,7 +525,7 @@ def main():
             "traffic": DECODE_TRAFFIC_BYTES,
             "traffic_source": DECODE_TRAFFIC_SOURCE,
             "bytes_per_launch": nbytes,
-            "launch": "wgkv_paged_decode_attn = decode_split_kernel (split-K chunks, last arriver merges)",
+            "launch": "wgkv_paged_decode_attn = decode_split_kernel + decode_merge_kernel",
         },
     }
     if not args.no_secondary:
@@ -549,6 +554,12 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_layer:
         result["layer_config1"] = layer_section(dev, args.cpu_seconds)
+    if not args.no_e2e:
+        torch.cuda.empty_cache()
+        try:
+            result["e2e"] = e2e_section(args)
+        except Exception as exc:  # the decode and prefill lines above stand on their own
+            result["e2e"] = {"error": f"{type(exc).__name__}: {exc}"}
     print(json.dumps(result), flush=True)
 
 

@@ -47,3 +47,20 @@ def test_timing_hooks_wrap_the_named_functions(granularity):
     assert t.phase == "warmup" and all(v == 0.0 for v in t.ms.values())
     with pytest.raises(ValueError):
         e2e.install_timing(m, "layer")
+
+
+def test_prompt_chunks_fold_short_tail_and_reject_bad_sizes():
+    """Chunk spans of e2e.run: contiguous, covering the prompt, every chunk
+    after the first 64-aligned and at least W long (a short tail joins the
+    chunk before it); impossible chunk sizes fail before any prefill work."""
+    from wgkv import e2e
+    W = 1024
+    for S in (400000, 4096 * 3 + 100, 4096 * 3 + 1024, 5000, 700, 4096):
+        spans = e2e.prompt_chunks(S, 4096, W)
+        assert spans[0][0] == 0 and spans[-1][1] == S
+        assert all(a[1] == b[0] for a, b in zip(spans, spans[1:]))
+        assert all(c0 % 64 == 0 and c1 - c0 >= W for c0, c1 in spans[1:])
+    assert e2e.prompt_chunks(4096 * 3 + 100, 4096, W)[-1] == (4096 * 2, 4096 * 3 + 100)
+    for bad in (1000, 4000, 512):
+        with pytest.raises(ValueError):
+            e2e.prompt_chunks(10000, bad, W)

@@ -384,6 +384,21 @@ def kv_cache_mib(cache):
     return b / (1024 * 1024)
 
 
+def prompt_chunks(S, chunk, W):
+    """[start, end) spans of a prompt of S tokens fed in chunks: every chunk
+    after the first must start at a multiple of 64 and hold at least W
+    tokens, so ``chunk`` must be a multiple of 64 and at least W, and a tail
+    shorter than W joins the chunk before it.  Checked before any prefill
+    work starts."""
+    if chunk % 64 or chunk < W:
+        raise ValueError(f"prompt chunks must be a multiple of 64 and at least W={W} tokens (got {chunk})")
+    spans = [[c0, min(c0 + chunk, S)] for c0 in range(0, S, chunk)]
+    if len(spans) > 1 and spans[-1][1] - spans[-1][0] < W:
+        tail = spans.pop()
+        spans[-1][1] = tail[1]
+    return [tuple(sp) for sp in spans]
+
+
 @torch.no_grad()
 def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=False, timers=None):
     """Chunked prefill of ids (1, S), then ``steps`` greedy decode steps, each
@@ -395,6 +410,7 @@ def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=Fals
         raise ValueError("per-granularity timers synchronise around each call; use an eager run")
     phase = (lambda name: setattr(timers, "phase", name)) if timers is not None else (lambda name: None)
     S = ids.shape[1]
+    spans = prompt_chunks(S, chunk, model.cfg.local_window_size)
     cache = DualCache()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -402,10 +418,10 @@ def run(model, ids, steps, chunk=4096, warmup_steps=2, progress=None, graph=Fals
     phase("prefill")
     ev0.record()
     logits = None
-    for c0 in range(0, S, chunk):
-        logits = model.forward_tokens(ids[:, c0:c0 + chunk], c0, cache)
-        if progress is not None and (c0 // chunk) % 16 == 0:
-            progress(f"prefill chunk {c0 // chunk + 1}/{(S + chunk - 1) // chunk}")
+    for n, (c0, c1) in enumerate(spans):
+        logits = model.forward_tokens(ids[:, c0:c1], c0, cache)
+        if progress is not None and n % 16 == 0:
+            progress(f"prefill chunk {n + 1}/{len(spans)}")
     ev1.record()
     torch.cuda.synchronize()
     res = E2EResult(prompt_length=S, prefill_ms=ev0.elapsed_time(ev1))
