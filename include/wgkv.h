@@ -316,10 +316,13 @@ int wgkv_sparse_prefill_attn(
  *      keys below chunk_start from the ring, the rest from the chunk.
  *   3. wgkv_chunk_cache_update(stage 1): ring slot i <- position
  *      chunk_start + chunk_len - W + i (flags and, with pre_key, the
- *      deferred-gating pre-RoPE keys).
- * Both stages of one chunk take the same workspace (stage 0 leaves an abort
- * flag there that stage 1 reads: a capacity failure sets status =
- * WGKV_ERR_CAPACITY and the chunk writes nothing).  key/value/pre_key are the
+ *      deferred-gating pre-RoPE keys); the global lengths and
+ *      next_free_block take the chunk's admissions here.
+ * Stage 0 is one launch (counts, plan and compaction); the pages and block
+ * table entries are final after it, the lengths after stage 1.  Both stages
+ * of one chunk take the same workspace (stage 0 leaves the counts and an
+ * abort flag there that stage 1 reads: a capacity failure sets status =
+ * WGKV_ERR_CAPACITY and the chunk writes nothing).  Up to 1024 heads.  key/value/pre_key are the
  * chunk's (Hkv, chunk_len, D) bf16 (strides per head and per position, d
  * contiguous); g_mask (Hkv, chunk_len) u8.  Requires chunk_start and W
  * multiples of 64, W a multiple of page_size and, after the first chunk,

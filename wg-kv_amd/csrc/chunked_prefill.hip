@@ -19,6 +19,7 @@
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
 constexpr int kTile = 512;   // virtual positions per scan tile
 constexpr int kBlk = 64;
 
@@ -30,6 +31,7 @@ struct ChunkArgs {
   int64_t pk_sh, pk_ss;
   const uint8_t* mask;  // chunk flags (H, C)
   int64_t m_sh;
+  int mask_vec16;       // mask rows 16-byte aligned (16 flags per load)
   int layer, H, C, D, W, page, max_tokens_per_head, c0;
   int64_t total_pages;
   uint16_t* pool_k;
@@ -43,13 +45,15 @@ struct ChunkArgs {
   int32_t* status;
   int32_t* column_count;  // (H, R_chunk)
   int r0, rchunk;         // first global row block of the chunk, row blocks in the chunk
-  // workspace
-  int ntiles;
-  int32_t* tile_cnt;
-  int32_t* tile_base;
-  int32_t* gl_before;
+  int ntiles;             // kTile-position tiles of the virtual sequence
+  // workspace, written by stage 0 and read by stage 1
+  int32_t* adm;           // (H) positions admitted by the chunk
+  int32_t* gl_before;     // (H) global lengths before the chunk
+  int32_t* next_free_after;
   int32_t* abort_flag;
 };
+
+constexpr int kMaxHeads = 1024;
 
 // Virtual sequence of a chunk: ring positions (c0 > 0 only) then the chunk.
 __device__ __forceinline__ int vlen(const ChunkArgs& a) { return (a.c0 > 0 ? a.W : 0) + a.C; }
@@ -61,132 +65,204 @@ __device__ __forceinline__ bool vflag(const ChunkArgs& a, int h, int v) {
   return a.mask[(int64_t)h * a.m_sh + (v - nr)] != 0;
 }
 
-__global__ __launch_bounds__(kThreads) void chunk_count_kernel(ChunkArgs a) {
-  __shared__ int s_red[kThreads];
-  const int h = blockIdx.y, tile = blockIdx.x;
-  const int n_adm = vlen(a) - a.W;  // admission range [0, n_adm) of the virtual sequence
-  int cnt = 0;
-  for (int v = tile * kTile + threadIdx.x; v < min(n_adm, (tile + 1) * kTile); v += kThreads) cnt += vflag(a, h, v);
-  s_red[threadIdx.x] = cnt;
-  __syncthreads();
-  for (int off = kThreads / 2; off > 0; off >>= 1) {
-    if (threadIdx.x < off) s_red[threadIdx.x] += s_red[threadIdx.x + off];
-    __syncthreads();
+// Admitted flags among virtual positions [v, min(v + 16, lim)) of head h
+// (flags are 0/1 bytes, so popcounts of the 16 bytes count them).  The ring
+// length W and v are multiples of 16, so the 16 positions lie all in the
+// ring or all in the chunk; reads never pass the chunk's own flags (v < lim
+// <= chunk_len + ring, and lim - v < 16 only at the admission range's end,
+// which lies W - 16 or more flags before the end of the chunk).
+__device__ __forceinline__ int count16(const ChunkArgs& a, int h, int v, int lim) {
+  const int nr = vring(a);
+  const int n = min(16, lim - v);
+  const uint8_t* p = v < nr ? a.local_is_global + ((int64_t)a.layer * a.H + h) * a.W + v
+                            : a.mask + (int64_t)h * a.m_sh + (v - nr);
+  u32x4_t w;
+  if (v < nr || a.mask_vec16) {
+    w = *(const u32x4_t*)p;
+  } else {
+    w = (u32x4_t){0u, 0u, 0u, 0u};
+    for (int i = 0; i < n; ++i) w[i >> 2] |= (uint32_t)p[i] << (8 * (i & 3));
   }
-  if (threadIdx.x == 0) a.tile_cnt[h * a.ntiles + tile] = s_red[0];
+  if (n < 16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int keep = min(4, max(0, n - 4 * q));  // bytes of word q inside the range
+      w[q] &= keep == 4 ? ~0u : ((1u << (8 * keep)) - 1u);
+    }
+  }
+  return __builtin_popcount(w[0]) + __builtin_popcount(w[1]) + __builtin_popcount(w[2]) + __builtin_popcount(w[3]);
 }
 
-// One workgroup: totals, capacity, page allocation (head order), lengths.
-// Everything is checked before the first write.
-__global__ __launch_bounds__(kThreads) void chunk_plan_kernel(ChunkArgs a) {
+// Admission of one chunk in one launch (workgroup = kTile virtual positions
+// of one head).  Every workgroup first counts the admitted flags of every
+// head and makes the same plan from them -- totals, capacity checks before
+// any write, pages bump-allocated in head order -- so no workgroup waits for
+// another; then it compacts its own tile into the head's pages (new pages are
+// numbered arithmetically from the plan, so the block-table entries written
+// here are not read back) and writes the column counts of the row blocks
+// whose band starts inside its tile: the count of row block r is the number
+// of admitted positions below p = 64 r - W + 1, i.e. the inclusive count at
+// virtual index p - 1 - base.  The global lengths and the bump pointer are
+// left to stage 1 (every workgroup here reads the lengths from before the
+// chunk).  Independent loads are issued together: the tile's flags, every
+// head's length and the 16-flag count loads, so the launch waits on memory
+// about three times (flags and lengths, existing page ids, K/V rows).
+__global__ __launch_bounds__(kThreads) void chunk_admit_kernel(ChunkArgs a) {
+  constexpr int kPer = kTile / kThreads;
+  constexpr int kCnt = 16;       // flags per count load
+  constexpr int kLoads = 16;     // count loads per thread issued together
+  __shared__ int s_tot[kMaxHeads];    // admitted positions of each head
+  __shared__ int s_first[kMaxHeads];  // first new page of each head, relative to the bump pointer
   __shared__ int s_tmp[kThreads];
-  __shared__ int s_n[1024];
-  __shared__ int s_first[1024];
-  __shared__ int s_fail;
+  __shared__ int s_wave[kWaves];
+  __shared__ int s_pre, s_fail, s_total_pages, s_nf;
+  __shared__ int s_src[kTile];        // virtual index
+  __shared__ int64_t s_dst[kTile];    // pool row
+  const int h = blockIdx.y, tile = blockIdx.x;
   const int t = threadIdx.x;
-  if (t == 0) s_fail = 0;
-  __syncthreads();
+  const int lane = t & 63, wid = t >> 6;
+  const int nr = vring(a);
+  const int n_adm = vlen(a) - a.W;  // admission range [0, n_adm) of the virtual sequence
   const int lb = a.W / a.page;
-  for (int h = t; h < a.H; h += kThreads) {
-    int run = 0;
-    for (int tl = 0; tl < a.ntiles; ++tl) {
-      a.tile_base[h * a.ntiles + tl] = run;
-      run += a.tile_cnt[h * a.ntiles + tl];
-    }
-    s_n[h] = run;
-    const int gl = a.global_lengths[a.layer * a.H + h];
-    if (run > 0 && (a.W + gl + run > a.max_tokens_per_head || lb + (gl + run + a.page - 1) / a.page > a.max_pages))
-      atomicOr(&s_fail, 1);
+
+  // this tile's flags and the lengths before the chunk
+  const int v0 = tile * kTile + t * kPer;
+  bool f[kPer];
+#pragma unroll
+  for (int k = 0; k < kPer; ++k) f[k] = v0 + k < n_adm && vflag(a, h, v0 + k);
+  const int gl_t = t < a.H ? a.global_lengths[a.layer * a.H + t] : 0;
+  for (int i = t; i < a.H; i += kThreads) s_tot[i] = 0;
+  if (t == 0) {
+    s_pre = 0;
+    s_fail = 0;
+    s_nf = *a.next_free;
   }
   __syncthreads();
-  const int nf = *a.next_free;
-  int carry = 0;
-  for (int h0 = 0; h0 < a.H; h0 += kThreads) {
-    const int h = h0 + t;
-    int pages = 0;
-    if (h < a.H) {
-      const int gl = a.global_lengths[a.layer * a.H + h];
-      pages = (gl + s_n[h] + a.page - 1) / a.page - (gl + a.page - 1) / a.page;
+
+  // ---- admitted counts of every head, and of this head before the tile ----
+  const int gph = n_adm > 0 ? (n_adm + kCnt - 1) / kCnt : 0;  // count loads per head
+  const int ng = a.H * gph;
+  for (int g0 = t; g0 < ng; g0 += kThreads * kLoads) {
+    int c[kLoads];
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+      const int g = g0 + k * kThreads;
+      c[k] = g < ng ? count16(a, g / gph, (g % gph) * kCnt, n_adm) : 0;
     }
-    int total = 0;
-    const int excl = block_exclusive_scan_256(pages, s_tmp, &total);
-    if (h < a.H) s_first[h] = nf + carry + excl;
-    carry += total;
+#pragma unroll
+    for (int k = 0; k < kLoads; ++k) {
+      const int g = g0 + k * kThreads;
+      if (g < ng && c[k]) {
+        const int hh = g / gph;
+        atomicAdd(&s_tot[hh], c[k]);
+        if (hh == h && (g % gph) * kCnt < tile * kTile) atomicAdd(&s_pre, c[k]);
+      }
+    }
   }
-  if (t == 0 && (int64_t)nf + carry > a.total_pages) s_fail = 1;
   __syncthreads();
-  // column counts the scatter does not write: rows whose band starts at
-  // position 0 and, on failure, every row (the chunk then sees no columns)
-  for (int e = t; e < a.H * a.rchunk; e += kThreads) {
-    const int i = e % a.rchunk;
-    if (s_fail || (a.r0 + i) * kBlk - a.W + 1 <= 0) a.column_count[e] = 0;
-  }
-  if (s_fail) {
+
+  // ---- the plan (identical in every workgroup) ----------------------------
+  if (a.H <= 64) {
+    if (wid == 0) {
+      int pages = 0;
+      if (lane < a.H) {
+        const int n = s_tot[lane];
+        pages = (gl_t + n + a.page - 1) / a.page - (gl_t + a.page - 1) / a.page;
+        if (n > 0 && (a.W + gl_t + n > a.max_tokens_per_head || lb + (gl_t + n + a.page - 1) / a.page > a.max_pages))
+          s_fail = 1;
+      }
+      const int incl = wave_incl_scan(pages, lane);
+      if (lane < a.H) s_first[lane] = incl - pages;
+      if (lane == 63) {
+        s_total_pages = incl;
+        if ((int64_t)s_nf + incl > a.total_pages) s_fail = 1;
+      }
+    }
+  } else {
+    int carry = 0;
+    for (int h0 = 0; h0 < a.H; h0 += kThreads) {
+      const int hh = h0 + t;
+      int pages = 0;
+      if (hh < a.H) {
+        const int n = s_tot[hh];
+        const int gl = h0 == 0 ? gl_t : a.global_lengths[a.layer * a.H + hh];
+        pages = (gl + n + a.page - 1) / a.page - (gl + a.page - 1) / a.page;
+        if (n > 0 && (a.W + gl + n > a.max_tokens_per_head || lb + (gl + n + a.page - 1) / a.page > a.max_pages))
+          atomicOr(&s_fail, 1);
+      }
+      int total = 0;
+      const int excl = block_exclusive_scan_256(pages, s_tmp, &total);
+      if (hh < a.H) s_first[hh] = carry + excl;
+      carry += total;
+    }
     if (t == 0) {
+      s_total_pages = carry;
+      if ((int64_t)s_nf + carry > a.total_pages) s_fail = 1;
+    }
+  }
+  __syncthreads();
+  const bool fail = s_fail != 0;
+  int32_t* cc = a.column_count + (int64_t)h * a.rchunk;
+  if (tile == 0) {
+    // rows whose band starts at position 0 see no admitted column; on a
+    // failure no row does (the chunk then attends to its band only)
+    for (int i = t; i < a.rchunk; i += kThreads)
+      if (fail || (a.r0 + i) * kBlk - a.W + 1 <= 0) cc[i] = 0;
+    if (fail && h == 0 && t == 0) {
       *a.status = WGKV_ERR_CAPACITY;
       *a.abort_flag = 1;
     }
-    return;
   }
-  for (int h = t; h < a.H; h += kThreads) {
-    const int gl = a.global_lengths[a.layer * a.H + h];
-    const int first_new = (gl + a.page - 1) / a.page;
-    const int pages = (gl + s_n[h] + a.page - 1) / a.page - first_new;
-    int32_t* row = a.block_table + ((int64_t)a.layer * a.H + h) * a.max_pages + lb;
-    for (int i = 0; i < pages; ++i) row[first_new + i] = s_first[h] + i;
-    a.gl_before[h] = gl;
-    a.global_lengths[a.layer * a.H + h] = gl + s_n[h];
-  }
-  if (t == 0) {
-    *a.next_free = nf + carry;
-    *a.abort_flag = 0;
-  }
-}
+  if (fail) return;  // tile 0 of each head has zeroed its column counts
 
-// Stable compaction of the admission range into the heads' global pages, and
-// column_count of the chunk's row blocks: the count of row block r is the
-// number of admitted positions below p = 64 r - W + 1, i.e. the inclusive
-// count at virtual index p - 1 - base, which falls in exactly one tile.
-__global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(ChunkArgs a) {
-  constexpr int kPer = kTile / kThreads;
-  __shared__ int s_tmp[kThreads];
-  __shared__ int s_src[kTile];     // virtual index
-  __shared__ int64_t s_dst[kTile]; // pool row
-  if (*a.abort_flag) return;
-  const int h = blockIdx.y, tile = blockIdx.x;
-  const int t = threadIdx.x;
-  const int nr = vring(a);
-  const int n_adm = vlen(a) - a.W;
-  const int lb = a.W / a.page;
-  const int base = a.c0 > 0 ? a.c0 - a.W : 0;  // global position of virtual index 0
+  // ---- this tile: stable compaction and column counts ----------------------
+  const int gl0 = a.global_lengths[a.layer * a.H + h];
+  const int first_new = (gl0 + a.page - 1) / a.page;  // index of the head's first new page
+  const int page0 = s_nf + s_first[h];                  // its page id
   const int32_t* bt = a.block_table + ((int64_t)a.layer * a.H + h) * a.max_pages + lb;
-  const int gl0 = a.gl_before[h];
-  const int v0 = tile * kTile + t * kPer;
-  bool f[kPer];
+  if (tile == 0) {
+    const int n_h = s_tot[h];
+    const int pages = (gl0 + n_h + a.page - 1) / a.page - first_new;
+    int32_t* row = a.block_table + ((int64_t)a.layer * a.H + h) * a.max_pages + lb;
+    for (int i = t; i < pages; i += kThreads) row[first_new + i] = page0 + i;
+    if (t == 0) {
+      a.adm[h] = n_h;
+      a.gl_before[h] = gl0;
+      if (h == 0) {
+        *a.next_free_after = s_nf + s_total_pages;
+        *a.abort_flag = 0;
+      }
+    }
+  }
+  const int base = a.c0 > 0 ? a.c0 - a.W : 0;  // global position of virtual index 0
   int cnt = 0;
 #pragma unroll
-  for (int k = 0; k < kPer; ++k) {
-    const int v = v0 + k;
-    f[k] = v < n_adm && vflag(a, h, v);
-    cnt += f[k] ? 1 : 0;
+  for (int k = 0; k < kPer; ++k) cnt += f[k] ? 1 : 0;
+  const int incl = wave_incl_scan(cnt, lane);
+  if (lane == 63) s_wave[wid] = incl;
+  __syncthreads();
+  int o = incl - cnt, total = 0;
+#pragma unroll
+  for (int w = 0; w < kWaves; ++w) {
+    o += w < wid ? s_wave[w] : 0;
+    total += s_wave[w];
   }
-  int total = 0;
-  int o = block_exclusive_scan_256(cnt, s_tmp, &total);
-  const int before = gl0 + a.tile_base[h * a.ntiles + tile];
-  int32_t* cc = a.column_count + (int64_t)h * a.rchunk;
+  const int before = gl0 + s_pre;
 #pragma unroll
   for (int k = 0; k < kPer; ++k) {
     const int v = v0 + k;
     if (f[k]) {
       const int j = before + o;  // logical index in the head's global cache
+      const int pi = j / a.page;
+      const int pg = pi < first_new ? bt[pi] : page0 + (pi - first_new);
       s_src[o] = v;
-      s_dst[o] = (int64_t)bt[j / a.page] * a.page + j % a.page;
+      s_dst[o] = (int64_t)pg * a.page + j % a.page;
       ++o;
     }
     // o is now the inclusive count at v within the tile
-    const int p = base + v + 1;
-    if (v < n_adm && p > 0 && (p + a.W - 1) % kBlk == 0) {
-      const int r = (p + a.W - 1) / kBlk;
+    const int pp = base + v + 1;
+    if (v < n_adm && pp > 0 && (pp + a.W - 1) % kBlk == 0) {
+      const int r = (pp + a.W - 1) / kBlk;
       if (r >= a.r0 && r < a.r0 + a.rchunk) cc[r - a.r0] = before + o;
     }
   }
@@ -215,6 +291,12 @@ __global__ __launch_bounds__(kThreads) void chunk_scatter_kernel(ChunkArgs a) {
 __global__ __launch_bounds__(kThreads) void chunk_ring_kernel(ChunkArgs a) {
   if (*a.abort_flag) return;
   const int h = blockIdx.x;
+  if (blockIdx.y == 0 && threadIdx.x == 0) {
+    // stage 0's admissions become the head's global length (no kernel of
+    // stage 0 could, since all of them read the length from before)
+    a.global_lengths[a.layer * a.H + h] = a.gl_before[h] + a.adm[h];
+    if (h == 0) *a.next_free = *a.next_free_after;
+  }
   const int n_loc = min(a.W, a.c0 + a.C);
   const int first = a.C - n_loc;  // chunk row of slot 0
   const int i0 = blockIdx.y * kBlk, i1 = min(n_loc, i0 + kBlk);
@@ -240,8 +322,9 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 }  // namespace
 
 extern "C" size_t wgkv_chunk_admit_workspace_bytes(int32_t num_kv_heads, int32_t chunk_len, int32_t local_window) {
-  const size_t ntiles = (size_t)(chunk_len + local_window + kTile - 1) / kTile;
-  return (2 * (size_t)num_kv_heads * ntiles + (size_t)num_kv_heads + 16) * sizeof(int32_t);
+  (void)chunk_len;
+  (void)local_window;
+  return (2 * (size_t)(num_kv_heads > 0 ? num_kv_heads : 0) + 16) * sizeof(int32_t);
 }
 
 extern "C" int wgkv_chunk_cache_update(
@@ -303,17 +386,15 @@ extern "C" int wgkv_chunk_cache_update(
   a.rchunk = (chunk_len + kBlk - 1) / kBlk;
   const int vl = (chunk_start > 0 ? local_window : 0) + chunk_len;
   a.ntiles = (vl + kTile - 1) / kTile;
+  a.mask_vec16 = (((uintptr_t)g_mask | (uintptr_t)gm_stride_h) & 15) == 0;
   int32_t* ws = (int32_t*)workspace;
-  a.tile_cnt = ws;
-  a.tile_base = ws + (size_t)num_kv_heads * a.ntiles;
-  a.gl_before = ws + 2 * (size_t)num_kv_heads * a.ntiles;
-  a.abort_flag = a.gl_before + num_kv_heads;
+  a.adm = ws;
+  a.gl_before = ws + num_kv_heads;
+  a.next_free_after = ws + 2 * (size_t)num_kv_heads;
+  a.abort_flag = a.next_free_after + 1;
   hipStream_t st = (hipStream_t)stream;
   if (stage == 0) {
-    dim3 grid(a.ntiles, num_kv_heads);
-    hipLaunchKernelGGL(chunk_count_kernel, grid, dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL(chunk_plan_kernel, dim3(1), dim3(kThreads), 0, st, a);
-    hipLaunchKernelGGL(chunk_scatter_kernel, grid, dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(chunk_admit_kernel, dim3(a.ntiles, num_kv_heads), dim3(kThreads), 0, st, a);
   } else {
     const int groups = (min(local_window, chunk_start + chunk_len) + kBlk - 1) / kBlk;
     hipLaunchKernelGGL(chunk_ring_kernel, dim3(num_kv_heads, groups), dim3(kThreads), 0, st, a);

@@ -89,16 +89,6 @@ struct Plan {
   int cp;        // sub-pages per chunk
 };
 
-// Inclusive prefix sum over the 64 lanes of a wave.
-__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const int u = __shfl_up(v, off, 64);
-    if (lane >= off) v += u;
-  }
-  return v;
-}
-
 // B*Hkv <= 64: lane bh of every wave takes head bh; the plan is two wave
 // scans in registers, no LDS and no barrier.  Workgroup 0 stores the plan
 // (first chunk of each head, then the chunk count) for the merge.

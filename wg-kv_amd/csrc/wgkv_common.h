@@ -82,6 +82,23 @@ WGKV_DEVICE float wave_sum(float x) {
   return (a + b) + (c + d);
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave.
+WGKV_DEVICE int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off, 64);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// Sum of an int over all 64 lanes (every lane gets the total).
+WGKV_DEVICE int wave_sum_int(int x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
 WGKV_DEVICE float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
