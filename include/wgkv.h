@@ -283,7 +283,7 @@ int wgkv_gate_pack_weights(
  *   (B, Hkv, R) contiguous, column_index with strides ci_sb, ci_sh.
  * Row block r of head hq (KV head hq / G) attends to the listed admitted
  * columns and to the band blocks [o, o+64), causally.  Softmax in fp32.
- * Supported: D in {64,128}, G in {1,2,4,8}, block 64.
+ * Supported: D in {32,64,128}, G = Hq/Hkv from 1 to 8, block 64.
  * ---------------------------------------------------------------------- */
 int wgkv_sparse_prefill_attn(
     const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,

@@ -108,6 +108,8 @@ CASES = [
     (1, 2, 1, 64, 128, [128, 256, 130], 0.0, False),
     (1, 4, 8, 128, 256, [2000], 0.2, False),
     (1, 2, 8, 128, 256, [1024, 1024, 512], 0.3, False),  # two head groups per KV head, continued chunks
+    (1, 2, 3, 32, 128, [256, 320, 512], 0.3, False),     # head_dim 32, three query heads per KV head
+    (1, 3, 3, 64, 64, [64, 128, 300], 0.4, True),
 ]
 
 

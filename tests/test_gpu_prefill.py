@@ -2,7 +2,8 @@
 
 Grid after utils/test_sparse_attn.py:7-13 (batch, KV heads, groups, S, head
 dim, window, admitted count; admitted set drawn like
-utils/test_sparse_utils.py:13-17), thinned for time.  Acceptance: max-abs
+utils/test_sparse_utils.py:13-17): every groups x head_dim pair of the
+contract at every sequence length, the other parameters rotating.  Acceptance: max-abs
 <= 2e-2 and mean-abs <= 2e-3 vs the fp64 masked SDPA, and the reference
 test's own criterion |maxdiff(kernel) - maxdiff(bf16 SDPA)| < 0.01
 (utils/test_sparse_attn.py:60-74).  The 32K-token shape is checked on a
@@ -40,16 +41,22 @@ def run(q, k, v, gm, W):
 
 
 CASES = []
-for B, Hkv, G in [(1, 2, 4), (2, 1, 1), (1, 3, 2), (1, 8, 4)]:
-    for S in [2, 63, 64, 65, 129, 193, 257, 1000, 2000]:
-        for D in [64, 128]:
-            for W in [64, 128, 256]:
-                for gs in [0, 123, 1000]:
-                    if Hkv * G * S > 8 * 1000 and S > 1000 and gs == 123:
-                        continue
-                    CASES.append((B, Hkv, G, S, D, W, gs))
-CASES = CASES[::3]  # every third case keeps every parameter value covered
-
+# Every (G, D) pair of the reference's contract (num_kv_groups 1-4, head_dim
+# 32/64/128) with every sequence length; window, admitted count, batch and
+# head count rotate through their values across the cases.
+_S = [2, 63, 64, 65, 127, 128, 129, 191, 192, 193, 255, 256, 257, 1000, 2000]
+_W = [64, 128, 256]
+_GS = [0, 123, 345, 567, 789, 1000]
+_BH = [(1, 1), (2, 2), (1, 3), (1, 4), (2, 8), (1, 2)]
+_i = 0
+for G in [1, 2, 3, 4]:
+    for D in [32, 64, 128]:
+        for S in _S:
+            B, Hkv = _BH[_i % len(_BH)]
+            if S >= 1000 and B * Hkv * G > 8:
+                B, Hkv = 1, 2
+            CASES.append((B, Hkv, G, S, D, _W[_i % len(_W)], _GS[(_i // 3) % len(_GS)]))
+            _i += 1
 
 @pytest.mark.parametrize("B,Hkv,G,S,D,W,gs", CASES)
 def test_reference_grid(B, Hkv, G, S, D, W, gs):

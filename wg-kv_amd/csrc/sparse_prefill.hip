@@ -68,14 +68,18 @@ __device__ __forceinline__ v4i16_t lds_read_tr16(const uint16_t* p) {
 // take one slice from each of 16 consecutive rows, so those rows must land
 // on 16 distinct slice positions modulo 256 bytes; a transpose read takes a
 // 32-byte slice pair from each of 8 consecutive rows.  The permutation only
-// uses the row bits that the 16-row and 32-row fragment offsets keep.
+// uses the row bits that the 16-row and 32-row fragment offsets keep.  At
+// D = 32 a row is 64 bytes: rows r and r + 4 share a 256-byte window
+// position, so the permutation takes bits 2-3 of the row (K: the 16 rows
+// fill 4 rows x 4 slices of the window; V: the 8 rows of a transpose read
+// use the two 32-byte halves alternately).
 template <int D>
 __device__ __forceinline__ int swz_k(int row) {
-  return D == 128 ? (row & 15) : ((row >> 1) & 7);
+  return D == 128 ? (row & 15) : D == 64 ? ((row >> 1) & 7) : ((row >> 2) & 3);
 }
 template <int D>
 __device__ __forceinline__ int swz_v(int row) {
-  return D == 128 ? 2 * (row & 7) : 2 * ((row >> 1) & 3);
+  return D == 128 ? 2 * (row & 7) : D == 64 ? 2 * ((row >> 1) & 3) : 2 * ((row >> 2) & 1);
 }
 
 struct PrefillArgs {
@@ -445,17 +449,26 @@ hipError_t launch(const PrefillArgs& a, hipStream_t st, bool chunked) {
   return hipGetLastError();
 }
 
-// Query heads per workgroup: min(G, 4)
-constexpr int kHeadsPerWg = 4;
+// Query heads per workgroup: the largest of 4, 2, 1 that divides G and lets
+// every wave load whole 1 KB blocks of a tile (2 * HPW waves, D / 8 blocks:
+// at most 2 heads at D = 32).  G = 3 then takes one head per workgroup.
+int heads_per_wg(int head_dim, int G) {
+  const int cap = head_dim == 32 ? 2 : 4;
+  for (int h = cap; h > 1; h >>= 1)
+    if (G % h == 0) return h;
+  return 1;
+}
 
 hipError_t launch_any(PrefillArgs& a, hipStream_t st, int head_dim, int G, bool chunked) {
   a.G = G;
-  const int hpw = G < kHeadsPerWg ? G : kHeadsPerWg;
+  const int hpw = heads_per_wg(head_dim, G);
   if (head_dim == 128)
     return hpw == 1 ? launch<128, 1>(a, st, chunked) : hpw == 2 ? launch<128, 2>(a, st, chunked)
                     : launch<128, 4>(a, st, chunked);
-  return hpw == 1 ? launch<64, 1>(a, st, chunked) : hpw == 2 ? launch<64, 2>(a, st, chunked)
-                  : launch<64, 4>(a, st, chunked);
+  if (head_dim == 64)
+    return hpw == 1 ? launch<64, 1>(a, st, chunked) : hpw == 2 ? launch<64, 2>(a, st, chunked)
+                    : launch<64, 4>(a, st, chunked);
+  return hpw == 1 ? launch<32, 1>(a, st, chunked) : launch<32, 2>(a, st, chunked);
 }
 
 }  // namespace
@@ -472,8 +485,8 @@ extern "C" int wgkv_sparse_prefill_attn(
   if (batch <= 0 || seq_len <= 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return WGKV_ERR_ARG;
   if (block != kBlk) return WGKV_ERR_UNSUPPORTED;
   const int G = num_q_heads / num_kv_heads;
-  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return WGKV_ERR_UNSUPPORTED;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (G < 1 || G > 8) return WGKV_ERR_UNSUPPORTED;
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15) return WGKV_ERR_UNSUPPORTED;
   if ((q_sb | q_ss | q_sh | kv_sb | kv_ss | kv_sh | o_sb | o_ss | o_sh) & 7) return WGKV_ERR_UNSUPPORTED;
   PrefillArgs a;
@@ -529,8 +542,8 @@ extern "C" int wgkv_chunk_prefill_attn(
   if (page_size != kPage) return WGKV_ERR_UNSUPPORTED;
   if (chunk_start > 0 && chunk_start < local_window) return WGKV_ERR_ARG;  // the ring must be full
   const int G = num_q_heads / num_kv_heads;
-  if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
-  if (G != 1 && G != 2 && G != 4 && G != 8) return WGKV_ERR_UNSUPPORTED;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (G < 1 || G > 8) return WGKV_ERR_UNSUPPORTED;
   if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out | (uintptr_t)pool_k | (uintptr_t)pool_v) & 15)
     return WGKV_ERR_UNSUPPORTED;
   if ((q_ss | q_sh | kv_ss | kv_sh | o_ss | o_sh) & 7) return WGKV_ERR_UNSUPPORTED;
