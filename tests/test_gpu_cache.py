@@ -146,23 +146,41 @@ def test_prefill_capacity_error_writes_nothing():
     assert bool((cache.block_table[:, :, lb:] == cache.total_blocks - 1).all())
 
 
-def test_decode_capacity_error_raises():
-    from wgkv import layers
+@pytest.mark.parametrize("per_step", [False, True])
+def test_decode_capacity_error_raises(per_step):
+    """Every token admitted, tiny per-head budget: promotion overflows.  By
+    default the decode steps do not read the device status (no host sync);
+    the failure stays latched and raise_if_failed reports it.  With
+    check_capacity_decode the step itself raises, as the reference's assert."""
+    from wgkv import _lib, layers
     from wgkv.cache import DualCache
-    # every token admitted, tiny per-head budget: promotion must overflow and raise
     sc = dict(scenarios.CACHE_SCENARIOS["short_prompt"], max_tokens_per_head=128 + 20, step_rate=1.0, rates=(1.0, 1.0))
     inp = scenarios.cache_inputs(sc)
     dev = torch.device("cuda:0")
     mods = [make_self(sc, l) for l in range(sc["L"])]
+    for m in mods:
+        m.config.check_capacity_decode = per_step
     cache = DualCache()
     for l in range(sc["L"]):
         q, pk, k, v, mask = inp["prompt"][l]
         layers.self_attn_forward_patch_inference(mods[l], cache, (1, sc["S"]), q.to(dev), pk.to(dev), k.to(dev),
                                                  v.to(dev), None, g_mask=mask.to(dev))
-    with pytest.raises(AssertionError):
+
+    def steps():
         for step in inp["steps"]:
             for l in range(sc["L"]):
                 q, pk, k, v, mask = step[l]
                 layers.self_attn_forward_patch_inference(mods[l], cache, (1, 1), q.to(dev), pk.to(dev), k.to(dev),
                                                          v.to(dev), None, g_mask=mask.to(dev))
+
+    if per_step:
+        with pytest.raises(AssertionError):
+            steps()
+    else:
+        steps()
+        torch.cuda.synchronize()
+        assert int(cache.status.item()) == _lib.ERR_CAPACITY
+        with pytest.raises(_lib.WGKVCapacityError):
+            cache.raise_if_failed("decode")
+        assert int(cache.status.item()) == 0
     assert int(cache.global_lengths.max()) <= 20

@@ -59,15 +59,22 @@ class WGKVConfig:
     snapkv_evict_ratio: float = 0.0
     snapkv_window_size: int = 256
     snapkv_kernel_size: int = 5
-    check_capacity: bool = True  # read the device status after cache writes (a host sync)
+    # Capacity failures are latched in the cache's device ``status`` (the
+    # failing write stores nothing).  check_capacity reads it after each
+    # layer's prefill (one host sync per layer and chunk); a decode step reads
+    # it only with check_capacity_decode (a host sync per step, as the
+    # reference's asserts make).  Otherwise a decode-time overflow stays latched
+    # until DualCache.raise_if_failed is called.
+    check_capacity: bool = True
+    check_capacity_decode: bool = False
 
     def __post_init__(self):
         if self.head_dim is None:
             self.head_dim = self.hidden_size // self.num_attention_heads
 
 
-def _layer_cache_check(self, cache, where):
-    if getattr(self.config, "check_capacity", True):
+def _layer_cache_check(self, cache, where, decode=False):
+    if getattr(self.config, "check_capacity_decode" if decode else "check_capacity", not decode):
         cache.raise_if_failed(where)
 
 
@@ -179,9 +186,10 @@ def refresh_local_is_global(self, past_key_value, device, on_device=False):
 
 
 def migrate_local_kv_to_global(self, past_key_value, device, local_blocks_per_head):
-    """src/modeling_layers.py:674-763 on the device (no host syncs)."""
+    """src/modeling_layers.py:674-763 on the device (no host syncs unless
+    check_capacity_decode asks for the reference's per-step overflow assert)."""
     ops.decode_append(past_key_value, 0, migrate=True, write=False)
-    _layer_cache_check(self, past_key_value, "migrate_local_kv_to_global")
+    _layer_cache_check(self, past_key_value, "migrate_local_kv_to_global", decode=True)
 
 
 def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
