@@ -219,14 +219,26 @@ int wgkv_decode_append_ring(
  * dtype, times its norm weight.  act 0 = exact-erf GELU, 1 = SiLU.
  * clamp_min > 0 applies the conv path's clamp (:205).  Outputs (may be NULL,
  * not both): scores f32 (B,H,S), mask u8 (B,H,S) = scores > threshold.
+ * precision: 0 = the gate with fp32 parameters (fp32 arithmetic after the
+ * inputs' norm cast); 1 / 2 = the gate with bf16 parameters, the reference's
+ * inference configuration (its scripts load the gate checkpoint in bf16,
+ * scripts/profiling.py:222-226), on bf16 inputs: each op's result is rounded
+ * to bf16 as torch rounds it -- the norm product, the first layer (1 = fast
+ * path :186-190: einsum output rounded, then the bias add rounded; 2 = conv
+ * path :197-199: one rounding after the bias), the activation, the second
+ * layer likewise, the sigmoid -- the weights passed as f32 copies of the
+ * bf16 values, and the score is compared with bf16(threshold) and clamped
+ * to bf16(clamp_min), as a bf16 tensor compared with a Python float is.
  * Supported: D in {64,128}, inner a multiple of 16, n_in*D <= 384.
  * w1_packed (may be NULL): the same weights as written by
- * wgkv_gate_pack_weights.  With bf16 inputs (16-byte aligned, strides
- * multiples of 8 elements) and seq_len > 4 the first layer then runs on the
- * bf16 matrix core: the norm weights are folded into w1 in fp32 and the
- * product split into three bf16 planes that carry all its bits, so the
- * result equals the fp32 layer up to rounding order.  Otherwise ignored
- * (w1 and the norm weights are always read by the other paths).
+ * wgkv_gate_pack_weights with the same precision.  With bf16 inputs (16-byte
+ * aligned, strides multiples of 8 elements; with precision != 0 16-byte
+ * aligned norm weights) and seq_len > 4 the first layer then runs on the
+ * bf16 matrix core.  precision 0: the norm weights are folded into w1 in
+ * fp32 and the product split into three bf16 planes that carry all its
+ * bits, so the result equals the fp32 layer up to rounding order; precision
+ * 1 / 2: one plane, w1 itself.  Otherwise ignored (w1 and the norm weights
+ * are always read by the other paths).
  * active_flag (may be NULL): a device int32; when given, the launch does
  * nothing unless *active_flag == active_value -- the condition is read on the
  * device, so a captured decode step can re-gate its window only on the step
@@ -247,7 +259,7 @@ int wgkv_gate_scores(
     const float* w_pre, const float* w_post, const float* w_v,
     const float* w1, const float* b1, const float* w2, const float* b2,
     int32_t batch, int32_t num_kv_heads, int32_t seq_len, int32_t head_dim, int32_t inner,
-    int32_t act, int32_t rms, float clamp_min, float threshold,
+    int32_t act, int32_t rms, int32_t precision, float clamp_min, float threshold,
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
     const void* w1_packed,
@@ -259,14 +271,16 @@ int wgkv_gate_scores(
  * one-time layout of GatingPredictor's conv1.weight and norm weights,
  * src/modeling_layers.py:134-161, for the bf16 matrix-core path above).
  * wgkv_gate_packed_bytes: size for in_features = n_in * head_dim (a multiple
- * of 32) and inner (a multiple of 16), or -1.  wgkv_gate_pack_weights writes
- * w_norm_i[d] * w1[h*inner + j][i*D + d] (norm weights only with rms != 0)
- * as three bf16 planes hi + mid + lo; inputs_mask and rms as for
- * wgkv_gate_scores.  Repack after the weights change. */
-int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, int32_t in_features);
+ * of 32) and inner (a multiple of 16), or -1.  wgkv_gate_pack_weights writes,
+ * for precision 0, w_norm_i[d] * w1[h*inner + j][i*D + d] (norm weights only
+ * with rms != 0) as three bf16 planes hi + mid + lo; for precision 1 / 2,
+ * w1 as one bf16 plane (its values are bf16; the norm weights are applied
+ * to the inputs).  inputs_mask, rms and precision as for wgkv_gate_scores.
+ * Repack after the weights change. */
+int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, int32_t in_features, int32_t precision);
 int wgkv_gate_pack_weights(
     const float* w_pre, const float* w_post, const float* w_v, int32_t inputs_mask, int32_t rms,
-    const float* w1, int32_t num_kv_heads, int32_t head_dim, int32_t inner,
+    const float* w1, int32_t num_kv_heads, int32_t head_dim, int32_t inner, int32_t precision,
     void* packed, int64_t packed_bytes, void* stream);
 
 /* ------------------------------------------------------------------------

@@ -19,8 +19,10 @@ Parameter names and shapes are the reference's state-dict keys:
 ``conv1.bias (Hkv*inner)``, ``conv2.weight (Hkv, inner, 1)``,
 ``conv2.bias (Hkv)`` with ``inner = int(D * g_expand)``.
 
-The build's scores are float32 computed from float32 copies of the inputs and
-weights; the reference runs the same graph in the model dtype.
+``gate_scores`` is the graph with float32 parameters (float32 arithmetic after
+the bf16 cast of the normalised inputs); ``gate_scores_bf16`` is the graph
+with bf16 parameters, the reference's inference configuration, with each
+op's bf16 rounding.
 """
 import math
 
@@ -64,6 +66,81 @@ def gate_scores(pre_key, post_key, value, params, g_inputs=("pre_k", "post_k"),
     if not fast_path:
         g = torch.clamp(g, min=g_epsilon)
     return g
+
+
+def _rb(x):
+    """Round-to-nearest-even to bf16, kept in the container's dtype."""
+    return x.to(torch.bfloat16).to(x.dtype)
+
+
+def gate_scores_bf16(pre_key, post_key, value, params, g_inputs=("pre_k", "post_k"),
+                     g_act_fn="gelu", fast_path=True, g_epsilon=1e-3, return_logit=False):
+    """The reference's gate as its inference runs it: bf16 parameters (the
+    model loads the gate checkpoint in bf16, scripts/profiling.py:222-226)
+    on bf16 inputs.  Every op returns bf16, so its value is rounded once per
+    op; products are accumulated here in float64 (the value an exactly
+    summed float32 accumulation would round):
+
+        x  = bf16(w_norm * bf16(rms(k)))                       (:124-128)
+        fast path (:186-195): h = bf16(bf16(W1 x) + b1), a = bf16(act(h)),
+                              y = bf16(bf16(w2 . a) + b2)
+        conv path (:197-205): h = bf16(W1 x + b1), a = bf16(act(h)),
+                              y = bf16(w2 . a + b2)
+        g = bf16(sigmoid(y)); conv path: g = max(g, bf16(g_epsilon))
+
+    The einsum / Conv1d rounding points were read off torch's CPU results
+    (an einsum output is rounded before a separate bias add; a Conv1d adds
+    its bias before its single rounding).  Inputs (B,H,S,D) bf16; returns
+    float64 scores holding bf16 values (and, with return_logit, the bf16
+    pre-sigmoid y as well)."""
+    B, H, S, D = post_key.shape
+    f64 = torch.float64
+
+    def norm(x, w):
+        xf = x.to(torch.float32)
+        var = xf.pow(2).mean(-1, keepdim=True)
+        y = (xf * torch.rsqrt(var + RMS_EPS)).to(torch.bfloat16).to(f64)
+        return _rb(w.to(torch.bfloat16).to(f64) * y)
+
+    states = []
+    names = {"pre_k": (pre_key, "pre_key_norm.weight"), "post_k": (post_key, "post_key_norm.weight"),
+             "v": (value, "value_norm.weight")}
+    for name in ("pre_k", "post_k", "v"):
+        if name in g_inputs:
+            t, wname = names[name]
+            states.append(norm(t, params[wname]) if wname in params else t.to(f64))
+    x = torch.cat(states, dim=-1)
+    n_in = x.shape[-1]
+    p16 = {k: v.to(torch.bfloat16).to(f64) for k, v in params.items()}
+    w1 = p16["conv1.weight"].reshape(H, -1, n_in)
+    b1 = p16["conv1.bias"].reshape(1, H, 1, -1)
+    acc = torch.einsum("bhli,hji->bhlj", x, w1)
+    hdn = _rb(_rb(acc) + b1) if fast_path else _rb(acc + b1)
+    hf = hdn.to(torch.float32)
+    act = torch.nn.functional.silu(hf) if g_act_fn == "silu" else torch.nn.functional.gelu(hf)
+    a = _rb(act.to(f64))
+    w2 = p16["conv2.weight"].reshape(H, 1, -1)
+    b2 = p16["conv2.bias"].reshape(1, H, 1, 1)
+    acc2 = torch.einsum("bhlj,hoj->bhlo", a, w2)
+    y = _rb(_rb(acc2) + b2) if fast_path else _rb(acc2 + b2)
+    y = y.squeeze(-1)
+    g = sigmoid_bf16(y, None if fast_path else g_epsilon)
+    return (g, y) if return_logit else g
+
+
+def sigmoid_bf16(y, clamp=None):
+    """bf16(sigmoid(y)) evaluated in float32 (then max with bf16(clamp))."""
+    g = _rb(torch.sigmoid(y.to(torch.float32)).to(torch.float64))
+    if clamp is not None:
+        g = torch.clamp(g, min=float(torch.tensor(clamp).to(torch.bfloat16)))
+    return g
+
+
+def bf16_threshold(threshold):
+    """The threshold a bf16 score tensor is compared with: ``g > tau`` with a
+    Python float promotes to the tensor's dtype, so tau is rounded to bf16
+    (0.1 -> 0.10009765625)."""
+    return float(torch.tensor(threshold).to(torch.bfloat16))
 
 
 def bf16_midpoint_distance(y):

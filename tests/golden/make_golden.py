@@ -1,12 +1,14 @@
 """Write golden vectors with the reference's own implementation.
 
 Run once in the development container (the only place the reference
-checkout exists):  ``python tests/golden/make_golden.py /path/to/WG-KV``.
+checkout exists):  ``python tests/golden/make_golden.py /path/to/WG-KV
+[gate|gate_bf16|cache|quest|snapkv ...]`` (all when none is named).
 
 Only functions that no closed form or reference test pins are run here:
 
 * ``GatingPredictor.forward`` (src/modeling_layers.py:134-205), fast and conv
-  paths -- float32 scores;
+  paths -- float32 scores, and the same module converted to bf16 on bf16
+  inputs (the inference scripts' configuration) -- bf16 scores;
 * the dual-cache state machine through ``self_attn_forward_patch_inference``
   (:1452-1509) -> ``prefill_wrapper`` (:1183-1376), ``decode_wrapper``
   (:1379-1449), ``migrate_local_kv_to_global`` (:674-763),
@@ -41,8 +43,8 @@ def load_reference(root):
     return mod
 
 
-def make_gate(ref, H, D, g_expand, params, fast_path):
-    g = ref.GatingPredictor(D, H, ["pre_k", "post_k"], "gelu", g_expand, 1e-3, True, fast_path)
+def make_gate(ref, H, D, g_expand, params, fast_path, g_inputs=("pre_k", "post_k"), act="gelu"):
+    g = ref.GatingPredictor(D, H, list(g_inputs), act, g_expand, 1e-3, True, fast_path)
     sd = {k: v.clone() for k, v in params.items()}
     g.load_state_dict(sd, strict=True)
     return g.eval()
@@ -61,6 +63,26 @@ def gate_golden(ref):
             scenarios.checksum(pre_k, post_k, *params.values()).encode(), dtype=np.uint8)
     np.savez_compressed(os.path.join(HERE, "gate_golden.npz"), **out)
     print("gate:", {k: v.shape for k, v in out.items() if not k.endswith("sha256")})
+
+
+def gate_bf16_golden(ref):
+    """The reference's GatingPredictor converted to bf16 (as its inference
+    scripts load the gate checkpoint) on bf16 inputs: bf16 scores, stored as
+    their int16 bit patterns."""
+    out = {}
+    for name, sc in scenarios.GATE_BF16_SCENARIOS.items():
+        params, pre_k, post_k, value = scenarios.gate_inputs_bf16(sc)
+        for fast in (True, False):
+            g = make_gate(ref, sc["H"], sc["D"], sc["g_expand"], {k: v.float() for k, v in params.items()},
+                          fast, sc["g_inputs"], sc["act"]).to(torch.bfloat16)
+            with torch.no_grad():
+                s = g(pre_k, post_k, value)
+            assert s.dtype == torch.bfloat16
+            out[f"{name}.{'fast' if fast else 'conv'}"] = s.view(torch.int16).numpy()
+        out[f"{name}.inputs_sha256"] = np.frombuffer(
+            scenarios.checksum(pre_k, post_k, value, *params.values()).encode(), dtype=np.uint8)
+    np.savez_compressed(os.path.join(HERE, "gate_bf16_golden.npz"), **out)
+    print("gate bf16:", {k: v.shape for k, v in out.items() if not k.endswith("sha256")})
 
 
 def fake_attention_module(ref, sc, layer_idx, record, gate):
@@ -171,8 +193,13 @@ def main():
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     ref = load_reference(root)
     torch.set_num_threads(4)
-    gate_golden(ref)
-    cache_golden(ref)
+    only = sys.argv[2:] or ["gate", "gate_bf16", "cache"]
+    if "gate" in only:
+        gate_golden(ref)
+    if "gate_bf16" in only:
+        gate_bf16_golden(ref)
+    if "cache" in only:
+        cache_golden(ref)
 
 
 if __name__ == "__main__":

@@ -30,6 +30,16 @@ GATE_SCENARIOS = {
     "qwen3_like": dict(H=2, D=128, g_expand=1.5, S=96, seed=11),
 }
 
+# The gate with bf16 parameters on bf16 inputs (the reference's inference
+# configuration).  conv2.bias is shifted by logit(0.1) so that the scores sit
+# around the threshold and admission is decided at every bf16 step near it.
+GATE_BF16_SCENARIOS = {
+    "llama8b": dict(H=2, D=128, g_expand=4.0, S=2048, seed=20, g_inputs=("pre_k", "post_k"), act="gelu"),
+    "qwen3": dict(H=2, D=128, g_expand=1.5, S=1024, seed=21, g_inputs=("pre_k", "post_k"), act="gelu"),
+    "d64_kv_silu": dict(H=2, D=64, g_expand=4.0, S=1024, seed=22, g_inputs=("pre_k", "post_k", "v"), act="silu"),
+    "decode": dict(H=8, D=128, g_expand=4.0, S=3, seed=23, g_inputs=("pre_k", "post_k"), act="gelu"),
+}
+
 
 def checksum(*tensors):
     h = hashlib.sha256()
@@ -64,6 +74,25 @@ def gate_inputs(sc):
     pre_k = torch.randn(1, H, S, D, generator=gen)
     post_k = torch.randn(1, H, S, D, generator=gen)
     value = torch.randn(1, H, S, D, generator=gen)
+    return params, pre_k, post_k, value
+
+
+def gate_inputs_bf16(sc):
+    """bf16 parameters (the fp32 draw of gate_params, rounded, conv2.bias
+    shifted by logit(0.1)) and bf16 (1, H, S, D) inputs."""
+    gen = torch.Generator().manual_seed(sc["seed"])
+    H, D, S = sc["H"], sc["D"], sc["S"]
+    params = gate_params(H, D, sc["g_expand"], gen)
+    if len(sc["g_inputs"]) == 3:
+        inner = int(D * sc["g_expand"])
+        b1 = 1.0 / np.sqrt(3 * D)
+        params["value_norm.weight"] = 1.0 + 0.1 * torch.randn(D, generator=gen)
+        params["conv1.weight"] = (torch.rand(H * inner, 3 * D, 1, generator=gen) * 2 - 1) * b1
+    params["conv2.bias"] = params["conv2.bias"] - 2.1972245773362196
+    params = {k: v.to(torch.bfloat16) for k, v in params.items()}
+    pre_k = torch.randn(1, H, S, D, generator=gen).to(torch.bfloat16)
+    post_k = torch.randn(1, H, S, D, generator=gen).to(torch.bfloat16)
+    value = torch.randn(1, H, S, D, generator=gen).to(torch.bfloat16)
     return params, pre_k, post_k, value
 
 

@@ -46,6 +46,33 @@ def test_gate_oracle_matches_reference(gate_gold, name):
     assert np.array_equal((fast.numpy() > 0.1)[far], (ref > 0.1)[far])
 
 
+@pytest.mark.parametrize("name", list(scenarios.GATE_BF16_SCENARIOS))
+def test_bf16_gate_oracle_matches_reference_bit_for_bit(name):
+    """oracle.gate.gate_scores_bf16 (the rounding points of the reference's
+    module in bf16) reproduces every bf16 score the reference wrote, on the
+    fast and the Conv1d path; the golden admission is score > bf16(0.1)."""
+    z = np.load(os.path.join(GOLD, "gate_bf16_golden.npz"))
+    sc = scenarios.GATE_BF16_SCENARIOS[name]
+    params, pre_k, post_k, value = scenarios.gate_inputs_bf16(sc)
+    assert bytes(z[f"{name}.inputs_sha256"]).decode() == scenarios.checksum(pre_k, post_k, value, *params.values())
+    for fast in (True, False):
+        gold = torch.from_numpy(z[f"{name}.{'fast' if fast else 'conv'}"]).view(torch.bfloat16).double()
+        got = gate.gate_scores_bf16(pre_k, post_k, value, params, g_inputs=sc["g_inputs"], g_act_fn=sc["act"],
+                                    fast_path=fast)
+        assert torch.equal(got, gold), (name, fast)
+        # the fp32-parameter graph differs: bf16 rounding moves scores by more than float32 noise
+        if sc["S"] > 4:
+            f32 = gate.gate_scores(pre_k, post_k, value, {k: v.float() for k, v in params.items()},
+                                   g_inputs=sc["g_inputs"], g_act_fn=sc["act"], fast_path=fast).double()
+            assert (f32 - gold).abs().max().item() > 1e-4
+
+
+def test_bf16_threshold_rounds_like_torch():
+    assert gate.bf16_threshold(0.1) == 0.10009765625
+    x = torch.tensor([0.10009765625, 0.1005859375], dtype=torch.bfloat16)
+    assert (x > 0.1).tolist() == [x[i].item() > gate.bf16_threshold(0.1) for i in range(2)] == [False, True]
+
+
 def test_gate_oracle_matches_float64_loop():
     sc = dict(scenarios.GATE_SCENARIOS["llama_cfg1"], S=6)
     params, pre_k, post_k, value = scenarios.gate_inputs(sc)

@@ -6,6 +6,13 @@
 //   h  = act(W1[h] x + b1[h])                                        (inner)
 //   g  = sigmoid(w2[h] . h + b2[h]);  conv path: g = max(g, clamp_min)
 //   mask = g > threshold
+// Two arithmetics (GateArgs::prec): fp32 parameters (fp32 from the normalised
+// inputs on, as the reference with fp32 gate weights), or bf16 parameters
+// (the reference's inference: the gate checkpoint loads in bf16) where every
+// op's result is rounded to bf16 -- the norm product, the first layer's
+// output (fast path: einsum output, then the bias add; conv path: one
+// rounding after the bias), the activation, the second layer likewise, the
+// sigmoid -- and the score is compared with bf16(threshold).
 // One workgroup = 64 tokens of one (batch, KV head), heads dealt across the
 // XCDs so each head's W1 stays in one L2.  The normalised inputs
 // go to LDS (fp32, rows padded for conflict-free 16-byte reads); the hidden
@@ -13,6 +20,8 @@
 // is read once per workgroup; x @ W1^T runs on v_mfma_f32_16x16x4f32 with
 // each lane feeding four consecutive k from one 16-byte load; the epilogue
 // applies bias, activation and w2 and reduces over columns in registers.
+#include <string.h>
+
 #include "wgkv_common.h"
 
 namespace {
@@ -30,6 +39,7 @@ struct GateArgs {
   const float* w2;
   const float* b2;
   int B, H, S, D, inner, act;
+  int prec;  // 0 fp32 parameters, 1 bf16 parameters (fast path), 2 bf16 parameters (conv path)
   float clamp_min, threshold;
   float* scores;
   int64_t sc_sb, sc_sh;
@@ -64,6 +74,32 @@ __device__ __forceinline__ float round_bf16(float x) {
 __device__ __forceinline__ float gelu_erf(float z) { return 0.5f * z * (1.0f + erff(z * 0.70710678118654752f)); }
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }
 
+// Layer output from the fp32 accumulation and the bias, at the rounding
+// points of the arithmetic prec (0: none; 1: einsum output, then the bias
+// add; 2: one rounding after the bias).
+__device__ __forceinline__ float layer_out(float acc, float bias, int prec) {
+  if (prec == 1) return round_bf16(round_bf16(acc) + bias);
+  if (prec == 2) return round_bf16(acc + bias);
+  return acc + bias;
+}
+
+__device__ __forceinline__ float activation(float z, int act, int prec) {
+  const float r = act ? silu(z) : gelu_erf(z);
+  return prec ? round_bf16(r) : r;
+}
+
+// Normalised input element y times its norm weight (rounded with bf16 parameters).
+__device__ __forceinline__ float norm_out(float w, float y, int prec) { return prec ? round_bf16(w * y) : w * y; }
+
+// Score and admission flag from the second layer's fp32 sum z (before b2).
+__device__ __forceinline__ float score_of(const GateArgs& a, float z, float b2) {
+  z = layer_out(z, b2, a.prec);
+  float g = 1.0f / (1.0f + expf(-z));
+  if (a.prec) g = round_bf16(g);
+  if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+  return g;
+}
+
 // End of a 64-token tile: lane (n, kq) holds partial logits of tokens
 // mt*16 + 4*kq + i over its columns; sum over the 16 lanes of each row, then
 // over the 4 waves, and apply b2, sigmoid, clamp and threshold.
@@ -82,9 +118,7 @@ __device__ __forceinline__ void finish_tile(const GateArgs& a, const float (&log
     const int m = threadIdx.x;
     const int s = s0 + m;
     if (s < a.S) {
-      const float z = ((s_part[0][m] + s_part[1][m]) + (s_part[2][m] + s_part[3][m])) + a.b2[h];
-      float g = 1.0f / (1.0f + expf(-z));
-      if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+      const float g = score_of(a, (s_part[0][m] + s_part[1][m]) + (s_part[2][m] + s_part[3][m]), a.b2[h]);
       if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
       if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
     }
@@ -142,7 +176,7 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
           if (d < D) {
             float y = a.rms ? v[u][i][e] * scale : v[u][i][e];
             if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
-            xs[m * LDX + i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+            xs[m * LDX + i * D + d] = a.rms ? norm_out(a.w_norm[i][d], y, a.prec) : y;
           }
         }
       }
@@ -205,8 +239,8 @@ __global__ __launch_bounds__(kThreads) void gate_kernel(GateArgs a) {
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float z = c[mt][j][i] + bias;
-          logit[mt][i] = fmaf(wo, a.act ? silu(z) : gelu_erf(z), logit[mt][i]);
+          const float z = layer_out(c[mt][j][i], bias, a.prec);
+          logit[mt][i] = fmaf(wo, activation(z, a.act, a.prec), logit[mt][i]);
         }
     }
   }
@@ -264,9 +298,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
   const int D = a.D;
   // sigmoid, clamp, threshold and the stores of token s's logit z (before b2)
   auto finish = [&](int s, float z) {
-    z += a.b2[h];
-    float g = 1.0f / (1.0f + expf(-z));
-    if (a.clamp_min > 0.f) g = fmaxf(g, a.clamp_min);
+    const float g = score_of(a, z, a.b2[h]);
     if (a.scores) a.scores[(int64_t)b * a.sc_sb + (int64_t)h * a.sc_sh + s] = g;
     if (a.mask) a.mask[(int64_t)b * a.mk_sb + (int64_t)h * a.mk_sh + s] = g > a.threshold ? 1 : 0;
   };
@@ -313,7 +345,7 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
         if (d < D) {
           float y = a.rms ? v[i][e] * scale : v[i][e];
           if (a.rms && !a.in_f32) y = round_bf16(y);  // cast back to the input dtype (:128)
-          xs[s][i * D + d] = a.rms ? a.w_norm[i][d] * y : y;
+          xs[s][i * D + d] = a.rms ? norm_out(a.w_norm[i][d], y, a.prec) : y;
         }
       }
     }
@@ -358,8 +390,8 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
 #pragma unroll
     for (int t = 0; t < kSmallTok; ++t) {
       if (t >= nt) break;
-      const float z = reduce16_columns(dot[t], lane) + bias;
-      const float y = wo * (a.act ? silu(z) : gelu_erf(z));  // one activation per lane
+      const float z = layer_out(reduce16_columns(dot[t], lane), bias, a.prec);
+      const float y = wo * activation(z, a.act, a.prec);  // one activation per lane
       logit[t] += (lane & 3) == 0 ? y : 0.f;
     }
   }
@@ -412,13 +444,19 @@ __global__ __launch_bounds__(64 * kSmallWaves) void gate_small_kernel(GateArgs a
 // fp32 and the matrix core accumulates the three products in fp32, so the
 // layer costs three bf16 MFMAs where fp32 MFMAs would take eight times the
 // cycles of one.
+// With bf16 parameters W1 is itself bf16 and the norm product is rounded on
+// its own, so the packing is one plane holding W1 and the norm weight is
+// applied to the inputs.
 // Packed layout, bf16: [head][16-column tile][32-input k-step][plane][lane][8]
 // -- the B operand of v_mfma_f32_16x16x32_bf16, lane kg*16 + n holding
 // column n and inputs 8*kg .. 8*kg+7 -- so one wave load reads 1 KB.
 constexpr int kPlanes = 3;
 
+__host__ __device__ constexpr int planes_of(int prec) { return prec ? 1 : kPlanes; }
+
 __global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0, const float* wn1,
-                                 const float* wn2, int H, int inner, int D, int n_in, u32x4_t* __restrict__ packed) {
+                                 const float* wn2, int H, int inner, int D, int n_in, int np,
+                                 u32x4_t* __restrict__ packed) {
   const int K = n_in * D, NT = inner / 16, KS = K / 32;
   const int64_t total = (int64_t)H * NT * KS * 64;
   for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total; id += (int64_t)gridDim.x * blockDim.x) {
@@ -436,7 +474,7 @@ __global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0,
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int k = k0 + e + u, i = k / D, d = k - i * D;
-        const float* wn = i == 0 ? wn0 : i == 1 ? wn1 : wn2;
+        const float* wn = np == 1 ? nullptr : i == 0 ? wn0 : i == 1 ? wn1 : wn2;
         const float f = w1[((int64_t)h * inner + col) * K + k] * (wn ? wn[d] : 1.f);
         const uint16_t hi = f32_to_bf16(f);
         const float r1 = f - bf16lo(hi);
@@ -449,9 +487,8 @@ __global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0,
 #pragma unroll
       for (int p = 0; p < kPlanes; ++p) w[p][e / 2] = (uint32_t)pl[p][0] | ((uint32_t)pl[p][1] << 16);
     }
-    u32x4_t* dst = packed + (((int64_t)(h * NT + nt) * KS + ks) * kPlanes) * 64 + lane;
-#pragma unroll
-    for (int p = 0; p < kPlanes; ++p) dst[p * 64] = (u32x4_t){w[p][0], w[p][1], w[p][2], w[p][3]};
+    u32x4_t* dst = packed + (((int64_t)(h * NT + nt) * KS + ks) * np) * 64 + lane;
+    for (int p = 0; p < np; ++p) dst[p * 64] = (u32x4_t){w[p][0], w[p][1], w[p][2], w[p][3]};
   }
 }
 
@@ -463,9 +500,11 @@ __global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0,
 // four; per 32-input k-step it reads the four 64-token A fragments from LDS
 // and the 4 x 3 packed B fragments of the next k-step from global memory.
 // Two waves per SIMD (two workgroups per CU) hide each other's loads and
-// GELU epilogues.
-template <int D, int NIN>
+// GELU epilogues.  PREC is GateArgs::prec (three planes for fp32 parameters,
+// one for bf16 parameters).
+template <int D, int NIN, int PREC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_bf16_kernel(GateArgs a, const u32x4_t* __restrict__ packed) {
+  constexpr int NP = planes_of(PREC);
   constexpr int K = NIN * D;
   constexpr int KS = K / 32;
   constexpr int LDY = K + 8;     // LDS row stride (bf16)
@@ -516,6 +555,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           const float scale = 1.0f / sqrtf(ss / (float)D + 1e-6f);
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(f[2 * e] * scale, f[2 * e + 1] * scale);  // cast back to bf16 (:128)
+          if (PREC) {  // times the bf16 norm weight, rounded (:128)
+            const f32x4_t w0 = *(const f32x4_t*)(a.w_norm[i] + c * 8);
+            const f32x4_t w1v = *(const f32x4_t*)(a.w_norm[i] + c * 8 + 4);
+            const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1v[0], w1v[1], w1v[2], w1v[3]};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(wv[2 * e] * bf16lo(y[e]), wv[2 * e + 1] * bf16hi(y[e]));
+          }
         }
         const int m = wid * 16 + u * RPL + lane / LPR;
         *(u32x4_t*)(&ys[m * LDY + i * D + c * 8]) = y;
@@ -526,7 +572,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   // ---- y @ (w_norm * W1[h])^T: three bf16 MFMAs per k-step and tile pair --
   const int n = lane & 15, kg = lane >> 4;
   const int ntot = a.inner / 16;
-  const u32x4_t* ph = packed + (int64_t)h * ntot * KS * kPlanes * 64 + lane;
+  const u32x4_t* ph = packed + (int64_t)h * ntot * KS * NP * 64 + lane;
   const float* b1h = a.b1 + (int64_t)h * a.inner;
   const float* w2h = a.w2 + (int64_t)h * a.inner;
   float logit[4][4];
@@ -543,25 +589,25 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) c[mt][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    u32x4_t bw[4][kPlanes];
+    u32x4_t bw[4][NP];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
-      for (int p = 0; p < kPlanes; ++p) bw[j][p] = ph[((int64_t)tj[j] * KS * kPlanes + p) * 64];
+      for (int p = 0; p < NP; ++p) bw[j][p] = ph[((int64_t)tj[j] * KS * NP + p) * 64];
 #pragma unroll 2
     for (int ks = 0; ks < KS; ++ks) {
-      u32x4_t bn[4][kPlanes];
+      u32x4_t bn[4][NP];
       if (ks + 1 < KS)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int p = 0; p < kPlanes; ++p) bn[j][p] = ph[(((int64_t)tj[j] * KS + ks + 1) * kPlanes + p) * 64];
+          for (int p = 0; p < NP; ++p) bn[j][p] = ph[(((int64_t)tj[j] * KS + ks + 1) * NP + p) * 64];
       bf16x8_t ax[4];
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
         ax[mt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&ys[(mt * 16 + n) * LDY + ks * 32 + kg * 8]));
 #pragma unroll
-      for (int p = kPlanes - 1; p >= 0; --p)  // smallest plane first
+      for (int p = NP - 1; p >= 0; --p)  // smallest plane first
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -571,7 +617,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-          for (int p = 0; p < kPlanes; ++p) bw[j][p] = bn[j][p];
+          for (int p = 0; p < NP; ++p) bw[j][p] = bn[j][p];
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -582,8 +628,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float z = c[mt][j][i] + bias;
-          logit[mt][i] = fmaf(wo, a.act ? silu(z) : gelu_erf(z), logit[mt][i]);
+          const float z = layer_out(c[mt][j][i], bias, PREC);
+          logit[mt][i] = fmaf(wo, activation(z, a.act, PREC), logit[mt][i]);
         }
     }
   }
@@ -603,6 +649,16 @@ void launch_gate(const GateArgs& a, hipStream_t st) {
 
 namespace {
 int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+// Round-to-nearest-even f32 -> bf16 -> f32 on the host (finite values).
+float host_round_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return f;
+}
 }  // namespace
 
 extern "C" int64_t wgkv_gate_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t inner) {
@@ -619,7 +675,7 @@ extern "C" int wgkv_gate_scores(
     const float* w_pre, const float* w_post, const float* w_v,
     const float* w1, const float* b1, const float* w2, const float* b2,
     int32_t batch, int32_t num_kv_heads, int32_t seq_len, int32_t head_dim, int32_t inner,
-    int32_t act, int32_t rms, float clamp_min, float threshold,
+    int32_t act, int32_t rms, int32_t precision, float clamp_min, float threshold,
     float* scores, int64_t sc_sb, int64_t sc_sh,
     uint8_t* mask, int64_t mk_sb, int64_t mk_sh,
     const void* w1_packed,
@@ -631,6 +687,8 @@ extern "C" int wgkv_gate_scores(
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
   if (inner <= 0 || inner % 16) return WGKV_ERR_UNSUPPORTED;  // 16-column tiles
   if (in_dtype != 0 && in_dtype != 1) return WGKV_ERR_UNSUPPORTED;
+  if (precision < 0 || precision > 2) return WGKV_ERR_ARG;
+  if (precision && in_dtype != 0) return WGKV_ERR_UNSUPPORTED;  // bf16 parameters take bf16 inputs
   GateArgs a = {};
   const void* srcs[3] = {pre_key, post_key, value};
   const float* wn[3] = {w_pre, w_post, w_v};
@@ -660,8 +718,11 @@ extern "C" int wgkv_gate_scores(
   a.D = head_dim;
   a.inner = inner;
   a.act = act;
-  a.clamp_min = clamp_min;
-  a.threshold = threshold;
+  a.prec = precision;
+  // bf16 scores are compared with (and clamped to) the bf16 value of the
+  // Python float, as a bf16 tensor compared with a scalar is
+  a.clamp_min = precision ? host_round_bf16(clamp_min) : clamp_min;
+  a.threshold = precision ? host_round_bf16(threshold) : threshold;
   a.scores = scores;
   a.sc_sb = sc_sb;
   a.sc_sh = sc_sh;
@@ -684,12 +745,19 @@ extern "C" int wgkv_gate_scores(
   if (w1_packed && in_dtype == 0 && seq_len > kSmallTok) {
     // the packed path reads 16-byte input slices
     bool aligned = ((uintptr_t)w1_packed & 15) == 0;
-    for (int i = 0; i < n_in; ++i)
+    for (int i = 0; i < n_in; ++i) {
       aligned = aligned && ((uintptr_t)a.in[i] & 15) == 0 && ((a.sb[i] | a.sh[i] | a.ss[i]) & 7) == 0;
+      if (precision && rms) aligned = aligned && ((uintptr_t)a.w_norm[i] & 15) == 0;  // 16-byte norm-weight loads
+    }
     if (aligned) {
       const u32x4_t* pk = (const u32x4_t*)w1_packed;
       const dim3 grid((seq_len + kTok - 1) / kTok, batch * num_kv_heads);
-#define WGKV_GATE_BF16(DD, NN) hipLaunchKernelGGL((gate_bf16_kernel<DD, NN>), grid, dim3(kThreads), 0, st, a, pk)
+#define WGKV_GATE_BF16(DD, NN)                                                                              \
+  do {                                                                                                      \
+    if (precision == 0) hipLaunchKernelGGL((gate_bf16_kernel<DD, NN, 0>), grid, dim3(kThreads), 0, st, a, pk); \
+    else if (precision == 1) hipLaunchKernelGGL((gate_bf16_kernel<DD, NN, 1>), grid, dim3(kThreads), 0, st, a, pk); \
+    else hipLaunchKernelGGL((gate_bf16_kernel<DD, NN, 2>), grid, dim3(kThreads), 0, st, a, pk);             \
+  } while (0)
       if (head_dim == 128) {
         if (n_in == 1) WGKV_GATE_BF16(128, 1);
         else if (n_in == 2) WGKV_GATE_BF16(128, 2);
@@ -714,16 +782,19 @@ extern "C" int wgkv_gate_scores(
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, int32_t in_features) {
+extern "C" int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, int32_t in_features,
+                                          int32_t precision) {
   if (num_kv_heads <= 0 || inner <= 0 || inner % 16 || in_features <= 0 || in_features % 32) return -1;
-  return (int64_t)num_kv_heads * inner * in_features * kPlanes * 2;
+  if (precision < 0 || precision > 2) return -1;
+  return (int64_t)num_kv_heads * inner * in_features * planes_of(precision) * 2;
 }
 
 extern "C" int wgkv_gate_pack_weights(
     const float* w_pre, const float* w_post, const float* w_v, int32_t inputs_mask, int32_t rms,
-    const float* w1, int32_t num_kv_heads, int32_t head_dim, int32_t inner,
+    const float* w1, int32_t num_kv_heads, int32_t head_dim, int32_t inner, int32_t precision,
     void* packed, int64_t packed_bytes, void* stream) {
   if (!w1 || !packed || num_kv_heads <= 0) return WGKV_ERR_ARG;
+  if (precision < 0 || precision > 2) return WGKV_ERR_ARG;
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
   if (inner <= 0 || inner % 16) return WGKV_ERR_UNSUPPORTED;
   const float* wn_all[3] = {w_pre, w_post, w_v};
@@ -735,11 +806,11 @@ extern "C" int wgkv_gate_pack_weights(
     wn[n_in++] = rms ? wn_all[i] : nullptr;
   }
   if (n_in == 0) return WGKV_ERR_ARG;
-  if (packed_bytes < wgkv_gate_packed_bytes(num_kv_heads, inner, n_in * head_dim)) return WGKV_ERR_ARG;
+  if (packed_bytes < wgkv_gate_packed_bytes(num_kv_heads, inner, n_in * head_dim, precision)) return WGKV_ERR_ARG;
   if (((uintptr_t)packed & 15) != 0) return WGKV_ERR_UNSUPPORTED;
   const int64_t total = (int64_t)num_kv_heads * (inner / 16) * (n_in * head_dim / 32) * 64;
   const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
   hipLaunchKernelGGL(gate_pack_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, w1, wn[0], wn[1], wn[2],
-                     num_kv_heads, inner, head_dim, n_in, (u32x4_t*)packed);
+                     num_kv_heads, inner, head_dim, n_in, planes_of(precision), (u32x4_t*)packed);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

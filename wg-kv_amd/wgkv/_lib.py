@@ -100,7 +100,7 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr, c_ptr,
         c_i32, c_i32, c_i32, c_i32, c_i32,
-        c_i32, c_i32, c_f32, c_f32,
+        c_i32, c_i32, c_i32, c_f32, c_f32,
         c_ptr, c_i64, c_i64,
         c_ptr, c_i64, c_i64,
         c_ptr,
@@ -108,9 +108,9 @@ SIGNATURES = {
         c_ptr, c_i64,
         c_ptr]),
     "wgkv_gate_workspace_bytes": (ctypes.c_int64, [c_i32, c_i32, c_i32]),
-    "wgkv_gate_packed_bytes": (ctypes.c_int64, [c_i32, c_i32, c_i32]),
+    "wgkv_gate_packed_bytes": (ctypes.c_int64, [c_i32, c_i32, c_i32, c_i32]),
     "wgkv_gate_pack_weights": (ctypes.c_int, [c_ptr, c_ptr, c_ptr, c_i32, c_i32, c_ptr, c_i32, c_i32, c_i32,
-                                              c_ptr, c_i64, c_ptr]),
+                                              c_i32, c_ptr, c_i64, c_ptr]),
     "wgkv_rms_norm": (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_ptr, c_i64,
                                      c_i32, c_i32, c_f32, c_ptr]),
     "wgkv_rope_qkv": (ctypes.c_int, [c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_i64, c_i64,

@@ -4,11 +4,17 @@ Parameter names and shapes are GatingPredictor's (src/modeling_layers.py:
 134-161), so gate checkpoints (keys ``...g_predictors.pre_key_norm.weight``,
 ``.post_key_norm.weight``, ``.conv1.{weight,bias}``, ``.conv2.{weight,bias}``)
 load with ``load_state_dict``.  The forward runs the HIP kernel
-``wgkv_gate_scores`` (fp32 arithmetic, fp32 scores); bf16 parameters are
-widened to fp32 copies before the call.  For bf16 inputs of more than four
-tokens the first layer runs on the bf16 matrix core from a packed copy of
-conv1.weight with the norm weights folded in (three bf16 planes that carry
-the fp32 product exactly), made once per device and weight version.
+``wgkv_gate_scores`` in the arithmetic the parameters' dtype gives the
+reference's module: fp32 parameters compute in fp32 (fp32 scores); bf16
+parameters on bf16 inputs -- the reference's inference, whose scripts load
+the gate checkpoint in bf16 -- round every op's result to bf16 at the points
+torch does and compare the bf16 score with bf16(g_threshold) (precision
+1 = g_fast_path, 2 = the Conv1d path).  Parameters reach the kernel as fp32
+copies (exact for bf16 values).  For bf16 inputs of more than four tokens
+the first layer runs on the bf16 matrix core from a packed copy of
+conv1.weight (fp32 parameters: the norm weights folded in, as three bf16
+planes that carry the fp32 product exactly; bf16 parameters: one plane),
+made once per device, weight version and precision.
 """
 import torch
 import torch.nn as nn
@@ -77,19 +83,27 @@ class GatingPredictor(nn.Module):
         norms = [self.pre_key_norm, self.post_key_norm, self.value_norm]
         return [self._f32(m.weight) if isinstance(m, GatingRMSNorm) else None for m in norms]
 
-    def packed_weights(self):
+    def precision(self, input_dtype):
+        """wgkv_gate_scores' arithmetic for inputs of ``input_dtype``: 0 with
+        fp32 parameters (or fp32 inputs), 1 / 2 with bf16 parameters on bf16
+        inputs (fast path / Conv1d path)."""
+        if input_dtype == torch.bfloat16 and self.conv1.weight.dtype == torch.bfloat16:
+            return 1 if self.g_fast_path else 2
+        return 0
+
+    def packed_weights(self, precision=0):
         """Packed first-layer weights (wgkv_gate_pack_weights) for the bf16
-        matrix-core path, cached per device and remade when conv1.weight or a
-        norm weight changes version."""
+        matrix-core path, cached per device and precision and remade when
+        conv1.weight or a norm weight changes version."""
         params = [self.conv1.weight] + [m.weight for m in (self.pre_key_norm, self.post_key_norm, self.value_norm)
                                         if isinstance(m, GatingRMSNorm)]
-        key = (self.conv1.weight.device, tuple((p.data_ptr(), p._version) for p in params))
+        key = (self.conv1.weight.device, precision, tuple((p.data_ptr(), p._version) for p in params))
         hit = self.__dict__.get("_packed_cache")
         if hit is not None and hit[0] == key:
             return hit[1]
         wn = self._norm_weights()
         packed = pack_weights(wn[0], wn[1], wn[2], self._f32(self.conv1.weight), self.g_inputs, self.g_rms,
-                              self.num_kv_heads, self.head_dim, self.inner_dim)
+                              self.num_kv_heads, self.head_dim, self.inner_dim, precision=precision)
         self.__dict__["_packed_cache"] = (key, packed)
         return packed
 
@@ -103,9 +117,10 @@ class GatingPredictor(nn.Module):
             raise AssertionError("gate input shape does not match the predictor")
         wn = self._norm_weights()
         w1 = self._f32(self.conv1.weight)
+        prec = self.precision(post_key.dtype)
         packed = None
         if post_key.dtype == torch.bfloat16 and S > 4 and post_key.is_cuda:
-            packed = self.packed_weights()
+            packed = self.packed_weights(prec)
         return gate_scores_and_mask(
             pre_key if "pre_k" in self.g_inputs else None, post_key if "post_k" in self.g_inputs else None,
             value if "v" in self.g_inputs else None, wn[0], wn[1], wn[2],
@@ -113,18 +128,20 @@ class GatingPredictor(nn.Module):
             self._f32(self.conv2.bias), self.inner_dim, self.act, self.g_rms,
             0.0 if self.g_fast_path else float(self.g_epsilon), threshold,
             like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores, w1_packed=packed,
-            active=active)
+            active=active, precision=prec)
 
     def forward(self, pre_key, post_key, value):
-        """Scores (B, H, S) float32, as the reference's forward returns."""
+        """Scores (B, H, S) as the reference's forward returns them: float32,
+        or bf16 with bf16 parameters on bf16 inputs."""
         scores, _ = self.scores_and_mask(pre_key, post_key, value, threshold=0.0)
-        return scores
+        return scores.to(torch.bfloat16) if self.precision(post_key.dtype) else scores
 
 
-def pack_weights(w_pre, w_post, w_v, w1, g_inputs, rms, num_kv_heads, head_dim, inner):
+def pack_weights(w_pre, w_post, w_v, w1, g_inputs, rms, num_kv_heads, head_dim, inner, precision=0):
     """wgkv_gate_pack_weights: conv1 weight (H*inner, n_in*D[, 1]) fp32 times
     the norm weights (when rms), as three bf16 planes in the matrix-core
-    operand layout.  Returns a uint8 device tensor."""
+    operand layout (precision 0), or conv1 weight alone as one plane
+    (precision 1 / 2: bf16 parameters).  Returns a uint8 device tensor."""
     bits = 0
     for name in g_inputs:
         bits |= _INPUT_BITS[name]
@@ -134,19 +151,20 @@ def pack_weights(w_pre, w_post, w_v, w1, g_inputs, rms, num_kv_heads, head_dim, 
             raise TypeError("gate parameters must be contiguous fp32")
     _require_cuda(w1)
     L = _lib.lib()
-    nbytes = int(L.wgkv_gate_packed_bytes(num_kv_heads, inner, n_in * head_dim))
+    nbytes = int(L.wgkv_gate_packed_bytes(num_kv_heads, inner, n_in * head_dim, int(precision)))
     if nbytes <= 0:
         raise ValueError("unsupported gate shape for packing")
     packed = torch.empty(nbytes, dtype=torch.uint8, device=w1.device)
     st = L.wgkv_gate_pack_weights(_ptr(w_pre), _ptr(w_post), _ptr(w_v), bits, int(bool(rms)), _ptr(w1),
-                                  num_kv_heads, head_dim, inner, _ptr(packed), nbytes, _lib.stream_handle(w1.device))
+                                  num_kv_heads, head_dim, inner, int(precision), _ptr(packed), nbytes,
+                                  _lib.stream_handle(w1.device))
     _lib.check(st, "wgkv_gate_pack_weights")
     return packed
 
 
 def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
                          clamp_min, threshold, like=None, scores_out=None, mask_out=None, want_scores=True,
-                         w1_packed=None, active=None):
+                         w1_packed=None, active=None, precision=0):
     """The gate kernel on explicit fp32 parameters (GatingPredictor.forward,
     src/modeling_layers.py:170-205, with the admission of :1465): inputs
     (B, H, S, D) bf16 or fp32 (None for inputs not used), RMS-norm weights (D)
@@ -155,8 +173,11 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
     conv path's clamp; w1_packed (optional) = pack_weights() of the same
     weights, used for bf16 inputs of more than four tokens; active (optional)
     = (int32 device tensor, value): the launch computes and writes nothing
-    unless the tensor's first element equals value.  Returns (scores f32
-    (B,H,S) or None, mask bool (B,H,S))."""
+    unless the tensor's first element equals value; precision 0 (fp32
+    parameters) or 1 / 2 (bf16 parameters given as fp32 copies, bf16 inputs;
+    fast / Conv1d path rounding, threshold compared in bf16; w1_packed made
+    with the same precision).  Returns (scores f32 (B,H,S) or None, mask bool
+    (B,H,S))."""
     ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
     ref = like if like is not None else next(t for t in (post_key, pre_key, value) if t is not None)
     B, H, S, D = ref.shape
@@ -195,7 +216,7 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         _ptr(w_pre), _ptr(w_post), _ptr(w_v),
         _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
         B, H, S, D, int(inner),
-        int(act), int(bool(rms)), float(clamp_min), float(threshold),
+        int(act), int(bool(rms)), int(precision), float(clamp_min), float(threshold),
         _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
         _ptr(mk), mk.stride(0), mk.stride(1),
         _ptr(w1_packed),

@@ -35,9 +35,9 @@ _LIB.define("generate_sparse_indices(Tensor g_mask, int local_window_size, int b
             "-> (Tensor, Tensor, Tensor, Tensor)")
 _LIB.define("gate_scores_and_mask(Tensor? pre_key, Tensor? post_key, Tensor? value, Tensor? w_pre, "
             "Tensor? w_post, Tensor? w_v, Tensor w1, Tensor b1, Tensor w2, Tensor b2, int inner, int act, "
-            "bool rms, float clamp_min, float threshold, Tensor? w1_packed=None) -> (Tensor, Tensor)")
+            "bool rms, float clamp_min, float threshold, Tensor? w1_packed=None, int precision=0) -> (Tensor, Tensor)")
 _LIB.define("gate_pack_weights(Tensor? w_pre, Tensor? w_post, Tensor? w_v, Tensor w1, int inputs_mask, bool rms, "
-            "int num_kv_heads, int head_dim, int inner) -> Tensor")
+            "int num_kv_heads, int head_dim, int inner, int precision=0) -> Tensor")
 
 
 # ---- CUDA (HIP) kernels: the library calls ----------------------------------
@@ -56,14 +56,14 @@ def _generate_sparse_indices(g_mask, local_window_size, block_size=64):
 
 
 def _gate(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, threshold,
-          w1_packed=None):
+          w1_packed=None, precision=0):
     return _gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
-                                 clamp_min, threshold, w1_packed=w1_packed)
+                                 clamp_min, threshold, w1_packed=w1_packed, precision=precision)
 
 
-def _gate_pack(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner):
+def _gate_pack(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner, precision=0):
     names = [n for i, n in enumerate(_INPUT_NAMES) if inputs_mask >> i & 1]
-    return _pack_weights(w_pre, w_post, w_v, w1, names, rms, num_kv_heads, head_dim, inner)
+    return _pack_weights(w_pre, w_post, w_v, w1, names, rms, num_kv_heads, head_dim, inner, precision=precision)
 
 
 _LIB.impl("sparse_attn", _sparse_attn, "CUDA")
@@ -92,7 +92,7 @@ def _generate_sparse_indices_meta(g_mask, local_window_size, block_size=64):
 
 
 def _gate_meta(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, threshold,
-               w1_packed=None):
+               w1_packed=None, precision=0):
     ref = next(t for t in (post_key, pre_key, value) if t is not None)
     B, H, S, _ = ref.shape
     return (torch.empty(B, H, S, dtype=torch.float32, device=ref.device),
@@ -102,9 +102,10 @@ def _gate_meta(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inn
 _LIB.impl("sparse_attn", _sparse_attn_meta, "Meta")
 _LIB.impl("paged_decode_attn", _paged_decode_attn_meta, "Meta")
 _LIB.impl("generate_sparse_indices", _generate_sparse_indices_meta, "Meta")
-def _gate_pack_meta(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner):
+def _gate_pack_meta(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner, precision=0):
     n_in = bin(inputs_mask & 7).count("1")
-    return torch.empty(num_kv_heads * inner * n_in * head_dim * 3 * 2, dtype=torch.uint8, device=w1.device)
+    planes = 1 if precision else 3
+    return torch.empty(num_kv_heads * inner * n_in * head_dim * planes * 2, dtype=torch.uint8, device=w1.device)
 
 
 _LIB.impl("gate_scores_and_mask", _gate_meta, "Meta")

@@ -161,10 +161,13 @@ class PrefillWorkload:
     local_window: int
 
 
-def prefill_llama(S=32768, Hq=32, Hkv=8, D=128, W=1024, frac=0.2, threshold=0.1, device="cuda", seed=0):
+def prefill_llama(S=32768, Hq=32, Hkv=8, D=128, W=1024, frac=0.2, threshold=0.1, device="cuda", seed=0,
+                  gate_dtype=torch.bfloat16):
     """Config-4 shapes: bf16 q/k/v/pre-RoPE k ~ N(0,1) in (B, S, H, D) layout,
     a gate with the reference's default init whose conv2 bias is shifted per
-    head so ~``frac`` of the prompt scores above ``threshold``."""
+    head so ~``frac`` of the prompt scores above ``threshold``.  The gate's
+    parameters are bf16 by default, as the reference's profiling run loads
+    them (scripts/profiling.py:222-226)."""
     import math
     from .gate import GatingPredictor
     g = torch.Generator(device=device).manual_seed(seed)
@@ -174,7 +177,8 @@ def prefill_llama(S=32768, Hq=32, Hkv=8, D=128, W=1024, frac=0.2, threshold=0.1,
 
     q, k, v, pk = rn(1, S, Hq, D), rn(1, S, Hkv, D), rn(1, S, Hkv, D), rn(1, S, Hkv, D)
     torch.manual_seed(seed)
-    gate = GatingPredictor(D, Hkv, ["pre_k", "post_k"], "gelu", 4.0, 1e-3, True, True).to(device)
+    gate = GatingPredictor(D, Hkv, ["pre_k", "post_k"], "gelu", 4.0, 1e-3, True, True).to(device=device,
+                                                                                         dtype=gate_dtype)
     scores, _ = gate.scores_and_mask(pk.transpose(1, 2), k.transpose(1, 2), None, 0.5)
     logit = torch.log(scores.double()) - torch.log1p(-scores.double())
     with torch.no_grad():
