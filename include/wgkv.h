@@ -415,6 +415,45 @@ int wgkv_quest_select(
     void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * SnapKV eviction over the dual cache (the reference's comparison baseline,
+ * snapkv_evict, src/modeling_layers.py:595-671, and its trigger :1500-1507),
+ * in four launches with no host synchronisation.
+ *
+ * Runs only if the sum of global_lengths (L*H) exceeds max_cached_tokens
+ * (decided on the device; state[0] = 1 when it ran, state[1] counts the
+ * evictions, the reference's snapkv_evict_count).  Then, for every (layer,
+ * KV head) with n global tokens and n_evict = int(n * evict_ratio) > 0: the
+ * window queries query_window bf16 (L, window, Hq, D) (the reference's
+ * snapkv_query_buffer, Hq = H * num_kv_groups) score the head's global keys
+ * -- softmax over the keys of q.k * softmax_scale (logits_bf16 != 0: the
+ * logit rounded as the reference's bf16 matmul and scalar multiply round
+ * it, bf16(bf16(q.k) * scale); 0: fp32), max over the group's query heads,
+ * mean over the window, max-pooled over kernel_size (odd) positions --, the
+ * n_evict lowest pooled scores are dropped (equal scores: lower position
+ * first; the reference's topk leaves their order unspecified), the kept
+ * tokens are packed in order into the head's first pages of pool_k /
+ * pool_v (bf16 (total_pages*block_size, D)), global_lengths is set to the
+ * kept count, and the head's pages past the kept ones are appended to
+ * free_ids (free_count entries, heads in (layer, head) order, pages in
+ * table order) with their block_table entries set to total_pages - 1.
+ * block_table i32 (L, H, max_pages): local_pages ring pages, then the
+ * global pages.  scores_out (may be NULL): f32 (L*H, max_tokens_per_head),
+ * the pooled scores of each evicted head's tokens.  D in {64, 128},
+ * num_kv_groups <= 8.  workspace: wgkv_snapkv_workspace_bytes() bytes,
+ * 256-byte aligned, not shared by concurrent calls.
+ * ---------------------------------------------------------------------- */
+int64_t wgkv_snapkv_workspace_bytes(int32_t num_layers, int32_t num_kv_heads, int32_t num_kv_groups,
+                                    int32_t window, int32_t max_tokens_per_head);
+int wgkv_snapkv_evict(
+    void* pool_k, void* pool_v, int32_t* block_table, int32_t* global_lengths,
+    int32_t* free_ids, int32_t* free_count, const void* query_window,
+    int32_t num_layers, int32_t num_kv_heads, int32_t num_kv_groups, int32_t head_dim, int32_t block_size,
+    int32_t local_pages, int32_t max_pages, int32_t total_pages, int32_t max_tokens_per_head,
+    int32_t window, int32_t kernel_size, double evict_ratio, float softmax_scale, int64_t max_cached_tokens,
+    int32_t logits_bf16, int32_t* state, float* scores_out,
+    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Decoder building blocks for the end-to-end harness around the path (bf16).
  * No counterpart among the path's functions: each replaces a chain of torch
  * kernels of the reference model with one launch, with the same bf16

@@ -10,11 +10,16 @@ the kept tokens are packed in order into the head's first pages, and the
 released pages are appended to ``free_block_ids`` (reused first by
 promotion, ``DualCacheOracle.migrate``).
 
-Kept as the GPU path does: fp32 products (the reference multiplies in bf16)
-and equal scores dropped lower position first (the reference's topk order is
-unspecified).  Pinned in tests/test_oracle_snapkv.py by properties: the
-dropped count, order preservation, every kept score >= every dropped score,
-ratio 1 releasing every page, and a planted key every window query attends to.
+The logits are fp32 products, or (``logits_bf16``) rounded as the
+reference's bf16 matmul and scalar multiply round them,
+bf16(bf16(q.k) * scale); equal scores are dropped lower position first (the
+reference's topk leaves their order unspecified).  Pinned by the reference's
+own outputs (tests/golden/snapkv_golden.npz, written by its snapkv_evict in
+bf16 and in fp32: pooled scores, dropped positions, lengths, tables, free
+list and kept contents) and, in tests/test_oracle_snapkv.py, by properties:
+the dropped count, order preservation, every kept score >= every dropped
+score, ratio 1 releasing every page, and a planted key every window query
+attends to.
 """
 import torch
 import torch.nn.functional as F
@@ -46,16 +51,29 @@ class QueryWindow:
                 self.ptr = (self.ptr + 1) % self.window
 
 
-def head_scores(qw, keys, scale, kernel_size):
+def logits(qw, keys, scale, logits_bf16=False):
+    """(G, window, n) float32 logits q.k * scale; with logits_bf16 the product
+    sum is rounded to bf16, then the scaled value (the reference's bf16
+    torch.matmul(...) * self.scaling, src/modeling_layers.py:616-617)."""
+    if logits_bf16:
+        acc = (qw.double() @ keys.double().T).to(torch.bfloat16).float()
+        return (acc * torch.tensor(scale, dtype=torch.float32)).to(torch.bfloat16).float()
+    return (qw.float() @ keys.float().T) * scale
+
+
+def head_scores(qw, keys, scale, kernel_size, logits_bf16=False):
     """qw (G, window, D), keys (n, D) -> pooled scores (n,) float32."""
-    attn = torch.softmax((qw.float() @ keys.float().T) * scale, dim=-1)
+    attn = torch.softmax(logits(qw, keys, scale, logits_bf16), dim=-1)
     s = attn.amax(dim=0).mean(dim=0).view(1, 1, -1)
     return F.max_pool1d(s, kernel_size=kernel_size, stride=1, padding=kernel_size // 2).view(-1)
 
 
-def evict(cache, window, num_kv_groups, scale, ratio, kernel_size):
+def evict(cache, window, num_kv_groups, scale, ratio, kernel_size, logits_bf16=False, choose=None):
     """Evict on every (layer, head) of ``cache``; returns the dropped positions
-    per (layer, head) (logical global indices before the eviction)."""
+    per (layer, head) (logical global indices before the eviction).
+    ``choose(l, h, scores, n_evict)`` (optional) names the dropped positions
+    instead of the lowest-score rule (to replay another implementation's
+    choice among equal scores)."""
     if not hasattr(cache, "free_block_ids"):
         cache.free_block_ids = []
     P, D, lb = cache.P, cache.D, cache.local_blocks_per_head
@@ -72,8 +90,11 @@ def evict(cache, window, num_kv_groups, scale, ratio, kernel_size):
             pages = (n + P - 1) // P
             ids = cache.block_table[l, h, lb:lb + pages].long()
             keys = kc[ids].reshape(-1, D)[:n]
-            s = head_scores(qw[h], keys, scale, kernel_size)
-            ev = torch.sort(s, stable=True).indices[:n_evict]
+            s = head_scores(qw[h], keys, scale, kernel_size, logits_bf16)
+            if choose is not None:
+                ev = torch.as_tensor(choose(l, h, s, n_evict), dtype=torch.int64)
+            else:
+                ev = torch.sort(s, stable=True).indices[:n_evict]
             keep = torch.ones(n, dtype=torch.bool)
             keep[ev] = False
             kept_idx = torch.nonzero(keep).flatten()

@@ -9,6 +9,9 @@ Only functions that no closed form or reference test pins are run here:
 * ``GatingPredictor.forward`` (src/modeling_layers.py:134-205), fast and conv
   paths -- float32 scores, and the same module converted to bf16 on bf16
   inputs (the inference scripts' configuration) -- bf16 scores;
+* ``snapkv_evict`` (:595-671) on seeded cache states, bf16 and fp32 -- the
+  pooled scores and dropped positions of every head, the resulting lengths,
+  tables, free list and kept contents;
 * the dual-cache state machine through ``self_attn_forward_patch_inference``
   (:1452-1509) -> ``prefill_wrapper`` (:1183-1376), ``decode_wrapper``
   (:1379-1449), ``migrate_local_kv_to_global`` (:674-763),
@@ -189,17 +192,73 @@ def cache_golden(ref):
         json.dump(meta, f, indent=1, sort_keys=True)
 
 
+def snapkv_golden(ref):
+    """The reference's snapkv_evict (src/modeling_layers.py:595-671) on the
+    seeded states of scenarios.SNAPKV_SCENARIOS, in bf16 and in fp32: per
+    evicted head (call order) its pooled scores (the input of its
+    torch.topk) and dropped positions, then the lengths, tables, free list
+    and a checksum of every head's kept tokens in order."""
+    out, meta = {}, {}
+    for name, sc in scenarios.SNAPKV_SCENARIOS.items():
+        st = scenarios.snapkv_state(sc)
+        L, H, G, D, W = sc["L"], sc["H"], sc["G"], sc["D"], sc["W"]
+        lb = W // 16
+        cfg = types.SimpleNamespace(num_hidden_layers=L, num_key_value_heads=H, snapkv_evict_ratio=sc["ratio"],
+                                    snapkv_kernel_size=sc["ksz"], block_size=16, snapkv_window_size=sc["win"])
+        mod = types.SimpleNamespace(config=cfg, num_key_value_groups=G, head_dim=D, scaling=D ** -0.5,
+                                    layer_idx=L - 1)
+        pkv = types.SimpleNamespace(block_pool_k=st["pool_k"].clone(), block_pool_v=st["pool_v"].clone(),
+                                    block_table=st["block_table"].clone(),
+                                    global_lengths=st["global_lengths"].clone(), free_block_ids=list(st["free_ids"]),
+                                    total_blocks=st["total_blocks"], snapkv_query_buffer=st["qbuf"].clone(),
+                                    snapkv_query_length=sc["win"])
+        calls = []
+        orig = torch.topk
+
+        def recording_topk(*args, **kwargs):
+            r = orig(*args, **kwargs)
+            calls.append((args[0].detach().float().clone(), r.indices.clone()))
+            return r
+
+        torch.topk = recording_topk
+        try:
+            with torch.no_grad():
+                ref.snapkv_evict(mod, pkv, torch.device("cpu"), lb)
+        finally:
+            torch.topk = orig
+        heads = [(l, h) for l in range(L) for h in range(H)
+                 if int(int(st["global_lengths"][l, h]) * sc["ratio"]) > 0]
+        assert len(heads) == len(calls)
+        out[f"{name}.heads"] = np.array(heads, dtype=np.int32).reshape(-1, 2)
+        out[f"{name}.scores"] = torch.cat([c[0] for c in calls]).numpy()
+        out[f"{name}.evicted"] = torch.cat([torch.sort(c[1]).values for c in calls]).to(torch.int32).numpy()
+        out[f"{name}.global_lengths"] = pkv.global_lengths.numpy().copy()
+        out[f"{name}.block_table"] = pkv.block_table.numpy().copy()
+        out[f"{name}.free_ids"] = np.array(pkv.free_block_ids, dtype=np.int32)
+        kept_k = scenarios.logical_tokens(pkv.block_pool_k, pkv.block_table, pkv.global_lengths, lb)
+        kept_v = scenarios.logical_tokens(pkv.block_pool_v, pkv.block_table, pkv.global_lengths, lb)
+        meta[name] = dict(
+            inputs_sha256=scenarios.checksum(st["pool_k"], st["pool_v"], st["qbuf"], st["block_table"]),
+            kept_sha256=scenarios.checksum(*[kept_k[k] for k in sorted(kept_k)], *[kept_v[k] for k in sorted(kept_v)]))
+        print(name, meta[name], "evicted heads", heads)
+    np.savez_compressed(os.path.join(HERE, "snapkv_golden.npz"), **out)
+    with open(os.path.join(HERE, "snapkv_golden.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+
+
 def main():
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     ref = load_reference(root)
     torch.set_num_threads(4)
-    only = sys.argv[2:] or ["gate", "gate_bf16", "cache"]
+    only = sys.argv[2:] or ["gate", "gate_bf16", "cache", "snapkv"]
     if "gate" in only:
         gate_golden(ref)
     if "gate_bf16" in only:
         gate_bf16_golden(ref)
     if "cache" in only:
         cache_golden(ref)
+    if "snapkv" in only:
+        snapkv_golden(ref)
 
 
 if __name__ == "__main__":

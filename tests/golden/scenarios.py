@@ -77,6 +77,66 @@ def gate_inputs(sc):
     return params, pre_k, post_k, value
 
 
+# SnapKV eviction states: pages of each head's global tokens scattered over
+# the pool, a free list already holding two pages, a full query window.
+SNAPKV_SCENARIOS = {
+    "bf16_k5": dict(L=2, H=2, G=2, D=64, W=64, lengths=((300, 517), (16, 2)), win=32, ksz=5, ratio=0.3,
+                    dtype="bf16", seed=30),
+    "bf16_k1": dict(L=2, H=2, G=2, D=64, W=64, lengths=((301, 160), (47, 0)), win=16, ksz=1, ratio=0.25,
+                    dtype="bf16", seed=31),
+    "f32_k5": dict(L=1, H=2, G=2, D=64, W=64, lengths=((257, 400),), win=32, ksz=5, ratio=0.4, dtype="f32", seed=32),
+    "d128_g4": dict(L=1, H=2, G=4, D=128, W=128, lengths=((700, 129),), win=48, ksz=3, ratio=0.5, dtype="bf16",
+                    seed=33),
+    "ratio1": dict(L=1, H=2, G=1, D=64, W=64, lengths=((40, 33),), win=16, ksz=5, ratio=1.0, dtype="bf16", seed=34),
+}
+
+
+def snapkv_state(sc):
+    """A dual-cache state for a SnapKV scenario: dict with pool_k, pool_v
+    ((total_blocks*16, D); bf16, or fp32 holding bf16 values), block_table
+    int32 (L, H, max_pages) (W/16 ring pages, then the global pages, the
+    sentinel total_blocks-1 after them), global_lengths int32 (L, H),
+    free_ids (list), total_blocks, qbuf (L, win, H*G, D) like the pool."""
+    gen = torch.Generator().manual_seed(sc["seed"])
+    L, H, G, D, W, P = sc["L"], sc["H"], sc["G"], sc["D"], sc["W"], 16
+    lengths = torch.tensor(sc["lengths"], dtype=torch.int32)
+    lb = W // P
+    maxp = lb + (int(lengths.max()) + P - 1) // P + 2
+    need = L * H * lb + int(((lengths + P - 1) // P).sum())
+    total = need + 6
+    perm = torch.randperm(total - 1 - L * H * lb, generator=gen) + L * H * lb  # pages past the ring pages
+    table = torch.full((L, H, maxp), total - 1, dtype=torch.int32)
+    table[:, :, :lb] = torch.arange(L * H * lb, dtype=torch.int32).view(L, H, lb)
+    at = 0
+    for l in range(L):
+        for h in range(H):
+            np_ = (int(lengths[l, h]) + P - 1) // P
+            table[l, h, lb:lb + np_] = perm[at:at + np_].to(torch.int32)
+            at += np_
+    free_ids = [int(x) for x in perm[at:at + 2]]
+    dt = torch.bfloat16
+    pool_k = torch.randn(total * P, D, generator=gen).to(dt)
+    pool_v = torch.randn(total * P, D, generator=gen).to(dt)
+    qbuf = (1.5 * torch.randn(L, sc["win"], H * G, D, generator=gen)).to(dt)
+    if sc["dtype"] == "f32":
+        pool_k, pool_v, qbuf = pool_k.float(), pool_v.float(), qbuf.float()
+    return dict(pool_k=pool_k, pool_v=pool_v, block_table=table, global_lengths=lengths.clone(), free_ids=free_ids,
+                total_blocks=total, qbuf=qbuf)
+
+
+def logical_tokens(pool, table, lengths, lb, P=16):
+    """Per (layer, head) the (n, D) rows of the head's global tokens in order."""
+    D = pool.shape[1]
+    out = {}
+    L, H = lengths.shape
+    for l in range(L):
+        for h in range(H):
+            n = int(lengths[l, h])
+            ids = table[l, h, lb:lb + (n + P - 1) // P].long()
+            out[(l, h)] = pool.view(-1, P, D)[ids].reshape(-1, D)[:n]
+    return out
+
+
 def gate_inputs_bf16(sc):
     """bf16 parameters (the fp32 draw of gate_params, rounded, conv2.bias
     shifted by logit(0.1)) and bf16 (1, H, S, D) inputs."""

@@ -25,6 +25,7 @@ c_i32 = ctypes.c_int32
 c_i64 = ctypes.c_int64
 c_ptr = ctypes.c_void_p
 c_f32 = ctypes.c_float
+c_f64 = ctypes.c_double
 c_size = ctypes.c_size_t
 
 # name -> (restype, argtypes); kept in the order of include/wgkv.h
@@ -148,6 +149,15 @@ SIGNATURES = {
         c_i32, c_i32, c_i32, c_i32,
         c_ptr, c_i32, c_ptr,
         c_ptr, c_size, c_ptr]),
+    "wgkv_snapkv_workspace_bytes": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),
+    "wgkv_snapkv_evict": (ctypes.c_int, [
+        c_ptr, c_ptr, c_ptr, c_ptr,
+        c_ptr, c_ptr, c_ptr,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_f64, c_f32, c_i64,
+        c_i32, c_ptr, c_ptr,
+        c_ptr, c_i64, c_ptr]),
     "wgkv_chunk_admit_workspace_bytes": (c_size, [c_i32, c_i32, c_i32]),
     "wgkv_chunk_cache_update": (ctypes.c_int, [
         c_i32,

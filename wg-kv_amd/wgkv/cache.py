@@ -67,7 +67,8 @@ class DualCache:
                                                    head_dim, dtype=dtype, device=device)
             self.snapkv_query_length = 0
             self.snapkv_query_ptr = 0
-            self.snapkv_evict_count = 0
+            # [evicted on the last call, evictions so far] -- decided on the device
+            self.snapkv_state = torch.zeros(2, **i32)
             # the released pages, in release order, and their count -- on the device,
             # where the promotion kernel takes pages from the end of the list
             self.free_block_ids_dev = torch.zeros(self.total_blocks, **i32)
@@ -112,6 +113,12 @@ class DualCache:
         ``free_block_ids_dev[:free_count_dev]``)."""
         n = int(self.free_count_dev.item())
         return self.free_block_ids_dev[:n].tolist()
+
+    @property
+    def snapkv_evict_count(self):
+        """Evictions so far (the reference's snapkv_evict_count, :1506); a
+        host read of the device counter."""
+        return int(self.snapkv_state[1].item())
 
     @property
     def next_free_block(self):

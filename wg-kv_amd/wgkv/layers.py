@@ -11,7 +11,8 @@ HIP library (kernels (1)-(4)).  ``self`` needs ``config``, ``layer_idx``,
 
 Only inference (gating_mode 3) is on the hot path.  Of the comparison
 baselines, QUEST page selection (``use_quest``) and SnapKV eviction
-(``snapkv_enabled``) run on the same page tables and kernels; the training
+(``snapkv_enabled``, scored, selected and packed by device kernels) run on
+the same page tables; the training
 modes, DuoAttention and AdaEA are outside it and raise NotImplementedError.
 """
 from dataclasses import dataclass, field
@@ -104,60 +105,26 @@ def snapkv_record_queries(self, past_key_value, query_states):
 
 
 @torch.no_grad()
-def snapkv_evict(self, past_key_value, device, local_blocks_per_head):
-    """src/modeling_layers.py:595-671, on the device: per (layer, KV head),
-    score the global tokens by the window queries' attention (softmax in
+def snapkv_evict(self, past_key_value, device, local_blocks_per_head, max_cached_tokens=None):
+    """src/modeling_layers.py:595-671 on the device (wgkv_snapkv_evict): per
+    (layer, KV head), score the global tokens by the window queries'
+    attention (logits rounded as the reference's bf16 product, softmax in
     fp32, max over the grouped heads, mean over the window, max-pooled),
     drop the int(len * ratio) lowest (equal scores: lower position first),
     pack the kept tokens into the head's first pages, release the rest to the
-    free list and reset their table slots.  The products are fp32 (the
-    reference multiplies in bf16)."""
-    import torch.nn.functional as F
+    free list and reset their table slots -- no host synchronisation.
+
+    With ``max_cached_tokens`` the eviction runs only if the global lengths
+    sum to more (the trigger of :1503-1506, decided on the device, which
+    also counts the eviction); without it, it always runs, as the reference's
+    function does."""
     c = past_key_value
     cfg = self.config
-    if c.snapkv_query_length != cfg.snapkv_window_size:
-        raise AssertionError("SnapKV eviction needs a full query window")
-    P, D = c.block_size, c.head_dim
-    H, L = c.num_kv_heads, c.num_layers
-    G = cfg.num_attention_heads // cfg.num_key_value_heads
-    win, ksz = cfg.snapkv_window_size, cfg.snapkv_kernel_size
-    lb = local_blocks_per_head
-    lengths = c.global_lengths.cpu()
-    free_n = int(c.free_count_dev.item())
-    offs = torch.arange(P, dtype=torch.int64, device=device)
-    for l in range(L):
-        qw = c.snapkv_query_buffer[l].view(win, H, G, D).permute(1, 2, 0, 3).float()  # (H, G, win, D)
-        for h in range(H):
-            n = int(lengths[l, h])
-            n_evict = int(n * cfg.snapkv_evict_ratio)
-            if n_evict == 0:
-                continue
-            pages = (n + P - 1) // P
-            ids = c.block_table[l, h, lb:lb + pages].long()
-            linear = (ids[:, None] * P + offs[None, :]).reshape(-1)[:n]
-            keys = c.block_pool_k[linear].float()
-            attn = torch.softmax((qw[h] @ keys.T) * self.scaling, dim=-1)          # (G, win, n)
-            score = F.max_pool1d(attn.amax(dim=0).mean(dim=0).view(1, 1, -1), kernel_size=ksz, stride=1,
-                                 padding=ksz // 2).view(-1)
-            evict = torch.sort(score, stable=True).indices[:n_evict]
-            keep_mask = torch.ones(n, dtype=torch.bool, device=device)
-            keep_mask[evict] = False
-            keep = torch.nonzero(keep_mask).flatten()
-            kept = n - n_evict
-            new_pages = (kept + P - 1) // P
-            if kept > 0:
-                dst = linear[:kept]
-                kk = c.block_pool_k[linear[keep]]
-                vv = c.block_pool_v[linear[keep]]
-                c.block_pool_k[dst] = kk
-                c.block_pool_v[dst] = vv
-            if new_pages < pages:
-                freed = c.block_table[l, h, lb + new_pages:lb + pages].clone()
-                c.block_table[l, h, lb + new_pages:lb + pages] = c.total_blocks - 1
-                c.free_block_ids_dev[free_n:free_n + freed.numel()] = freed
-                free_n += freed.numel()
-            c.global_lengths[l, h] = kept
-    c.free_count_dev.fill_(free_n)
+    if max_cached_tokens is None and c.snapkv_query_length != cfg.snapkv_window_size:
+        raise AssertionError("SnapKV eviction needs a full query window")  # :597
+    ops.snapkv_evict(c, cfg.num_attention_heads // cfg.num_key_value_heads, self.scaling, cfg.snapkv_window_size,
+                     cfg.snapkv_kernel_size, cfg.snapkv_evict_ratio,
+                     -1 if max_cached_tokens is None else max_cached_tokens)
 
 
 def refresh_local_is_global(self, past_key_value, device, on_device=False):
@@ -306,12 +273,16 @@ def self_attn_forward_patch_inference(self, past_key_value, input_shape, query_s
     if self.config.snapkv_enabled:  # :1500-1507
         c = past_key_value
         if c.device_ring:
-            raise AssertionError("SnapKV eviction is decided on the host; it cannot run with device_ring")
+            raise AssertionError("the SnapKV query window advances on the host; it cannot run with device_ring")
         snapkv_record_queries(self, c, query_states)
-        if (self.layer_idx == self.config.num_hidden_layers - 1 and
-                int(c.global_lengths.sum().item()) > self.config.snapkv_max_cached_tokens):
-            c.snapkv_evict_count += 1
-            snapkv_evict(self, c, device, lbph)
+        if self.layer_idx == self.config.num_hidden_layers - 1:
+            budget = self.config.snapkv_max_cached_tokens
+            if c.snapkv_query_length == self.config.snapkv_window_size:
+                snapkv_evict(self, c, device, lbph, max_cached_tokens=budget)  # trigger decided on the device
+            elif int(c.global_lengths.sum().item()) > budget:
+                # the reference's eviction asserts a full window (:597); only a
+                # window not yet full reads the trigger back to raise it here
+                raise AssertionError("SnapKV eviction needs a full query window")
     return out
 
 

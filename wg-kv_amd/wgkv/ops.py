@@ -437,3 +437,45 @@ def quest_select(cache, layer, q, local_tokens, token_budget):
         _ptr(ws), ws.numel(), _lib.stream_handle(dev))
     _lib.check(st, "wgkv_quest_select")
     return sel_len, sel_bt
+
+
+def snapkv_evict(cache, num_kv_groups, softmax_scale, window, kernel_size, evict_ratio, max_cached_tokens=-1,
+                 logits_bf16=True, scores_out=None):
+    """wgkv_snapkv_evict over every (layer, KV head) of ``cache``
+    (snapkv_evict, src/modeling_layers.py:595-671): scores, lowest-score
+    selection, in-place packing and page release on the device, run only if
+    the sum of the global lengths exceeds ``max_cached_tokens`` (decided on
+    the device; -1 always runs).  ``cache.snapkv_state`` (int32 (2)) holds
+    [ran on this call, evictions so far].  ``logits_bf16`` rounds the logits
+    as the reference's bf16 matmul does.  ``scores_out`` (optional, f32
+    (L*H, max_tokens_per_head)) receives the pooled scores of the evicted
+    heads."""
+    L, H, D, P = cache.num_layers, cache.num_kv_heads, cache.head_dim, cache.block_size
+    mtph = cache.max_tokens_per_head
+    qbuf = cache.snapkv_query_buffer
+    _require_cuda(qbuf, cache.block_pool_k)
+    if qbuf.dtype != torch.bfloat16 or not qbuf.is_contiguous():
+        raise TypeError("the SnapKV query window must be contiguous bf16")
+    if tuple(qbuf.shape) != (L, window, H * num_kv_groups, D):
+        raise AssertionError("query window shape does not match the cache")
+    dev = qbuf.device
+    lib = _lib.lib()
+    nbytes = int(lib.wgkv_snapkv_workspace_bytes(L, H, num_kv_groups, window, mtph))
+    if nbytes <= 0:
+        raise ValueError("unsupported SnapKV shape")
+    ws = cache.__dict__.get("_snapkv_ws")
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        cache.__dict__["_snapkv_ws"] = ws
+    if scores_out is not None and (scores_out.dtype != torch.float32 or scores_out.numel() < L * H * mtph
+                                   or not scores_out.is_contiguous()):
+        raise ValueError("scores_out must be contiguous f32 with L*H*max_tokens_per_head elements")
+    st = lib.wgkv_snapkv_evict(
+        _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.block_table), _ptr(cache.global_lengths),
+        _ptr(cache.free_block_ids_dev), _ptr(cache.free_count_dev), _ptr(qbuf),
+        L, H, int(num_kv_groups), D, P,
+        cache.local_window_size // P, cache.block_table.shape[2], cache.total_blocks, mtph,
+        int(window), int(kernel_size), float(evict_ratio), float(softmax_scale), int(max_cached_tokens),
+        int(bool(logits_bf16)), _ptr(cache.snapkv_state), _ptr(scores_out),
+        _ptr(ws), ws.numel(), _lib.stream_handle(dev))
+    _lib.check(st, "wgkv_snapkv_evict")
