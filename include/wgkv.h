@@ -388,7 +388,9 @@ int wgkv_chunk_prefill_attn(
  * wgkv_quest_select: the selection of quest_select_blocks for one decode
  * step of `layer`: q bf16 (Hq, D) (stride q_stride_h) of the step's token;
  * each KV head scores its full global pages by max over its G query heads of
- * sum_d q_d * (q_d >= 0 ? key_max_d : key_min_d) (fp32), keeps the top
+ * sum_d q_d * (q_d >= 0 ? key_max_d : key_min_d) (fp32; with scores_bf16
+ * != 0 rounded as the reference's bf16 torch ops round it: each product to
+ * bf16, the fp32 sum to bf16), keeps the top
  * k = min(ceil(max(budget - local_tokens, 0)/page), global pages) - (1 if a
  * partial page exists) full pages (equal scores at the cut: lowest page
  * first) and the partial page, and writes sel_block_table i32 (H, sel_cap):
@@ -410,7 +412,7 @@ int wgkv_quest_select(
     const int32_t* block_table, int32_t max_pages_per_head, const int32_t* global_lengths,
     const void* key_min, const void* key_max,
     int32_t layer, int32_t num_layers, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t local_window, int32_t page_size, int32_t local_tokens, int32_t token_budget,
+    int32_t local_window, int32_t page_size, int32_t local_tokens, int32_t token_budget, int32_t scores_bf16,
     int32_t* sel_block_table, int32_t sel_cap, int32_t* sel_seqlens,
     void* workspace, size_t workspace_bytes, void* stream);
 

@@ -9,6 +9,8 @@ Only functions that no closed form or reference test pins are run here:
 * ``GatingPredictor.forward`` (src/modeling_layers.py:134-205), fast and conv
   paths -- float32 scores, and the same module converted to bf16 on bf16
   inputs (the inference scripts' configuration) -- bf16 scores;
+* ``quest_select_blocks`` (:452-576) on seeded cache states, bf16 and fp32
+  -- the selected tables and lengths and the page ranking it made;
 * ``snapkv_evict`` (:595-671) on seeded cache states, bf16 and fp32 -- the
   pooled scores and dropped positions of every head, the resulting lengths,
   tables, free list and kept contents;
@@ -246,11 +248,54 @@ def snapkv_golden(ref):
         json.dump(meta, f, indent=1, sort_keys=True)
 
 
+def quest_golden(ref):
+    """The reference's quest_select_blocks (src/modeling_layers.py:452-576)
+    at each step of scenarios.QUEST_SCENARIOS: the returned cache_seqlens and
+    block_table, and per head that ranks its full pages the page scores and
+    the chosen positions (the input and output of its torch.topk)."""
+    out, meta = {}, {}
+    for name, sc in scenarios.QUEST_SCENARIOS.items():
+        st = scenarios.quest_state(sc)
+        H, G, D, W = sc["H"], sc["G"], sc["D"], sc["W"]
+        pkv = types.SimpleNamespace(block_table=st["block_table"], global_lengths=st["global_lengths"],
+                                    quest_block_key_min=st["key_min"], quest_block_key_max=st["key_max"])
+        meta[name] = dict(inputs_sha256=scenarios.checksum(st["pool_k"], st["key_min"], st["key_max"],
+                                                           st["block_table"], *st["qs"]))
+        for i, (local, budget) in enumerate(sc["steps"]):
+            cfg = types.SimpleNamespace(num_key_value_heads=H, block_size=16, quest_token_budget=budget)
+            mod = types.SimpleNamespace(config=cfg, num_key_value_groups=G, head_dim=D, layer_idx=0)
+            calls = []
+            orig = torch.topk
+
+            def recording_topk(*args, **kwargs):
+                r = orig(*args, **kwargs)
+                calls.append((args[0].detach().float().clone(), r.indices.clone()))
+                return r
+
+            torch.topk = recording_topk
+            try:
+                with torch.no_grad():
+                    seqlens, table = ref.quest_select_blocks(mod, st["qs"][i].view(1, H * G, 1, D), pkv, W // 16,
+                                                             torch.device("cpu"), local)
+            finally:
+                torch.topk = orig
+            out[f"{name}.{i}.seqlens"] = seqlens.numpy().copy()
+            out[f"{name}.{i}.block_table"] = table.numpy().copy()
+            out[f"{name}.{i}.ranked_scores"] = (torch.cat([c[0] for c in calls]).numpy() if calls
+                                                else np.zeros(0, np.float32))
+            out[f"{name}.{i}.ranked_choice"] = (torch.cat([c[1] for c in calls]).to(torch.int32).numpy() if calls
+                                                else np.zeros(0, np.int32))
+            print(name, i, (local, budget), "seqlens", seqlens.tolist(), "ranked heads", len(calls))
+    np.savez_compressed(os.path.join(HERE, "quest_golden.npz"), **out)
+    with open(os.path.join(HERE, "quest_golden.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+
+
 def main():
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     ref = load_reference(root)
     torch.set_num_threads(4)
-    only = sys.argv[2:] or ["gate", "gate_bf16", "cache", "snapkv"]
+    only = sys.argv[2:] or ["gate", "gate_bf16", "cache", "snapkv", "quest"]
     if "gate" in only:
         gate_golden(ref)
     if "gate_bf16" in only:
@@ -259,6 +304,8 @@ def main():
         cache_golden(ref)
     if "snapkv" in only:
         snapkv_golden(ref)
+    if "quest" in only:
+        quest_golden(ref)
 
 
 if __name__ == "__main__":

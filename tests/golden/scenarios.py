@@ -91,6 +91,53 @@ SNAPKV_SCENARIOS = {
 }
 
 
+# QUEST page selection: cache states with page key bounds, and per scenario
+# a list of (local tokens, token budget) decode steps, each with its own query.
+QUEST_SCENARIOS = {
+    "g4_d128": dict(H=3, G=4, D=128, W=64, lengths=(700, 129, 64), dtype="bf16", seed=40,
+                    steps=((64, 320), (17, 200), (64, 40), (1, 4096), (33, 120))),
+    "g2_d64_f32": dict(H=2, G=2, D=64, W=64, lengths=(500, 33), dtype="f32", seed=41,
+                       steps=((64, 256), (5, 100), (64, 64))),
+    "g1_d64": dict(H=2, G=1, D=64, W=64, lengths=(256, 255), dtype="bf16", seed=42,
+                   steps=((64, 128), (64, 150), (10, 4000))),
+}
+
+
+def quest_state(sc):
+    """One layer's cache state for a QUEST scenario: pool_k, block_table
+    (1, H, max_pages), global_lengths (1, H), key_min / key_max (total_blocks,
+    D) -- the min / max over each global page's valid rows, as the
+    reference's prefill writes them -- and one query (H*G, D) per step."""
+    gen = torch.Generator().manual_seed(sc["seed"])
+    H, G, D, W, P = sc["H"], sc["G"], sc["D"], sc["W"], 16
+    lengths = torch.tensor([sc["lengths"]], dtype=torch.int32)
+    lb = W // P
+    maxp = lb + (int(lengths.max()) + P - 1) // P + 1
+    total = H * lb + int(((lengths + P - 1) // P).sum()) + 4
+    perm = torch.randperm(total - 1 - H * lb, generator=gen) + H * lb
+    table = torch.full((1, H, maxp), total - 1, dtype=torch.int32)
+    table[0, :, :lb] = torch.arange(H * lb, dtype=torch.int32).view(H, lb)
+    at = 0
+    for h in range(H):
+        np_ = (int(lengths[0, h]) + P - 1) // P
+        table[0, h, lb:lb + np_] = perm[at:at + np_].to(torch.int32)
+        at += np_
+    pool_k = torch.randn(total * P, D, generator=gen).to(torch.bfloat16)
+    kmin = torch.zeros(total, D, dtype=torch.bfloat16)
+    kmax = torch.zeros(total, D, dtype=torch.bfloat16)
+    for h in range(H):
+        n = int(lengths[0, h])
+        for p in range((n + P - 1) // P):
+            pg = int(table[0, h, lb + p])
+            rows = pool_k[pg * P:pg * P + min(P, n - p * P)]
+            kmin[pg], kmax[pg] = rows.amin(0), rows.amax(0)
+    qs = [torch.randn(H * G, D, generator=gen).to(torch.bfloat16) for _ in sc["steps"]]
+    if sc["dtype"] == "f32":
+        pool_k, kmin, kmax, qs = pool_k.float(), kmin.float(), kmax.float(), [q.float() for q in qs]
+    return dict(pool_k=pool_k, block_table=table, global_lengths=lengths, key_min=kmin, key_max=kmax, qs=qs,
+                total_blocks=total)
+
+
 def snapkv_state(sc):
     """A dual-cache state for a SnapKV scenario: dict with pool_k, pool_v
     ((total_blocks*16, D); bf16, or fp32 holding bf16 values), block_table

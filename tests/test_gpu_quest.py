@@ -1,15 +1,23 @@
-"""QUEST on the GPU (through the C ABI) against the oracle: page key bounds
-after one-shot prefill, chunked prefill and decode-time promotion are
-bit-exact; the selected pages and token counts equal the oracle's (heads
-whose cut falls within 1e-5 of a tie are reported, not compared); decode
-attention over the selection matches the fp64 attention over the oracle's
-selected pages within max-abs 2e-2 / mean-abs 2e-3."""
+"""QUEST on the GPU (through the C ABI): against the reference's own
+quest_select_blocks (tests/golden/quest_golden.*: bf16 page scores and fp32)
+the token counts, local pages and partial page are exact and the kept full
+pages a valid top-k for the reference's scores (equal up to one bf16 step
+of the cut, where the reference's topk order is unspecified and an fp32 sum
+in another order may round a score to the next bf16 value); against the
+oracle, page key bounds after one-shot prefill, chunked prefill and
+decode-time promotion are bit-exact, the fp32 selection equals the
+oracle's (heads whose cut falls within 1e-5 of a tie are reported, not
+compared), and decode attention over the selection matches the fp64
+attention over the oracle's selected pages within max-abs 2e-2 / mean-abs
+2e-3."""
 import types
 
 import pytest
 import torch
 
+import scenarios
 from oracle import attention, quest
+from test_oracle_quest import check_selection_against_golden, quest_gold
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -109,7 +117,7 @@ def test_selection_matches_oracle(G, D, budget):
     for trial in range(5):
         local = [W, 17, 1][trial % 3]
         q = torch.randn(H * G, D, generator=g).to(torch.bfloat16)
-        sel_len, sel_bt = ops.quest_select(c, 0, q.to(DEV), local, budget)
+        sel_len, sel_bt = ops.quest_select(c, 0, q.to(DEV), local, budget, scores_bf16=False)
         torch.cuda.synchronize()
         o_len, o_blocks = quest.select(hv, 0, q.float(), local, budget, G)
         for h in range(H):
@@ -162,7 +170,8 @@ def test_decode_attention_over_selection():
         # the oracle selection over the cache state this step attended to
         hv = host_view(c)
         local_tokens = min(local_before + 1, W)
-        o_len, o_blocks = quest.select(hv, 0, qi[0, :, 0].float().cpu(), local_tokens, budget, G)
+        # the layer ranks pages by the reference's bf16 scores (equal scores: lowest page first)
+        o_len, o_blocks = quest.select(hv, 0, qi[0, :, 0].float().cpu(), local_tokens, budget, G, scores_bf16=True)
         kc, vc = c.k_cache().cpu().float(), c.v_cache().cpu().float()
         for h in range(H):
             rows_k = kc[o_blocks[h]].reshape(-1, D)[:o_len[h]]
@@ -174,3 +183,29 @@ def test_decode_attention_over_selection():
                 got = out[0, 0, h * G + gi].double().cpu()
                 err = (got - ref).abs()
                 assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3, (step, h, gi, err.max().item())
+
+
+@pytest.mark.parametrize("name", list(scenarios.QUEST_SCENARIOS))
+def test_selection_matches_reference_golden(name):
+    from wgkv import ops
+    z, meta = quest_gold()
+    sc = scenarios.QUEST_SCENARIOS[name]
+    st = scenarios.quest_state(sc)
+    print(f"[quest golden] {name}", flush=True)
+    H, D, W, P = sc["H"], sc["D"], sc["W"], 16
+    c = types.SimpleNamespace(num_layers=1, num_kv_heads=H, head_dim=D, block_size=P, local_window_size=W,
+                              block_table=st["block_table"].to(DEV), global_lengths=st["global_lengths"].to(DEV),
+                              quest_block_key_min=st["key_min"].to(torch.bfloat16).to(DEV),
+                              quest_block_key_max=st["key_max"].to(torch.bfloat16).to(DEV))
+    bf = sc["dtype"] == "bf16"
+    for i, (local, budget) in enumerate(sc["steps"]):
+        q = st["qs"][i].to(torch.bfloat16).to(DEV)
+        sel_len, sel_bt = ops.quest_select(c, 0, q, local, budget, scores_bf16=bf)
+        torch.cuda.synchronize()
+        rows = []
+        budget_blocks = (max(budget - local, 0) + P - 1) // P
+        for h, n in enumerate(sc["lengths"]):
+            count = (local + P - 1) // P + min(budget_blocks, (n + P - 1) // P)
+            rows.append(sel_bt[0, h, :count].cpu().tolist())
+        check_selection_against_golden(z, name, i, sc, st, sel_len[0].cpu().tolist(), rows)
+    print(f"[quest golden] {name}: {len(sc['steps'])} steps, lengths exact, selections equal up to ties", flush=True)

@@ -16,8 +16,10 @@
 //     of the k-th largest score, then a
 //     stable compaction that writes local pages, the kept full pages in page
 //     order and the partial page, and the head's token count.
-// Scores are fp32 (the reference's are bf16 products summed by torch);
-// equal scores at the cut keep the lowest page index.
+// Scores are fp32, or (scores_bf16) rounded as the reference's bf16 torch ops
+// round them: each product q_d * bound_d to bf16, the fp32 sum over d to
+// bf16.  Equal scores at the cut keep the lowest page index (the reference's
+// topk leaves their order unspecified).
 #include "wgkv_common.h"
 
 namespace {
@@ -36,6 +38,7 @@ struct BoundsArgs {
 };
 
 __device__ __forceinline__ float bf(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
+__device__ __forceinline__ float round_bf16f(float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); }
 
 // grid (H, groups): workgroup g of head h takes pages first+g, first+g+groups, ...
 __global__ __launch_bounds__(kThreads) void quest_bounds_kernel(BoundsArgs a) {
@@ -70,7 +73,7 @@ struct SelectArgs {
   const int32_t* len;  // global_lengths + layer * H
   const uint16_t* kmin;
   const uint16_t* kmax;
-  int H, G, D, page, local_tokens, budget;
+  int H, G, D, page, local_tokens, budget, scores_bf16;
   int32_t* sel_bt;     // (H, sel_cap)
   int sel_cap;
   int32_t* sel_len;    // (H)
@@ -109,12 +112,17 @@ __global__ __launch_bounds__(kThreads) void quest_scores_kernel(SelectArgs a) {
         const float u = (e & 1) ? bf16hi(hi[e >> 1]) : bf16lo(hi[e >> 1]);
         for (int g = 0; g < a.G; ++g) {
           const float qd = s_q[g][c * 8 + e];
-          s[g] = fmaf(qd, qd >= 0.f ? u : l, s[g]);
+          const float b = qd >= 0.f ? u : l;
+          // a product of two bf16 values is exact in fp32; bf16 ops round it
+          s[g] = a.scores_bf16 ? s[g] + round_bf16f(qd * b) : fmaf(qd, b, s[g]);
         }
       }
     }
     float best = -INFINITY;
-    for (int g = 0; g < a.G; ++g) best = fmaxf(best, row_sum16(s[g]));
+    for (int g = 0; g < a.G; ++g) {
+      const float v = row_sum16(s[g]);
+      best = fmaxf(best, a.scores_bf16 ? round_bf16f(v) : v);
+    }
     if (ok && lane16 == 0) sc[p] = best;
   }
 }
@@ -247,7 +255,7 @@ extern "C" int wgkv_quest_select(
     const int32_t* block_table, int32_t max_pages_per_head, const int32_t* global_lengths,
     const void* key_min, const void* key_max,
     int32_t layer, int32_t num_layers, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-    int32_t local_window, int32_t page_size, int32_t local_tokens, int32_t token_budget,
+    int32_t local_window, int32_t page_size, int32_t local_tokens, int32_t token_budget, int32_t scores_bf16,
     int32_t* sel_block_table, int32_t sel_cap, int32_t* sel_seqlens,
     void* workspace, size_t workspace_bytes, void* stream) {
   if (!q || !block_table || !global_lengths || !key_min || !key_max || !sel_block_table || !sel_seqlens)
@@ -277,6 +285,7 @@ extern "C" int wgkv_quest_select(
   a.page = page_size;
   a.local_tokens = local_tokens;
   a.budget = token_budget;
+  a.scores_bf16 = scores_bf16 ? 1 : 0;
   a.sel_bt = sel_block_table;
   a.sel_cap = sel_cap;
   a.sel_len = sel_seqlens;

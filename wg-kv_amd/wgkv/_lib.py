@@ -146,7 +146,7 @@ SIGNATURES = {
         c_ptr, c_i32, c_ptr,
         c_ptr, c_ptr,
         c_i32, c_i32, c_i32, c_i32, c_i32,
-        c_i32, c_i32, c_i32, c_i32,
+        c_i32, c_i32, c_i32, c_i32, c_i32,
         c_ptr, c_i32, c_ptr,
         c_ptr, c_size, c_ptr]),
     "wgkv_snapkv_workspace_bytes": (c_i64, [c_i32, c_i32, c_i32, c_i32, c_i32]),

@@ -412,10 +412,11 @@ def quest_update_bounds(cache, layer, from_lengths=None):
     _lib.check(st, "wgkv_quest_update_bounds")
 
 
-def quest_select(cache, layer, q, local_tokens, token_budget):
+def quest_select(cache, layer, q, local_tokens, token_budget, scores_bf16=True):
     """quest_select_blocks (src/modeling_layers.py:452-576) for one decode
-    step of ``layer``: q (Hq, D) bf16.  Returns (cache_seqlens (1, H),
-    block_table (1, H, cap)) for paged_decode_attn."""
+    step of ``layer``: q (Hq, D) bf16.  Page scores are rounded as the
+    reference's bf16 ops round them (``scores_bf16``; False: fp32).  Returns
+    (cache_seqlens (1, H), block_table (1, H, cap)) for paged_decode_attn."""
     H, D = cache.num_kv_heads, cache.head_dim
     P = cache.block_size
     cap = (local_tokens + P - 1) // P + (max(token_budget - local_tokens, 0) + P - 1) // P + 1
@@ -432,7 +433,7 @@ def quest_select(cache, layer, q, local_tokens, token_budget):
         _ptr(cache.block_table), cache.block_table.shape[2], _ptr(cache.global_lengths),
         _ptr(cache.quest_block_key_min), _ptr(cache.quest_block_key_max),
         layer, cache.num_layers, q.shape[0], H, D,
-        cache.local_window_size, P, int(local_tokens), int(token_budget),
+        cache.local_window_size, P, int(local_tokens), int(token_budget), int(bool(scores_bf16)),
         _ptr(sel_bt), cap, _ptr(sel_len),
         _ptr(ws), ws.numel(), _lib.stream_handle(dev))
     _lib.check(st, "wgkv_quest_select")
