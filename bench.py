@@ -226,6 +226,7 @@ def prefill_section(dev, steps, warmup):
     inner = 4 * D
     gate_flop = 2.0 * (2 * D * inner + inner) * S * Hkv
     gate_l1_flop = 2.0 * 2 * D * inner * S * Hkv
+    planes = 1 if w.gate.precision(torch.bfloat16) else 3
     admitted = mask.float().mean().item()
     # the one-shot kernel over the whole prompt, for comparison (same visible set)
     md = wgkv.generate_sparse_indices(mask, W, 1, Hkv, S)
@@ -242,12 +243,15 @@ def prefill_section(dev, steps, warmup):
                         "one_shot_ms": round(t_one, 4),
                         "one_shot_mfma_frac_bf16": round(attn_flop / t_one / 1e9 / BF16_PEAK_TFLOPS, 4),
                         "dense_causal_tflop": round(4.0 * D * Hq * S * (S + 1) / 2 / 1e12, 3)},
-        # bf16 inputs: the first layer runs on the bf16 matrix core over three
-        # weight planes (3 bf16 products per fp32 multiply-add)
+        # bf16 inputs: the first layer runs on the bf16 matrix core -- bf16
+        # parameters (the reference's inference) over one weight plane at the
+        # reference's bf16 rounding points, fp32 parameters over three planes
+        # (3 bf16 products per fp32 multiply-add)
         "gate": {"gflop": round(gate_flop / 1e9, 2), "tflops": round(gate_flop / ms["gate"] / 1e9, 1),
-                 "path": "first layer on bf16 MFMA, weights in 3 bf16 planes",
-                 "bf16_gflop_executed": round(3 * gate_l1_flop / 1e9, 2),
-                 "mfma_frac_bf16": round(3 * gate_l1_flop / ms["gate"] / 1e9 / BF16_PEAK_TFLOPS, 4)},
+                 "parameters": str(w.gate.conv1.weight.dtype).replace("torch.", ""),
+                 "path": f"first layer on bf16 MFMA, weights in {planes} bf16 plane{'s' if planes > 1 else ''}",
+                 "bf16_gflop_executed": round(planes * gate_l1_flop / 1e9, 2),
+                 "mfma_frac_bf16": round(planes * gate_l1_flop / ms["gate"] / 1e9 / BF16_PEAK_TFLOPS, 4)},
     }
 
 
