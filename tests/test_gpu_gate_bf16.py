@@ -76,14 +76,15 @@ def check(label, scores, mask, gold, thr, y=None, clamp=None):
     assert not (flips & ~diff).any()
 
 
-@pytest.mark.parametrize("name", list(scenarios.GATE_BF16_SCENARIOS))
+# few-token inputs (S <= 4) take the few-token kernel either way: one case each
+CASES = [(n, p) for n, sc in scenarios.GATE_BF16_SCENARIOS.items() for p in ((True,) if sc["S"] <= 4 else (True, False))]
+
+
+@pytest.mark.parametrize("name,packed", CASES)
 @pytest.mark.parametrize("fast", [True, False])
-@pytest.mark.parametrize("packed", [True, False])
 def test_bf16_gate_matches_reference_golden(name, fast, packed):
     from wgkv import gate as wgate
     sc = scenarios.GATE_BF16_SCENARIOS[name]
-    if sc["S"] <= 4 and not packed:
-        pytest.skip("few-token inputs take one kernel")
     z = np.load(os.path.join(GOLD, "gate_bf16_golden.npz"))
     params, pre_k, post_k, value = scenarios.gate_inputs_bf16(sc)
     assert scenarios.checksum(pre_k, post_k, value, *params.values()) == bytes(z[f"{name}.inputs_sha256"]).decode()

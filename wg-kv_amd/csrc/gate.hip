@@ -67,9 +67,7 @@ __device__ __forceinline__ float load_in(const GateArgs& a, int i, int b, int h,
   return __uint_as_float((uint32_t)((const uint16_t*)a.in[i])[off] << 16);
 }
 
-__device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float((uint32_t)f32_to_bf16(x) << 16);
-}
+__device__ __forceinline__ float round_bf16(float x) { return round_to_bf16(x); }
 
 __device__ __forceinline__ float gelu_erf(float z) { return 0.5f * z * (1.0f + erff(z * 0.70710678118654752f)); }
 __device__ __forceinline__ float silu(float z) { return z / (1.0f + expf(-z)); }

@@ -38,7 +38,7 @@ struct BoundsArgs {
 };
 
 __device__ __forceinline__ float bf(uint16_t x) { return __uint_as_float((uint32_t)x << 16); }
-__device__ __forceinline__ float round_bf16f(float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); }
+__device__ __forceinline__ float round_bf16f(float x) { return round_to_bf16(x); }
 
 // grid (H, groups): workgroup g of head h takes pages first+g, first+g+groups, ...
 __global__ __launch_bounds__(kThreads) void quest_bounds_kernel(BoundsArgs a) {

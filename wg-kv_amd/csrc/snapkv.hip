@@ -56,7 +56,7 @@ struct SnapArgs {
   int32_t* newp;  // (L*H): global pages kept
 };
 
-__device__ __forceinline__ float round_bf16f(float x) { return __uint_as_float((uint32_t)f32_to_bf16(x) << 16); }
+__device__ __forceinline__ float round_bf16f(float x) { return round_to_bf16(x); }
 
 // The logit of an fp32 product sum: bf16(bf16(acc) * scale) as the
 // reference's bf16 matmul and scalar multiply round, or acc * scale.

@@ -34,6 +34,10 @@ WGKV_DEVICE uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// f32 rounded to the nearest bf16 (ties to even) and widened back: one
+// v_cvt_pk_bf16_f32 and a shift.
+WGKV_DEVICE float round_to_bf16(float x) { return (float)(__bf16)x; }
+
 // ---- DPP row (16-lane) reductions -----------------------------------------
 // quad_perm(1,0,3,2), quad_perm(2,3,0,1), row_half_mirror, row_mirror: after
 // the four steps every lane of a 16-lane row holds the row-wide result.
