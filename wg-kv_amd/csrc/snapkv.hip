@@ -41,7 +41,7 @@ struct SnapArgs {
   int32_t* free_ids;
   int32_t* free_count;
   const uint16_t* qwin;  // (L, win, Hq, D) bf16
-  int L, H, G, D, P, lb, max_pages, total_pages, mtph, win, win_pad, ksz;
+  int L, H, G, D, P, pshift, lb, max_pages, total_pages, mtph, win, win_pad, ksz;
   double ratio;
   float scale;
   int64_t max_cached;
@@ -50,32 +50,48 @@ struct SnapArgs {
   float* scores_out;  // optional pooled scores (L*H, mtph)
   // workspace
   int32_t* meta;  // [0] triggered, [1] free list length before the call
-  float* stats;   // (L*H, G, win_pad, 2): softmax max and sum per query row
+  float* stats;   // (L*H, G, win_pad, 2): softmax max and 1/sum per query row
   float* base;    // (L*H, mtph): unpooled scores
   int32_t* rel;   // (L*H): pages released
   int32_t* newp;  // (L*H): global pages kept
 };
 
-__device__ __forceinline__ float round_bf16f(float x) { return round_to_bf16(x); }
-
-// The logit of an fp32 product sum: bf16(bf16(acc) * scale) as the
-// reference's bf16 matmul and scalar multiply round, or acc * scale.
-__device__ __forceinline__ float logit_of(float acc, const SnapArgs& a) {
-  return a.logits_bf16 ? round_bf16f(round_bf16f(acc) * a.scale) : acc * a.scale;
+// The four logits of an MFMA output fragment of fp32 product sums:
+// bf16(bf16(acc) * scale) as the reference's bf16 matmul and scalar multiply
+// round them (two values per conversion), or acc * scale.
+__device__ __forceinline__ void logits4(const f32x4_t& c, const SnapArgs& a, float (&x)[4]) {
+  if (a.logits_bf16) {
+#pragma unroll
+    for (int i = 0; i < 4; i += 2) {
+      const uint32_t r = pack_bf16x2(c[i], c[i + 1]);
+      const uint32_t y = pack_bf16x2(bf16lo(r) * a.scale, bf16hi(r) * a.scale);
+      x[i] = bf16lo(y);
+      x[i + 1] = bf16hi(y);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = c[i] * a.scale;
+  }
 }
 
 __device__ __forceinline__ int n_evict_of(const SnapArgs& a, int n) { return (int)((double)n * a.ratio); }
 
+// Pool row of logical token i of a head (pages of P = 1 << pshift tokens).
+__device__ __forceinline__ int64_t row_of(const SnapArgs& a, const int32_t* bt, int i) {
+  return ((int64_t)bt[a.lb + (i >> a.pshift)] << a.pshift) + (i & (a.P - 1));
+}
+
 __device__ __forceinline__ const uint16_t* key_row(const SnapArgs& a, const int32_t* bt, int i) {
-  const int pg = bt[a.lb + i / a.P];
-  return a.pool_k + ((int64_t)pg * a.P + i % a.P) * a.D;
+  return a.pool_k + row_of(a, bt, i) * a.D;
 }
 
 // ---- 1: trigger and softmax row statistics ----------------------------------
-// grid (G * win_pad / 64, L*H), 256 threads: wave w of the workgroup takes
-// the 16 windows wb*64 + 16w .. +15 of group member g and streams the head's
-// keys in tiles of 64 (four 16-key MFMA column blocks), keeping per row the
-// running max and the sum of exp2((x - max) * log2 e).
+// grid (G * win_pad / 256, L*H), 256 threads: wave w of the workgroup takes
+// the 64 windows wb*256 + 64w .. +63 of group member g (four 16-row MFMA
+// blocks, the A operands held in registers) and streams the head's keys in
+// tiles of 64 (four 16-key column blocks, each K fragment serving the four
+// row blocks), keeping per row the running max and the sum of
+// exp2((x - max) * log2 e).
 template <int D>
 __global__ __launch_bounds__(256) void snapkv_rowstats_kernel(SnapArgs a) {
   __shared__ int64_t s_sum[4];
@@ -99,79 +115,113 @@ __global__ __launch_bounds__(256) void snapkv_rowstats_kernel(SnapArgs a) {
   const int lh = blockIdx.y;
   const int n = a.global_lengths[lh];
   if (n_evict_of(a, n) == 0) return;
-  const int wblocks = a.win_pad / 64;
+  const int wblocks = a.win_pad / 256;
   const int g = blockIdx.x / wblocks, wb = blockIdx.x - g * wblocks;
-  const int w0 = wb * 64 + wid * 16;
+  const int w0 = wb * 256 + wid * 64;
   if (w0 >= a.win) return;
   const int l = lh / a.H, h = lh - l * a.H;
   const int n16 = lane & 15, kg = lane >> 4;
   constexpr int KS = D / 32;
   const int32_t* bt = a.block_table + (int64_t)lh * a.max_pages;
-  // this lane's A fragments: query row w0 + n16 (rows past the window repeat the last)
-  bf16x8_t q[KS];
-  {
-    const int w = min(w0 + n16, a.win - 1);
+  // A fragments of the four row blocks: query rows w0 + 16rb + n16 (rows past the window repeat the last)
+  bf16x8_t q[4][KS];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int w = min(w0 + rb * 16 + n16, a.win - 1);
     const uint16_t* qrow = a.qwin + (((int64_t)l * a.win + w) * (a.H * a.G) + h * a.G + g) * D + kg * 8;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) q[ks] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + ks * 32));
+    for (int ks = 0; ks < KS; ++ks) q[rb][ks] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + ks * 32));
   }
-  float m[4], s[4];
+  // per lane and row: the running max over this lane's keys and the sum of
+  // exp2((x - max) log2 e) over them; the 16 lanes of a row combine at the end
+  float m[4][4], s[4][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -INFINITY;
-    s[i] = 0.f;
-  }
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      m[rb][i] = -INFINITY;
+      s[rb][i] = 0.f;
+    }
+  // the K fragments of the next tile are loaded while this tile computes
+  u32x4_t bk[4][KS];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const uint16_t* kr = key_row(a, bt, min(k0 + kb * 16 + n16, n - 1)) + kg * 8;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) bk[kb][ks] = *(const u32x4_t*)(kr + ks * 32);
+    }
+  };
+  load_tile(0);
   for (int k0 = 0; k0 < n; k0 += 64) {
-    f32x4_t c[4];
+    f32x4_t c[4][4];  // [row block][key block]
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int key = min(k0 + kb * 16 + n16, n - 1);
-      const uint16_t* kr = key_row(a, bt, key) + kg * 8;
-      c[kb] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        c[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q[ks], __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(kr + ks * 32)),
-                                                        c[kb], 0, 0, 0);
-    }
-    float x[4][4];
+      for (int rb = 0; rb < 4; ++rb) {
+        c[rb][kb] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const bool valid = k0 + kb * 16 + n16 < n;
+        for (int ks = 0; ks < KS; ++ks)
+          c[rb][kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q[rb][ks], __builtin_bit_cast(bf16x8_t, bk[kb][ks]),
+                                                              c[rb][kb], 0, 0, 0);
+      }
+    if (k0 + 64 < n) load_tile(k0 + 64);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[kb][i] = valid ? logit_of(c[kb][i], a) : -INFINITY;
-    }
+    for (int rb = 0; rb < 4; ++rb) {
+      float x[4][4];  // [key block][row]
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mx = fmaxf(fmaxf(x[0][i], x[1][i]), fmaxf(x[2][i], x[3][i]));
-      mx = row_max16(mx);
-      const float mn = fmaxf(m[i], mx);  // finite: every tile holds a valid key
-      float e = 0.f;
+      for (int kb = 0; kb < 4; ++kb) {
+        logits4(c[rb][kb], a, x[kb]);
+        if (k0 + kb * 16 + n16 >= n)
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) e += fast_exp2((x[kb][i] - mn) * kLog2e);
-      e = row_sum16(e);
-      s[i] = s[i] * fast_exp2((m[i] - mn) * kLog2e) + e;
-      m[i] = mn;
-    }
-  }
-  if (n16 == 0) {
+          for (int i = 0; i < 4; ++i) x[kb][i] = -INFINITY;
+      }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int w = w0 + 4 * kg + i;
-      if (w < a.win) {
-        float* st = a.stats + (((int64_t)lh * a.G + g) * a.win_pad + w) * 2;
-        st[0] = m[i];
-        st[1] = s[i];
+      for (int i = 0; i < 4; ++i) {
+        const float mx = fmaxf(fmaxf(x[0][i], x[1][i]), fmaxf(x[2][i], x[3][i]));
+        const float mn = fmaxf(m[rb][i], mx);
+        if (mn == -INFINITY) continue;  // no valid key of this lane yet
+        const float ml = mn * kLog2e;
+        float e = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) e += fast_exp2(fmaf(x[kb][i], kLog2e, -ml));
+        s[rb][i] = fmaf(s[rb][i], fast_exp2(fmaf(m[rb][i], kLog2e, -ml)), e);
+        m[rb][i] = mn;
       }
     }
+  }
+  // combine the 16 lanes of each row: M = max, S = sum of s * exp2((m - M) log2 e)
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float M = row_max16(m[rb][i]);  // finite: key 0 is valid
+      const float part = m[rb][i] == -INFINITY ? 0.f : s[rb][i] * fast_exp2((m[rb][i] - M) * kLog2e);
+      m[rb][i] = M;
+      s[rb][i] = row_sum16(part);
+    }
+  if (n16 == 0) {
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int w = w0 + rb * 16 + 4 * kg + i;
+        if (w < a.win) {
+          float* st = a.stats + (((int64_t)lh * a.G + g) * a.win_pad + w) * 2;
+          st[0] = m[rb][i];
+          st[1] = 1.0f / s[rb][i];
+        }
+      }
   }
 }
 
 // ---- 2: per-key scores ------------------------------------------------------
-// grid (NB, L*H), 256 threads: workgroups stride over the head's 64-key
-// tiles, wave w taking keys tile*64 + 16w .. +15 (the B operand, held in
-// registers); for each 16-window block and group member the MFMA gives the
-// logits, p = exp2((x - max) log2 e) / sum per row, the max over group
-// members, and the sum over windows accumulates per lane.
+// grid (NB, L*H), 256 threads: workgroups stride over the head's 256-key
+// tiles, wave w taking keys tile*256 + 64w .. +63 as four 16-key MFMA column
+// blocks (the B operands, held in registers); for each 16-window block and
+// group member one A fragment (the 16 window queries) serves the four
+// blocks: the logits, p = exp2((x - max) log2 e) / sum per row, the max over
+// group members, and the sum over windows accumulates per lane.
 template <int D>
 __global__ __launch_bounds__(256) void snapkv_scores_kernel(SnapArgs a) {
   if (a.meta[0] == 0) return;
@@ -185,42 +235,56 @@ __global__ __launch_bounds__(256) void snapkv_scores_kernel(SnapArgs a) {
   const int32_t* bt = a.block_table + (int64_t)lh * a.max_pages;
   const int Hq = a.H * a.G;
   const float inv_win = 1.0f / (float)a.win;
-  for (int tile = blockIdx.x; tile * 64 < n; tile += gridDim.x) {
-    const int kbase = tile * 64 + wid * 16;
+  for (int tile = blockIdx.x; tile * 256 < n; tile += gridDim.x) {
+    const int kbase = tile * 256 + wid * 64;
     if (kbase >= n) continue;
-    bf16x8_t bk[KS];
-    {
-      const uint16_t* kr = key_row(a, bt, min(kbase + n16, n - 1)) + kg * 8;
+    bf16x8_t bk[4][KS];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) bk[ks] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(kr + ks * 32));
+    for (int kb = 0; kb < 4; ++kb) {
+      const uint16_t* kr = key_row(a, bt, min(kbase + kb * 16 + n16, n - 1)) + kg * 8;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) bk[kb][ks] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(kr + ks * 32));
     }
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[4][4] = {};
     for (int w0 = 0; w0 < a.win; w0 += 16) {
-      float pmax[4] = {0.f, 0.f, 0.f, 0.f};
+      float pmax[4][4] = {};
       const int wq = min(w0 + n16, a.win - 1);
       for (int g = 0; g < a.G; ++g) {
         const uint16_t* qrow = a.qwin + (((int64_t)l * a.win + wq) * Hq + h * a.G + g) * D + kg * 8;
-        f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+        bf16x8_t q[KS];
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + ks * 32)),
-                                                      bk[ks], c, 0, 0, 0);
+        for (int ks = 0; ks < KS; ++ks) q[ks] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + ks * 32));
         const float* st = a.stats + (((int64_t)lh * a.G + g) * a.win_pad + w0 + 4 * kg) * 2;
+        const f32x4_t s01 = *(const f32x4_t*)st, s23 = *(const f32x4_t*)(st + 4);  // rows 4kg .. 4kg+3 (in win_pad)
+        const float ml[4] = {s01[0] * kLog2e, s01[2] * kLog2e, s23[0] * kLog2e, s23[2] * kLog2e};
+        const float irow[4] = {s01[1], s01[3], s23[1], s23[3]};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (w0 + 4 * kg + i < a.win) {
-            const float p = fast_exp2((logit_of(c[i], a) - st[2 * i]) * kLog2e) / st[2 * i + 1];
-            pmax[i] = fmaxf(pmax[i], p);
+        for (int kb = 0; kb < 4; ++kb) {
+          f32x4_t c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < KS; ++ks) c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(q[ks], bk[kb][ks], c, 0, 0, 0);
+          float x[4];
+          logits4(c, a, x);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(fmaf(x[i], kLog2e, -ml[i])) * irow[i];
+            pmax[kb][i] = w0 + 4 * kg + i < a.win ? fmaxf(pmax[kb][i], p) : 0.f;
           }
         }
       }
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += pmax[i];
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[kb][i] += pmax[kb][i];
     }
-    float tot = (acc[0] + acc[1]) + (acc[2] + acc[3]);
-    tot += __shfl_xor(tot, 16, 64);
-    tot += __shfl_xor(tot, 32, 64);
-    if (kg == 0 && kbase + n16 < n) a.base[(int64_t)lh * a.mtph + kbase + n16] = tot * inv_win;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      float tot = (acc[kb][0] + acc[kb][1]) + (acc[kb][2] + acc[kb][3]);
+      tot += __shfl_xor(tot, 16, 64);
+      tot += __shfl_xor(tot, 32, 64);
+      const int key = kbase + kb * 16 + n16;
+      if (kg == 0 && key < n) a.base[(int64_t)lh * a.mtph + key] = tot * inv_win;
+    }
   }
 }
 
@@ -335,8 +399,8 @@ __global__ __launch_bounds__(kSelectThreads) void snapkv_select_kernel(SnapArgs 
     u32x4_t kv[2][VEC];
     int64_t dst_off = 0;
     if (move) {
-      const int64_t src_off = ((int64_t)bt[a.lb + src_i / a.P] * a.P + src_i % a.P) * D + part * VEC * 8;
-      dst_off = ((int64_t)bt[a.lb + dst_i / a.P] * a.P + dst_i % a.P) * D + part * VEC * 8;
+      const int64_t src_off = row_of(a, bt, src_i) * D + part * VEC * 8;
+      dst_off = row_of(a, bt, dst_i) * D + part * VEC * 8;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) {
         kv[0][e] = *(const u32x4_t*)(a.pool_k + src_off + e * 8);
@@ -395,7 +459,7 @@ struct Layout {
 };
 
 Layout layout(int L, int H, int G, int win, int mtph) {
-  const int64_t LH = (int64_t)L * H, win_pad = (win + 63) / 64 * 64;
+  const int64_t LH = (int64_t)L * H, win_pad = (win + 255) / 256 * 256;
   Layout o;
   o.meta = 0;
   o.stats = 256;
@@ -433,6 +497,7 @@ extern "C" int wgkv_snapkv_evict(
   if ((int64_t)(max_pages - local_pages) * block_size < max_tokens_per_head - (int64_t)local_pages * block_size)
     return WGKV_ERR_ARG;
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
+  if (block_size & (block_size - 1)) return WGKV_ERR_UNSUPPORTED;  // pages of a power of two tokens
   if ((((uintptr_t)pool_k | (uintptr_t)pool_v | (uintptr_t)query_window) & 15) != 0) return WGKV_ERR_UNSUPPORTED;
   const Layout o = layout(num_layers, num_kv_heads, num_kv_groups, window, max_tokens_per_head);
   if (workspace_bytes < o.total || ((uintptr_t)workspace & 255) != 0) return WGKV_ERR_ARG;
@@ -450,12 +515,13 @@ extern "C" int wgkv_snapkv_evict(
   a.G = num_kv_groups;
   a.D = head_dim;
   a.P = block_size;
+  a.pshift = __builtin_ctz((unsigned)block_size);
   a.lb = local_pages;
   a.max_pages = max_pages;
   a.total_pages = total_pages;
   a.mtph = max_tokens_per_head;
   a.win = window;
-  a.win_pad = (window + 63) / 64 * 64;
+  a.win_pad = (window + 255) / 256 * 256;
   a.ksz = kernel_size;
   a.ratio = evict_ratio;
   a.scale = softmax_scale;
@@ -470,9 +536,9 @@ extern "C" int wgkv_snapkv_evict(
   a.newp = (int32_t*)(ws + o.newp);
   hipStream_t st = (hipStream_t)stream;
   const int LH = num_layers * num_kv_heads;
-  const dim3 g1(num_kv_groups * (a.win_pad / 64), LH);
+  const dim3 g1(num_kv_groups * (a.win_pad / 256), LH);
   // scoring workgroups per head: enough to spread a head's tiles over the chip
-  const int tiles = (max_tokens_per_head + 63) / 64;
+  const int tiles = (max_tokens_per_head + 255) / 256;
   const int nb = tiles < 32 ? tiles : 32;
   const dim3 g2(nb, LH);
   if (head_dim == 128) {
