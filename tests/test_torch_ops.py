@@ -61,7 +61,8 @@ def test_pack_meta_size_is_the_library_size(H, D, inner, n_in):
     pk = torch.ops.wgkv.gate_pack_weights(wn, wn, wn, w1, mask, True, H, D, inner)
     assert pk.dtype == torch.uint8 and pk.numel() == wgkv._lib.lib().wgkv_gate_packed_bytes(H, inner, n_in * D, 0)
     pk1 = torch.ops.wgkv.gate_pack_weights(wn, wn, wn, w1, mask, True, H, D, inner, 1)  # bf16 parameters: one plane
-    assert pk1.numel() == wgkv._lib.lib().wgkv_gate_packed_bytes(H, inner, n_in * D, 1) == pk.numel() // 3
+    assert pk1.numel() == wgkv._lib.lib().wgkv_gate_packed_bytes(H, inner, n_in * D, 1)
+    assert pk1.numel() == pk.numel() // 3 + 2 * 2 * 20 * 128 * 2  # plus the two activation tables
     # shapes the packed layout does not take
     assert wgkv._lib.lib().wgkv_gate_packed_bytes(H, 100, 2 * D, 0) == -1
     assert wgkv._lib.lib().wgkv_gate_packed_bytes(H, inner, 48, 0) == -1

@@ -452,6 +452,33 @@ constexpr int kPlanes = 3;
 
 __host__ __device__ constexpr int planes_of(int prec) { return prec ? 1 : kPlanes; }
 
+// With bf16 parameters the activation's input h is a bf16 value and its
+// result is rounded to bf16, so act is a function of h's 16 bits.  The pack
+// step tabulates bf16(act(h)) -- computed by activation() itself, so the
+// table holds exactly what the kernel would compute -- for |h| in
+// [2^-16, 16) (20 binades x 128 mantissas x 2 signs), one table for GELU
+// and one for SiLU after the weight plane; the kernel reads it from LDS and
+// computes the (rare) values outside the range.
+constexpr int kActE0 = 127 - 16;  // biased exponent of 2^-16
+constexpr int kActBinades = 20;
+constexpr int kActTab = 2 * kActBinades * 128;  // entries per activation
+
+__device__ __forceinline__ int act_index(float h) {
+  const uint32_t u = __float_as_uint(h);
+  const int e = (int)((u >> 23) & 0xff) - kActE0;
+  if ((unsigned)e >= (unsigned)kActBinades) return -1;
+  return (int)(u >> 31) * (kActBinades * 128) + e * 128 + (int)((u >> 16) & 127);
+}
+
+__global__ void gate_act_table_kernel(uint16_t* __restrict__ tab) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 2 * kActTab) return;
+  const int act = i / kActTab, j = i - act * kActTab;
+  const int sgn = j / (kActBinades * 128), r = j - sgn * (kActBinades * 128);
+  const uint32_t bits = ((uint32_t)sgn << 31) | ((uint32_t)(kActE0 + r / 128) << 23) | ((uint32_t)(r % 128) << 16);
+  tab[i] = (uint16_t)(__float_as_uint(activation(__uint_as_float(bits), act, 1)) >> 16);
+}
+
 __global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0, const float* wn1,
                                  const float* wn2, int H, int inner, int D, int n_in, int np,
                                  u32x4_t* __restrict__ packed) {
@@ -511,6 +538,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int NLD = 16 / RPL;  // wave loads per input for the wave's 16 tokens
   __shared__ __attribute__((aligned(16))) uint16_t ys[kTok * LDY];
   __shared__ float s_part[4][kTok];
+  __shared__ __attribute__((aligned(16))) uint16_t s_act[PREC ? kActTab : 8];
   if (inactive(a)) return;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int nbh = a.B * a.H;
@@ -518,6 +546,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int bh = lid % nbh, tile = lid / nbh;
   const int b = bh / a.H, h = bh - b * a.H;
   const int s0 = tile * kTok;
+  if (PREC) {  // this activation's table (after the weight plane) -> LDS; read after the barrier below
+    const u32x4_t* tab = (const u32x4_t*)(packed + (int64_t)a.H * (a.inner / 16) * KS * NP * 64) + a.act * (kActTab / 8);
+    for (int i = threadIdx.x; i < kActTab / 8; i += kThreads) ((u32x4_t*)s_act)[i] = tab[i];
+  }
 
   // ---- normalised inputs -> LDS (bf16) ------------------------------------
   {
@@ -587,6 +619,32 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) c[mt][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    if constexpr (NP == 1) {
+      // one plane: the B fragments are requested PD k-steps ahead, so the
+      // weight loads' latency is paid about once per group, not per k-step
+      constexpr int PD = KS < 4 ? KS : 4;
+      u32x4_t bq[KS][4];
+#pragma unroll
+      for (int ks = 0; ks < PD; ++ks)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bq[ks][j] = ph[((int64_t)tj[j] * KS + ks) * 64];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        if (ks + PD < KS)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) bq[ks + PD][j] = ph[((int64_t)tj[j] * KS + ks + PD) * 64];
+        bf16x8_t ax[4];
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          ax[mt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&ys[(mt * 16 + n) * LDY + ks * 32 + kg * 8]));
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            c[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt], __builtin_bit_cast(bf16x8_t, bq[ks][j]), c[mt][j], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);  // keep each k-step's loads in place (registers)
+      }
+    } else {
     u32x4_t bw[4][NP];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -617,6 +675,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
           for (int p = 0; p < NP; ++p) bw[j][p] = bn[j][p];
     }
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       if (t0 + 4 * j >= ntot) break;
@@ -627,7 +686,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float z = layer_out(c[mt][j][i], bias, PREC);
-          logit[mt][i] = fmaf(wo, activation(z, a.act, PREC), logit[mt][i]);
+          float y;
+          if (PREC) {
+            const int ti = act_index(z);
+            y = bf16lo(s_act[ti < 0 ? 0 : ti]);
+            if (ti < 0) y = activation(z, a.act, PREC);
+          } else {
+            y = activation(z, a.act, PREC);
+          }
+          logit[mt][i] = fmaf(wo, y, logit[mt][i]);
         }
     }
   }
@@ -784,7 +851,7 @@ extern "C" int64_t wgkv_gate_packed_bytes(int32_t num_kv_heads, int32_t inner, i
                                           int32_t precision) {
   if (num_kv_heads <= 0 || inner <= 0 || inner % 16 || in_features <= 0 || in_features % 32) return -1;
   if (precision < 0 || precision > 2) return -1;
-  return (int64_t)num_kv_heads * inner * in_features * planes_of(precision) * 2;
+  return (int64_t)num_kv_heads * inner * in_features * planes_of(precision) * 2 + (precision ? 2 * kActTab * 2 : 0);
 }
 
 extern "C" int wgkv_gate_pack_weights(
@@ -810,5 +877,9 @@ extern "C" int wgkv_gate_pack_weights(
   const int blocks = (int)((total + 255) / 256 < 4096 ? (total + 255) / 256 : 4096);
   hipLaunchKernelGGL(gate_pack_kernel, dim3(blocks), dim3(256), 0, (hipStream_t)stream, w1, wn[0], wn[1], wn[2],
                      num_kv_heads, inner, head_dim, n_in, planes_of(precision), (u32x4_t*)packed);
+  if (precision) {  // activation tables after the weight plane
+    uint16_t* tab = (uint16_t*)((char*)packed + (int64_t)num_kv_heads * inner * n_in * head_dim * 2);
+    hipLaunchKernelGGL(gate_act_table_kernel, dim3((2 * kActTab + 255) / 256), dim3(256), 0, (hipStream_t)stream, tab);
+  }
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

@@ -105,7 +105,9 @@ _LIB.impl("generate_sparse_indices", _generate_sparse_indices_meta, "Meta")
 def _gate_pack_meta(w_pre, w_post, w_v, w1, inputs_mask, rms, num_kv_heads, head_dim, inner, precision=0):
     n_in = bin(inputs_mask & 7).count("1")
     planes = 1 if precision else 3
-    return torch.empty(num_kv_heads * inner * n_in * head_dim * planes * 2, dtype=torch.uint8, device=w1.device)
+    tables = 2 * 2 * 20 * 128 * 2 if precision else 0  # bf16 parameters: GELU and SiLU tables after the plane
+    return torch.empty(num_kv_heads * inner * n_in * head_dim * planes * 2 + tables, dtype=torch.uint8,
+                       device=w1.device)
 
 
 _LIB.impl("gate_scores_and_mask", _gate_meta, "Meta")
