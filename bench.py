@@ -228,6 +228,19 @@ def prefill_section(dev, steps, warmup):
     gate_l1_flop = 2.0 * 2 * D * inner * S * Hkv
     planes = 1 if w.gate.precision(torch.bfloat16) else 3
     admitted = mask.float().mean().item()
+    # the same gate with fp32 parameters (fp32 arithmetic and scores), per chunk
+    import copy
+    g32 = copy.deepcopy(w.gate).float()
+    sc32 = torch.empty_like(scores)
+    mk32 = torch.empty_like(mask)
+
+    def gate32():
+        for c0, C in chunks:
+            sl = slice(c0, c0 + C)
+            g32.scores_and_mask(pk[:, :, sl], kk[:, :, sl], None, w.threshold, scores_out=sc32[:, :, sl],
+                                mask_out=mk32[:, :, sl])
+
+    t_gate32 = time_op(gate32, steps, warmup) / len(chunks)
     # the one-shot kernel over the whole prompt, for comparison (same visible set)
     md = wgkv.generate_sparse_indices(mask, W, 1, Hkv, S)
     out1 = torch.empty_like(w.q)
@@ -251,7 +264,8 @@ def prefill_section(dev, steps, warmup):
                  "parameters": str(w.gate.conv1.weight.dtype).replace("torch.", ""),
                  "path": f"first layer on bf16 MFMA, weights in {planes} bf16 plane{'s' if planes > 1 else ''}",
                  "bf16_gflop_executed": round(planes * gate_l1_flop / 1e9, 2),
-                 "mfma_frac_bf16": round(planes * gate_l1_flop / ms["gate"] / 1e9 / BF16_PEAK_TFLOPS, 4)},
+                 "mfma_frac_bf16": round(planes * gate_l1_flop / ms["gate"] / 1e9 / BF16_PEAK_TFLOPS, 4),
+                 "fp32_parameters_ms_per_chunk": round(t_gate32, 4)},
     }
 
 
