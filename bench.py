@@ -97,6 +97,30 @@ def time_op(fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def time_graph(fn, calls=20, replays=10):
+    """Average time of fn() per call with the host out of the way: `calls`
+    calls captured in one HIP graph, replayed `replays` times between HIP
+    events (a batch-1 decode call is shorter than its host-side launch
+    path, so back-to-back stream launches measure the host)."""
+    import torch
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(calls):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (calls * replays)
+
+
 def cpu_baseline(w, budget_s):
     """Oracle decode of whole sequences of the workload on the host cores.
 
@@ -627,9 +651,13 @@ def main():
             m2 = time_op(lambda: wgkv.paged_decode_attn(ws.q, ws.k_cache, ws.v_cache, ws.cache_seqlens,
                                                         ws.block_table, ws.softmax_scale, out=o2),
                          args.steps, args.warmup)
+            mg = time_graph(lambda: wgkv.paged_decode_attn(ws.q, ws.k_cache, ws.v_cache, ws.cache_seqlens,
+                                                           ws.block_table, ws.softmax_scale, out=o2))
             b2 = ws.algorithmic_bytes()
             sec.append({"workload": name, "ms": round(m2, 5), "bytes": b2,
-                        "GB/s": round(b2 / (m2 * 1e-3) / 1e9, 1), "cached_tokens": ws.total_tokens})
+                        "GB/s": round(b2 / (m2 * 1e-3) / 1e9, 1), "cached_tokens": ws.total_tokens,
+                        "ms_graph": round(mg, 5), "GB/s_graph": round(b2 / (mg * 1e-3) / 1e9, 1),
+                        "frac_graph": round(b2 / (mg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
             del ws
         result["secondary"] = sec
     if not args.no_cpu_baseline:
