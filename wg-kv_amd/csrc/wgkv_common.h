@@ -113,21 +113,18 @@ WGKV_DEVICE void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Block-wide exclusive scan of one int per thread (blockDim.x == 256).
-WGKV_DEVICE int block_exclusive_scan_256(int v, int* s_tmp /* >= 256 ints */, int* total) {
-  const int t = threadIdx.x;
-  s_tmp[t] = v;
+// Block-wide exclusive scan of one int per thread (blockDim.x == 256): a
+// wave prefix sum, then the four wave totals through LDS (two barriers).
+WGKV_DEVICE int block_exclusive_scan_256(int v, int* s_tmp /* >= 4 ints */, int* total) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int incl = wave_incl_scan(v, lane);
+  if (lane == 63) s_tmp[w] = incl;
   __syncthreads();
-  for (int off = 1; off < 256; off <<= 1) {
-    int add = t >= off ? s_tmp[t - off] : 0;
-    __syncthreads();
-    s_tmp[t] += add;
-    __syncthreads();
-  }
-  int incl = s_tmp[t];
-  if (total) *total = s_tmp[255];
+  const int t0 = s_tmp[0], t1 = s_tmp[1], t2 = s_tmp[2], t3 = s_tmp[3];
+  const int before = (w > 0 ? t0 : 0) + (w > 1 ? t1 : 0) + (w > 2 ? t2 : 0);
+  if (total) *total = (t0 + t1) + (t2 + t3);
   __syncthreads();
-  return incl - v;
+  return before + incl - v;
 }
 
 #define WGKV_HIP_CHECK(expr)                       \
