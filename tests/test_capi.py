@@ -53,3 +53,37 @@ def test_decode_wrapper_requires_device_tensors():
         wgkv.paged_decode_attn(q, kc, kc, sl, bt, 0.125)
     with pytest.raises(TypeError):
         wgkv.paged_decode_attn(q.float(), kc, kc, sl, bt, 0.125)
+
+
+def test_snapkv_and_gate_argument_checks_without_gpu():
+    """Host-side argument checks of the newer entry points (no HIP call is made)."""
+    import ctypes
+    from wgkv import _lib
+    L = _lib.lib()
+    assert L.wgkv_snapkv_workspace_bytes(2, 8, 4, 256, 1024) > 0
+    assert L.wgkv_snapkv_workspace_bytes(0, 8, 4, 256, 1024) == -1
+    p = ctypes.c_void_p(16)  # never dereferenced: the checks fail first
+
+    def evict(**kw):
+        args = dict(L=2, H=2, G=2, D=64, P=16, lb=4, maxp=40, total=200, mtph=640, win=16, ksz=5, ratio=0.3)
+        args.update(kw)
+        return L.wgkv_snapkv_evict(p, p, p, p, p, p, p, args["L"], args["H"], args["G"], args["D"], args["P"],
+                                   args["lb"], args["maxp"], args["total"], args["mtph"], args["win"], args["ksz"],
+                                   args["ratio"], 0.125, -1, 1, p, None, None, 0, None)
+
+    assert evict() == _lib.ERR_ARG                      # no workspace
+    assert evict(ksz=4) == _lib.ERR_ARG                 # even max-pool kernel (the reference asserts odd)
+    assert evict(ratio=0.0) == _lib.ERR_ARG             # ratio in (0, 1]
+    assert evict(ratio=1.5) == _lib.ERR_ARG
+    assert evict(G=9) == _lib.ERR_ARG
+    # gate: precision outside 0..2, and bf16 parameters with fp32 inputs
+    assert L.wgkv_gate_packed_bytes(8, 512, 256, 3) == -1
+    assert L.wgkv_gate_packed_bytes(8, 512, 256, 1) == 8 * 512 * 256 * 2 + 2 * 2 * 20 * 128 * 2
+
+    def gate(in_dtype, precision):
+        return L.wgkv_gate_scores(p, 0, 0, 0, p, 0, 0, 0, None, 0, 0, 0, in_dtype, 3, p, p, None, p, p, p, p,
+                                  1, 2, 8, 64, 256, 0, 1, precision, 0.0, 0.1, p, 0, 0, None, 0, 0, None,
+                                  None, 0, None, 0, None)
+
+    assert gate(0, 5) == _lib.ERR_ARG
+    assert gate(1, 1) == _lib.ERR_UNSUPPORTED
