@@ -54,7 +54,13 @@ const char* wgkv_status_string(int status);
  * with zero tokens yields zeros.  Supported: D in {64,128}, page_size in
  * {16,32,64}, G = Hq/Hkv in {1,2,3,4,8}, B*Hkv <= 2048.  Split planning happens
  * on the device; out-of-range lengths are clamped to max_pages*page_size and
- * out-of-range page ids to the pool, so no access leaves the buffers.
+ * out-of-range page ids to the pool, so no access leaves the buffers.  One
+ * kernel launch per call: the split partials of a head are merged by its last
+ * chunk to finish.
+ * The workspace (wgkv_paged_decode_workspace_bytes) holds per-head arrival
+ * counters and the split partials: zero-fill it before its first call; every
+ * call leaves the counters zero again.  Calls that share a workspace must be
+ * ordered (one stream, or events between streams).
  * ---------------------------------------------------------------------- */
 size_t wgkv_paged_decode_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t head_dim);
 
@@ -73,14 +79,15 @@ int wgkv_paged_decode_attn(
  * the reference: it is for callers that cannot allocate device memory or
  * pass a workspace (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  Same arguments and results as
- * wgkv_paged_decode_attn minus the workspace; the split partials and plan
- * live in a static device array of the library (12.2 MiB per device, held
- * until the process ends) that covers every supported call (head_dim <= 128,
- * G <= 8, batch*num_kv_heads <= 2048; larger sizes return
+ * wgkv_paged_decode_attn minus the workspace; the arrival counters and split
+ * partials live in a static device array of the library (12.2 MiB per device,
+ * held until the process ends) that covers every supported call (head_dim <=
+ * 128, G <= 8, batch*num_kv_heads <= 2048; larger sizes return
  * WGKV_ERR_UNSUPPORTED).  The array's device address is looked up on the
- * first call on each device.  No entry state needs clearing between calls,
- * but all calls on one device share the array: calls that overlap on one GPU
- * (different streams, no ordering between them) race and must not be made. */
+ * first call on each device, which also zeroes the counters with a small
+ * kernel on the call's stream; every call leaves them zero.  All calls on
+ * one device share the array: calls that overlap on one GPU (different
+ * streams, no ordering between them) race and must not be made. */
 int wgkv_paged_decode_attn_noalloc(
     const void* q, int64_t q_stride_b, int64_t q_stride_h,
     const void* k_cache, const void* v_cache, int64_t num_pages, int32_t page_size,

@@ -184,3 +184,25 @@ def test_many_chunks_batch1():
     torch.cuda.synchronize()
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[0], outs[2])
     run_and_compare(w.q, w.k_cache, w.v_cache, w.cache_seqlens, w.block_table, w.softmax_scale, "beta 128k seed 11")
+
+
+def test_shared_workspace_across_shapes():
+    """The per-head arrival counters live in the one shared workspace: calls
+    that alternate between 12-wave workgroups (batch 1, few heads) and 4-wave
+    ones (B*Hkv >= 32), and between head_dim 128 and 64, each match the
+    oracle, and repeating the first call gives the same bits (every call
+    leaves its counters zero for the next)."""
+    cases = [((32, 8), 128, 16, 1, 30000, 21), ((32, 8), 64, 32, 4, 9000, 22), ((8, 2), 64, 16, 1, 20000, 23),
+             ((16, 4), 128, 64, 8, 6000, 24)]
+    first = None
+    for heads, D, page, B, max_len, seed in cases:
+        q, k, v, sl, bt = reference_grid_case(heads, D, page, B, max_len, num_blocks=1 << 30, seed=seed)
+        out = run_and_compare(q, k, v, sl, bt, D ** -0.5, f"shared workspace B{B} heads{heads} D{D} page{page}")
+        if first is None:
+            first = (out, (q, k, v, sl, bt, D ** -0.5))
+    import wgkv
+    dev = torch.device("cuda:0")
+    q, k, v, sl, bt, scale = first[1]
+    again = wgkv.paged_decode_attn(q.to(dev), k.to(dev), v.to(dev), sl.to(dev), bt.to(dev), scale)
+    torch.cuda.synchronize()
+    assert torch.equal(first[0], again)

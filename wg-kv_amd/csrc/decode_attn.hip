@@ -2,11 +2,14 @@
 //
 // Work split: the logical sequence of every (batch row b, KV head h) is cut
 // into 16-token sub-pages; sub-pages are grouped into chunks of `cp`
-// sub-pages (cp a multiple of 16, chosen on the device so that the whole
-// batch, per-head remainders included, gives about one chunk per resident
-// workgroup slot).  One workgroup (4 waves) owns one chunk, and its waves
-// take 64-token "quads" (4 sub-pages) in turn.  Every K/V byte of the cache
-// is read exactly once, for all G query heads of the KV head together.
+// sub-pages (chosen on the device so that the whole batch, per-head
+// remainders included, gives about one chunk per resident workgroup slot).
+// One workgroup owns one chunk, and its waves take 64-token "quads" (4
+// sub-pages) in turn.  Every K/V byte of the cache is read exactly once, for
+// all G query heads of the KV head together.  Workgroups have 4 waves (three
+// per CU) or, when the batch has few heads (B*Hkv < 32, G <= 4), 12 waves
+// (one per CU), so that a head is cut into ~CUs/(B*Hkv) chunks rather than
+// three times as many.
 //
 // Per quad and wave:
 //   * K is read in the MFMA B-operand layout (lane n%16 = token row, lane/16
@@ -19,21 +22,26 @@
 //     fully coalesced (consecutive 16-byte slices of consecutive rows); P V
 //     runs on v_dot2_f32_bf16 over pairs of rows (P rounded to bf16, fp32
 //     sums).
-// At the end of a chunk the 4 waves merge through LDS.  A single-chunk head
-// writes its output directly; otherwise the chunk stores (m, l, acc)
-// partials that decode_merge_kernel combines with the log-sum-exp rule in
-// chunk order.  (Merging in the split kernel, by the last chunk of a head to
-// arrive, measured slower at batch 1: one workgroup then reads all ~80
-// partials of a head in three dependent rounds of loads, where the merge
-// launch spreads them over G*B*Hkv workgroups and one round.)
+// At the end of a chunk the waves merge through LDS.  A single-chunk head
+// writes its output directly.  Otherwise the chunk stores (m, l, acc)
+// partials, which are combined with the log-sum-exp rule in a fixed chunk
+// order (so the result does not depend on which chunk finishes first):
+//   * 12-wave workgroups: with device-coherent stores; the chunk counts its
+//     arrival on the head's counter, and the last chunk of the head to
+//     arrive merges the head's ~30 partials (one round of loads) and resets
+//     the counter -- one launch per call, ~2 us less at batch 1 than a
+//     second launch;
+//   * 4-wave workgroups: decode_merge_kernel, launched after the split
+//     kernel (at batch 8 the last arriver's write-through stores and
+//     arrival count cost as much as the second launch, which spreads the
+//     merge over B*Hkv*G workgroups).
 #include <mutex>
 
 #include "wgkv_common.h"
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
+constexpr int kPlanThreads = 256;   // plan_block's block scan: 4-wave workgroups
 constexpr int kMaxBH = 2048;
 constexpr int kWaveBH = 64;          // B*Hkv up to this: each wave plans alone, in registers
 constexpr int kMaxSlots = 1024;      // cap on CUs * resident workgroups per CU (workspace sizing)
@@ -42,9 +50,13 @@ constexpr int kMaxG = 8;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 units a running maximum may lag the scores
 
-// Resident workgroups per CU: G <= 4 fits three (158 VGPRs at D=128, G=4),
-// G = 8 (two head groups, 83 KB of LDS) one.
-constexpr int wg_per_cu(int G) { return G > 4 ? 1 : 3; }
+// Resident workgroups per CU: with 4 waves, G <= 4 fits three (158 VGPRs at
+// D=128, G=4), G = 8 (two head groups, 83 KB of LDS) one; a 12-wave
+// workgroup (G <= 4) fills a CU alone (three waves per SIMD).
+constexpr int wg_per_cu(int G, int NW) { return NW > 4 ? 1 : (G > 4 ? 1 : 3); }
+constexpr int waves_per_simd(int G, int NW) { return NW > 4 ? NW / 4 : wg_per_cu(G, NW); }
+// Batches with fewer heads than this (and G <= 4) take 12-wave workgroups.
+constexpr int kWideBelowBH = 32;
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -68,7 +80,12 @@ struct DecodeArgs {
   float* part_m;
   float* part_l;
   float* part_acc;
-  int* plan;  // [B*Hkv + 1] first chunk of each (b,h) and the chunk count, written by the split kernel
+  // arrival counters, one per (b, h): zero before a call, zero after it
+  // (12-wave workgroups)
+  int* counter;
+  // [B*Hkv + 1] first chunk of each (b,h) and the chunk count, written by
+  // the split kernel for decode_merge_kernel (4-wave workgroups)
+  int* plan;
 };
 
 __device__ __forceinline__ int clamped_tokens(const DecodeArgs& a, int bh) {
@@ -89,16 +106,27 @@ struct Plan {
   int cp;        // sub-pages per chunk
 };
 
+// Sub-pages per chunk: the total over the chunk slots, rounded up to a
+// multiple of 16 (4-wave workgroups: at least one quad per wave) or of 4
+// (12-wave workgroups: chunks stay quad-aligned, and the ~CU-count chunks of
+// a batch-1 call fill the CUs evenly), at least 16.
+template <int NW>
+__device__ __forceinline__ int chunk_subpages(int total, int target) {
+  const int cp = (total + target - 1) / target;
+  return NW > 4 ? max(16, (cp + 3) & ~3) : max(16, (cp + 15) & ~15);
+}
+
 // B*Hkv <= 64: lane bh of every wave takes head bh; the plan is two wave
-// scans in registers, no LDS and no barrier.  Workgroup 0 stores the plan
-// (first chunk of each head, then the chunk count) for the merge.
-__device__ Plan plan_wave(const DecodeArgs& a, int w, int* plan_out) {
+// scans in registers, no LDS and no barrier.  With 4-wave workgroups,
+// workgroup 0 stores the plan (first chunk of each head, then the chunk
+// count) for the merge kernel.
+template <int NW>
+__device__ Plan plan_wave(const DecodeArgs& a, int w) {
   const int BH = a.B * a.Hkv;
   const int lane = threadIdx.x & 63;
   const int ns = lane < BH ? (clamped_tokens(a, lane) + 15) >> 4 : 0;
   const int total = __builtin_amdgcn_readlane(wave_incl_scan(ns, lane), 63);
-  int cp = (total + a.target_chunks - 1) / a.target_chunks;
-  cp = max(16, (cp + 15) & ~15);
+  const int cp = chunk_subpages<NW>(total, a.target_chunks);
   const int ch = lane < BH ? max(1, (ns + cp - 1) / cp) : 0;
   const int incl = wave_incl_scan(ch, lane);
   const int excl = incl - ch;
@@ -110,26 +138,25 @@ __device__ Plan plan_wave(const DecodeArgs& a, int w, int* plan_out) {
   p.bh = own ? 63 - __builtin_clzll(own) : 0;
   p.first = __builtin_amdgcn_readlane(excl, p.bh);
   p.n_bh = __builtin_amdgcn_readlane(ch, p.bh);
-  if (w == 0 && threadIdx.x < 64) {
-    if (lane < BH) plan_out[lane] = excl;
-    if (lane == 0) plan_out[BH] = p.n_chunks;
+  if (NW == 4 && w == 0 && threadIdx.x < 64) {
+    if (lane < BH) a.plan[lane] = excl;
+    if (lane == 0) a.plan[BH] = p.n_chunks;
   }
   return p;
 }
 
-// B*Hkv > 64: block scans over the heads through LDS (workgroup 0 stores
-// the plan for the merge).
-__device__ Plan plan_block(const DecodeArgs& a, int w, int* s_pref, int* s_tmp, int* plan_out) {
+// B*Hkv > 64 (4-wave workgroups): block scans over the heads through LDS
+// (workgroup 0 stores the plan for the merge kernel).
+__device__ Plan plan_block(const DecodeArgs& a, int w, int* s_pref, int* s_tmp) {
   const int BH = a.B * a.Hkv;
   const int t = threadIdx.x;
-  const int per = (BH + kThreads - 1) / kThreads;
+  const int per = (BH + kPlanThreads - 1) / kPlanThreads;
   const int lo = min(BH, t * per), hi = min(BH, lo + per);
   int subs = 0;
   for (int bh = lo; bh < hi; ++bh) subs += (clamped_tokens(a, bh) + 15) >> 4;
   int total = 0;
   block_exclusive_scan_256(subs, s_tmp, &total);
-  int cp = (total + a.target_chunks - 1) / a.target_chunks;
-  cp = max(16, (cp + 15) & ~15);
+  const int cp = chunk_subpages<4>(total, a.target_chunks);
   int chunks = 0;
   for (int bh = lo; bh < hi; ++bh) {
     const int ns = (clamped_tokens(a, bh) + 15) >> 4;
@@ -145,7 +172,7 @@ __device__ Plan plan_block(const DecodeArgs& a, int w, int* s_pref, int* s_tmp, 
   if (t == 0) s_pref[BH] = n_chunks;
   __syncthreads();
   if (w == 0)
-    for (int i = t; i <= BH; i += kThreads) plan_out[i] = s_pref[i];
+    for (int i = t; i <= BH; i += kPlanThreads) a.plan[i] = s_pref[i];
   int l = 0, h = BH - 1;  // largest bh with s_pref[bh] <= w
   while (l < h) {
     const int mid = (l + h + 1) >> 1;
@@ -206,24 +233,53 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(wg_per_cu(G), wg_per_cu(G))))
+// Device-coherent accesses to the split partials.  The stores write through
+// to the point of coherence of the whole device and the loads do not return
+// a line that another XCD's writes left stale in this XCD's L2 (agent-scope
+// relaxed atomics: sc1 on gfx950; buffer cache-policy bit 4 for the 16-byte
+// loads).  No L2 writeback or invalidation is needed then: release/acquire
+// fences at device scope write back and invalidate whole L2s, which also
+// drops the K lines the other workgroups of the XCD are reading.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4_t load_coherent4(__amdgpu_buffer_rsrc_t r, int byte_off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 16));
+}
+
+template <int D, int G, int NW>
+__global__ __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(waves_per_simd(G, NW), waves_per_simd(G, NW))))
 void decode_split_kernel(DecodeArgs a) {
+  constexpr int kThreads = NW * 64;
   constexpr int KS = D / 32;       // MFMA k-steps per row
   constexpr int CH = D / 8;        // 16-byte slices per row
   constexpr int RPI = 64 / CH;     // rows per coalesced V load
   constexpr int NV = 64 / RPI;     // V loads per quad
   constexpr int NG = (G + 3) / 4;  // groups of 4 query heads (MFMA A operands)
   static_assert(G <= kMaxG, "query heads per KV head");
+  static_assert(NW == 4 || (NW == 12 && G <= 4), "4-wave workgroups, or 12-wave ones for G <= 4");
 
-  __shared__ int s_pref[kMaxBH + 1];
-  __shared__ int s_tmp[kThreads];
-  __shared__ f32x4_t s_p[kWaves][NG][64];
-  __shared__ __attribute__((aligned(16))) float s_acc[kWaves][RPI][G][D];
-  __shared__ float s_ml[kWaves][2][G];
+  constexpr bool kFused = NW > 4;  // the last chunk of a head merges (see top)
+  // s_buf: each wave's (RPI, G, D) accumulators, then the fused merge's
+  // group partials (kThreads x (m, l, float4 acc))
+  constexpr int kBufFloats = NW * RPI * G * D > (kFused ? kThreads * 6 : 0) ? NW * RPI * G * D : kThreads * 6;
+  __shared__ f32x4_t s_p[NW][NG][64];
+  __shared__ __attribute__((aligned(16))) float s_buf[kBufFloats];
+  __shared__ float s_ml[NW][2][G];
+  __shared__ int s_last;
 
   const int w = blockIdx.x;
-  const Plan pl = a.B * a.Hkv <= kWaveBH ? plan_wave(a, w, a.plan) : plan_block(a, w, s_pref, s_tmp, a.plan);
+  Plan pl;
+  if constexpr (NW == 4) {
+    __shared__ int s_pref[kMaxBH + 1];
+    __shared__ int s_tmp[kPlanThreads];
+    pl = a.B * a.Hkv <= kWaveBH ? plan_wave<NW>(a, w) : plan_block(a, w, s_pref, s_tmp);
+  } else {
+    pl = plan_wave<NW>(a, w);  // the host takes 12 waves only for B*Hkv < 32
+  }
   if (w >= pl.n_chunks) return;
   const int bh = pl.bh;
   const int ci = w - pl.first;
@@ -265,7 +321,7 @@ void decode_split_kernel(DecodeArgs a) {
   }
 
   const int nq = (s1 - s0 + 3) >> 2;
-  for (int jq = wid; jq < nq; jq += kWaves) {
+  for (int jq = wid; jq < nq; jq += NW) {
     const int sp0 = s0 + jq * 4;
     int64_t off[4];
 #pragma unroll
@@ -365,7 +421,7 @@ void decode_split_kernel(DecodeArgs a) {
     wave_lds_sync();
   }
 
-  // ---- merge the 4 waves ---------------------------------------------------
+  // ---- merge the waves -----------------------------------------------------
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const float lw = wave_sum(l_lane[i]);
@@ -375,11 +431,13 @@ void decode_split_kernel(DecodeArgs a) {
     }
   }
   {
+    // s_acc[wid][slot][i][d]: the RPI lanes that hold the same d summed rows
+    // of different V loads
     const int slot = lane / CH, cc = lane % CH;
 #pragma unroll
     for (int i = 0; i < G; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s_acc[wid][slot][i][cc * 8 + e] = acc[i][e];
+      for (int e = 0; e < 8; ++e) s_buf[((wid * RPI + slot) * G + i) * D + cc * 8 + e] = acc[i][e];
   }
   __syncthreads();
 
@@ -388,22 +446,28 @@ void decode_split_kernel(DecodeArgs a) {
     const int i = v / D, d = v - i * D;
     float M = -INFINITY;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, s_ml[ww][0][i]);
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, s_ml[ww][0][i]);
     float L = 0.f, A = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) {
+    for (int ww = 0; ww < NW; ++ww) {
       const float mw = s_ml[ww][0][i];
       if (mw == -INFINITY) continue;
       const float sc = fast_exp2(mw - M);
       float sum = 0.f;
 #pragma unroll
-      for (int sl = 0; sl < RPI; ++sl) sum += s_acc[ww][sl][i][d];
+      for (int sl = 0; sl < RPI; ++sl) sum += s_buf[((ww * RPI + sl) * G + i) * D + d];
       L = fmaf(sc, s_ml[ww][1][i], L);
       A = fmaf(sc, sum, A);
     }
     if (single) {
       const float o = L > 0.f ? A / L : 0.f;
       a.out[(int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + d] = f32_to_bf16(o);
+    } else if constexpr (kFused) {
+      if (d == 0) {
+        store_coherent(&a.part_m[w * G + i], M);
+        store_coherent(&a.part_l[w * G + i], L);
+      }
+      store_coherent(&a.part_acc[((int64_t)w * G + i) * D + d], A);
     } else {
       if (d == 0) {
         a.part_m[w * G + i] = M;
@@ -411,6 +475,89 @@ void decode_split_kernel(DecodeArgs a) {
       }
       a.part_acc[((int64_t)w * G + i) * D + d] = A;
     }
+  }
+  if (single) return;
+  if constexpr (!kFused) return;  // decode_merge_kernel follows
+
+  // ---- the last chunk of the head to arrive merges its partials -------------
+  // Each wave waits for its partial stores to complete (they write through
+  // to the device's point of coherence) before the workgroup counts its
+  // arrival; the last to arrive resets the counter for the next call.
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int prev = __hip_atomic_fetch_add(&a.counter[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = prev == pl.n_bh - 1;
+    if (last) __hip_atomic_store(&a.counter[bh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+
+  // Thread t sums the float4 quad t % NQ of the head's (G, D) output over the
+  // chunks grp, grp + GROUPS, ... of the head (grp = t / NQ), all loads of a
+  // batch issued before the (branch-free) online update consumes them; the
+  // groups are then combined through LDS in group order.  12-wave workgroups
+  // read the ~30 partials of a batch-1 head in one round of loads.
+  constexpr int NQ = G * D / 4;
+  constexpr int GROUPS = kThreads / NQ;
+  constexpr int kBatch = 8;
+  static_assert(GROUPS >= 1, "one float4 quad per thread at least");
+  const int t = threadIdx.x;
+  const int c0 = pl.first, c1 = pl.first + pl.n_bh;
+  const int vq = t % NQ, grp = t / NQ;
+  const int i = (vq * 4) / D;
+  float M = -INFINITY, L = 0.f;
+  f32x4_t A = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  if (grp < GROUPS) {
+    const __amdgpu_buffer_rsrc_t acc_rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(a.part_acc + (int64_t)c0 * G * D, (short)0, 0x7fffffff, 0x00020000);
+    for (int cb = c0 + grp; cb < c1; cb += GROUPS * kBatch) {
+      float mc[kBatch], lc[kBatch];
+      f32x4_t ac[kBatch];
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const int c = min(cb + k * GROUPS, c1 - 1);
+        mc[k] = load_coherent(&a.part_m[c * G + i]);
+        lc[k] = load_coherent(&a.part_l[c * G + i]);
+        ac[k] = load_coherent4(acc_rsrc, ((c - c0) * G * D + vq * 4) * (int)sizeof(float));
+      }
+#pragma unroll
+      for (int k = 0; k < kBatch; ++k) {
+        const bool valid = cb + k * GROUPS < c1 && mc[k] != -INFINITY;
+        const float mn = valid ? fmaxf(M, mc[k]) : M;
+        const float sa = M == -INFINITY ? 0.f : fast_exp2(M - mn);
+        const float sb = valid ? fast_exp2(mc[k] - mn) : 0.f;
+        L = L * sa + lc[k] * sb;
+        A = A * sa + ac[k] * sb;
+        M = mn;
+      }
+    }
+  }
+  // s_buf is free again (read before the arrival barriers): group partials
+  float* s_m = s_buf;
+  float* s_l = s_m + kThreads;
+  f32x4_t* s_a = (f32x4_t*)(s_l + kThreads);
+  s_m[t] = M;
+  s_l[t] = L;
+  s_a[t] = A;
+  __syncthreads();
+  if (t < NQ) {
+    float Mx = -INFINITY;
+    for (int gg = 0; gg < GROUPS; ++gg) Mx = fmaxf(Mx, s_m[gg * NQ + t]);
+    float Lt = 0.f;
+    f32x4_t At = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    for (int gg = 0; gg < GROUPS; ++gg) {
+      const float mg = s_m[gg * NQ + t];
+      if (mg == -INFINITY) continue;
+      const float sc = fast_exp2(mg - Mx);
+      Lt += sc * s_l[gg * NQ + t];
+      At += sc * s_a[gg * NQ + t];
+    }
+    const float inv = Lt > 0.f ? 1.f / Lt : 0.f;
+    uint16_t* o = a.out + (int64_t)b * a.out_sb + (int64_t)(h * G + i) * a.out_sh + (vq * 4 - i * D);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f32_to_bf16(Lt > 0.f ? At[e] * inv : 0.f);
   }
 }
 
@@ -422,7 +569,8 @@ void decode_split_kernel(DecodeArgs a) {
 // LDS in group order.  The plan comes from the split kernel, which ran
 // before on the same stream.
 template <int D, int G>
-__global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int kThreads = 256;
   constexpr int NQ = D / 4;
   constexpr int GROUPS = kThreads / NQ;
   __shared__ f32x4_t s_a[kThreads];
@@ -483,6 +631,12 @@ __global__ __launch_bounds__(kThreads) void decode_merge_kernel(DecodeArgs a) {
   }
 }
 
+// Zeroes the arrival counters of a workspace the library owns (once).
+__global__ void zero_counters_kernel(int* c, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) c[i] = 0;
+}
+
 int cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -495,17 +649,24 @@ int cu_count() {
   return cached[dev];
 }
 
-template <int D, int G>
-hipError_t launch(DecodeArgs a, hipStream_t st) {
+template <int D, int G, int NW>
+hipError_t launch_nw(DecodeArgs a, hipStream_t st) {
   const int BH = a.B * a.Hkv;
-  const int slots = min(kMaxSlots, cu_count() * wg_per_cu(G));
-  a.target_chunks = slots;
+  a.target_chunks = min(kMaxSlots, cu_count() * wg_per_cu(G, NW));
   // the plan makes at most target_chunks + BH chunks (one remainder per head)
-  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(a.target_chunks + BH), dim3(kThreads), 0, st, a);
+  hipLaunchKernelGGL((decode_split_kernel<D, G, NW>), dim3(a.target_chunks + BH), dim3(NW * 64), 0, st, a);
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH, G), dim3(kThreads), 0, st, a);
+  if (NW > 4 || e != hipSuccess) return e;
+  hipLaunchKernelGGL((decode_merge_kernel<D, G>), dim3(BH, G), dim3(256), 0, st, a);
   return hipGetLastError();
+}
+
+template <int D, int G>
+hipError_t launch(const DecodeArgs& a, hipStream_t st) {
+  if constexpr (G <= 4) {
+    if (a.B * a.Hkv < kWideBelowBH) return launch_nw<D, G, 12>(a, st);
+  }
+  return launch_nw<D, G, 4>(a, st);
 }
 
 template <int D>
@@ -519,15 +680,21 @@ hipError_t launch_g(const DecodeArgs& a, int G, hipStream_t st) {
   }
 }
 
+// Workspace layout: the arrival counters (one int per (b, h), at a fixed
+// offset so that calls of either head_dim share them), the partials, then
+// the plan.
+constexpr size_t kCounterBytes = ((size_t)kMaxBH * sizeof(int) + 255) & ~(size_t)255;
 size_t part_floats(int head_dim) { return (size_t)kMaxChunks * kMaxG * (2 + (size_t)head_dim); }
 
 // ---- scratch of the allocation-free entry point ------------------------------
-// The partials and the plan of the largest supported call (head_dim 128, G 8,
-// B*Hkv 2048): 12.2 MiB per device, held until the process ends.  In host
-// code `scratch` names a host-side stand-in; its device address is looked up
-// once per device with hipGetSymbolAddress and only that address is used.
-constexpr size_t kScratchBytes =
-    ((size_t)kMaxChunks * kMaxG * (2 + 128) * sizeof(float) + (size_t)(kMaxBH + 1) * sizeof(int) + 255) & ~(size_t)255;
+// The counters and partials of the largest supported call (head_dim 128,
+// G 8, B*Hkv 2048): 12.2 MiB per device, held until the process ends.  In
+// host code `scratch` names a host-side stand-in; its device address is
+// looked up once per device with hipGetSymbolAddress and only that address
+// is used.
+constexpr size_t kScratchBytes = (kCounterBytes + (size_t)kMaxChunks * kMaxG * (2 + 128) * sizeof(float) +
+                                  (size_t)(kMaxBH + 1) * sizeof(int) + 255) &
+                                 ~(size_t)255;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -536,7 +703,10 @@ void* g_scratch_ptr[kMaxDevices] = {};
 
 // Device address of `scratch` on the device that owns `stream` (the current
 // device for the null stream), resolved on the first call for that device
-// with the device made current for the lookup.
+// with the device made current for the lookup; that first call also zeroes
+// the arrival counters, with a kernel on `stream` (ordered before the call's
+// own launch; a fill kernel rather than a memset node if the stream is being
+// captured).
 int scratch_for_stream(hipStream_t stream, void** out) {
   int dev = -1;
   if (stream) {
@@ -554,6 +724,11 @@ int scratch_for_stream(hipStream_t stream, void** out) {
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (cur != dev && hipSetDevice(cur) != hipSuccess) return WGKV_ERR_HIP;
     if (e != hipSuccess || !p) return WGKV_ERR_HIP;
+    if (cur != dev && hipSetDevice(dev) != hipSuccess) return WGKV_ERR_HIP;
+    hipLaunchKernelGGL(zero_counters_kernel, dim3((kMaxBH + 255) / 256), dim3(256), 0, stream, (int*)p, kMaxBH);
+    const hipError_t ez = hipGetLastError();
+    if (cur != dev && hipSetDevice(cur) != hipSuccess) return WGKV_ERR_HIP;
+    if (ez != hipSuccess) return WGKV_ERR_HIP;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -565,7 +740,7 @@ int scratch_for_stream(hipStream_t stream, void** out) {
 extern "C" size_t wgkv_paged_decode_workspace_bytes(int32_t batch, int32_t num_kv_heads, int32_t head_dim) {
   (void)batch;
   (void)num_kv_heads;
-  return part_floats(head_dim > 0 ? head_dim : 0) * sizeof(float) + (size_t)(kMaxBH + 1) * sizeof(int);
+  return kCounterBytes + part_floats(head_dim > 0 ? head_dim : 0) * sizeof(float) + (size_t)(kMaxBH + 1) * sizeof(int);
 }
 
 extern "C" int wgkv_paged_decode_attn(
@@ -618,7 +793,8 @@ extern "C" int wgkv_paged_decode_attn(
   a.B = batch;
   a.Hkv = num_kv_heads;
   a.scale_log2 = softmax_scale * kLog2e;
-  float* ws = (float*)workspace;
+  a.counter = (int*)workspace;
+  float* ws = (float*)((char*)workspace + kCounterBytes);
   a.part_m = ws;
   a.part_l = ws + (size_t)kMaxChunks * kMaxG;
   a.part_acc = ws + (size_t)kMaxChunks * kMaxG * 2;

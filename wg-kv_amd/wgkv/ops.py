@@ -34,14 +34,15 @@ def workspace(device, nbytes):
 
 
 def decode_workspace(device):
-    """The decode attention's per-device workspace (split partials and the
-    split plan), sized for the largest head_dim so that it never grows and a
-    captured graph's address stays valid."""
+    """The decode attention's per-device workspace (arrival counters and split
+    partials), sized for the largest head_dim so that it never grows and a
+    captured graph's address stays valid.  Zero-filled once: every call
+    leaves its arrival counters zero again."""
     dev, key = _dev_key(device)
     ws = _decode_workspaces.get(key)
     if ws is None:
         nbytes = int(_lib.lib().wgkv_paged_decode_workspace_bytes(1, 1, 128))
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
         _decode_workspaces[key] = ws
     return ws
 
