@@ -654,10 +654,25 @@ def main():
             mg = time_graph(lambda: wgkv.paged_decode_attn(ws.q, ws.k_cache, ws.v_cache, ws.cache_seqlens,
                                                            ws.block_table, ws.softmax_scale, out=o2))
             b2 = ws.algorithmic_bytes()
-            sec.append({"workload": name, "ms": round(m2, 5), "bytes": b2,
-                        "GB/s": round(b2 / (m2 * 1e-3) / 1e9, 1), "cached_tokens": ws.total_tokens,
-                        "ms_graph": round(mg, 5), "GB/s_graph": round(b2 / (mg * 1e-3) / 1e9, 1),
-                        "frac_graph": round(b2 / (mg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)})
+            line = {"workload": name, "ms": round(m2, 5), "bytes": b2,
+                    "GB/s": round(b2 / (m2 * 1e-3) / 1e9, 1), "cached_tokens": ws.total_tokens,
+                    "ms_graph": round(mg, 5), "GB/s_graph": round(b2 / (mg * 1e-3) / 1e9, 1),
+                    "frac_graph": round(b2 / (mg * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+            if name.endswith("128k"):
+                # the same shape over 4 distinct caches in turn (~0.4 GB, more
+                # than the 256 MB Infinity Cache), so that repeated calls
+                # cannot be served from the last call's cached lines
+                rot = [ws] + [workloads.decode_beta(ctx=131072, device=dev, seed=sd) for sd in (1, 2, 3)]
+                outs = [o2] + [torch.empty_like(x.q) for x in rot[1:]]
+                fns = [(lambda x=x, o=o: wgkv.paged_decode_attn(x.q, x.k_cache, x.v_cache, x.cache_seqlens,
+                                                                 x.block_table, x.softmax_scale, out=o))
+                       for x, o in zip(rot, outs)]
+                mr = time_graph(lambda it=iter(range(1 << 30)): fns[next(it) % len(fns)]())
+                br = sum(x.algorithmic_bytes() for x in rot) / len(rot)
+                line["rotating_4_caches"] = {"ms_graph": round(mr, 5), "bytes_avg": int(br),
+                                             "GB/s_graph": round(br / (mr * 1e-3) / 1e9, 1)}
+                del rot, outs, fns
+            sec.append(line)
             del ws
         result["secondary"] = sec
     if not args.no_cpu_baseline:
