@@ -639,7 +639,7 @@ def main():
             "traffic": DECODE_TRAFFIC_BYTES,
             "traffic_source": DECODE_TRAFFIC_SOURCE,
             "bytes_per_launch": nbytes,
-            "launch": "wgkv_paged_decode_attn = decode_split_kernel (merge fused: last chunk of a head)",
+            "launch": "wgkv_paged_decode_attn = decode_split_kernel + decode_merge_kernel (B*Hkv >= 32; fewer heads: one launch, the last chunk of a head merges)",
         },
     }
     if not args.no_secondary:
