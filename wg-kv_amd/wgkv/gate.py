@@ -233,7 +233,9 @@ _DECODE_WS = {}
 def _decode_workspace(device, B, H, inner):
     """Zero-filled workspace of the few-token gate (partial logits and
     per-head counters that each launch leaves at zero), one per device, grown
-    when a call needs more; calls on one stream reuse it in turn."""
+    when a call needs more; calls on one stream reuse it in turn, and calls
+    on different streams that may overlap must not be made (they would share
+    the counters)."""
     need = int(_lib.lib().wgkv_gate_workspace_bytes(B, H, inner))
     ws = _DECODE_WS.get(device)
     if ws is None or ws.numel() < need:

@@ -2,10 +2,13 @@
 
 Each wrapper validates shapes/dtypes on the host, passes raw pointers and
 strides to the C ABI and raises on a non-zero status.  Scratch memory is a
-per-device workspace tensor allocated once and reused; calls on one device
-are ordered by the stream, so sharing it is safe.  A workspace that is
-replaced by a larger one is kept alive (not returned to the caching
-allocator), because a captured HIP graph may still hold its address.
+per-device workspace tensor allocated once and reused by every call on the
+device: calls issued on one stream run in turn, but calls on different
+streams of one device that may run at the same time would share (and
+corrupt) the workspace and must not be made -- the C ABI's rule for its
+workspace arguments.  A workspace that is replaced by a larger one is kept
+alive (not returned to the caching allocator), because a captured HIP graph
+may still hold its address.
 """
 import torch
 
