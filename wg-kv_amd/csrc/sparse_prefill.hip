@@ -214,7 +214,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   // address is that page's (scalar) base plus a 32-bit lane offset.
   const int32_t __attribute__((address_space(4)))* bt_h =
       CHUNK ? (const int32_t __attribute__((address_space(4)))*)(a.bt + (int64_t)h * a.bt_sh) : nullptr;
-  auto tile_idx = [&](int tl, Idx& ix) {
+  auto tile_idx = [&](int tl, Idx& ix) __attribute__((always_inline)) {
     if (tl < n_vtiles) {
       const int nval = min(kBlk, nv - tl * kBlk);
 #pragma unroll
@@ -239,9 +239,56 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     if (CHUNK && x < a.c0) return pool + (a.ring_row0 + (int64_t)h * a.W + (x - (a.c0 - a.W))) * D;
     return tensor_base + (int64_t)(x - (CHUNK ? a.c0 : 0)) * a.kv_ss;
   };
-  auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) {
+  // Chunked mode: a tile that needs no clamping is loaded from a scalar
+  // base plus a 32-bit lane offset -- within a page (admitted columns),
+  // within the ring (band rows before the chunk) or within the chunk's k/v
+  // (band rows of the chunk; 32-bit while 63 rows of the k/v stride fit).
+  // The general path below serves the last admitted tile, the band tile
+  // that straddles the chunk start and the tile that runs past the sequence
+  // end.  This keeps the per-lane 64-bit address arithmetic, which held the
+  // load issue of a tile at ~500 cycles per wave, off the common tiles.
+  auto dma_at = [&](const void* base, uint32_t off, uint16_t* lds) __attribute__((always_inline)) {
+    lds_dma16((const uint16_t*)((const char*)base + off), lds);
+  };
+  auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) __attribute__((always_inline)) {
     const bool vertical = tl < n_vtiles;
     const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
+    if (CHUNK) {
+      const int first = band_start + (tl - n_vtiles) * kBlk;  // band tiles: first key position
+      if (vertical && nval == kBlk) {
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+          const int blk = (wid + i * NW) * 512;
+          const int64_t pg = (int64_t)ix.k[i] * (kPage * D * 2);
+          const uint32_t r = (uint32_t)(krow[i] % kPage) * (D * 2);
+          dma_at((const char*)a.pool_k + pg, r + kcolK[i] * 16, dK + blk);
+          dma_at((const char*)a.pool_v + pg, r + kcolV[i] * 16, dV + blk);
+        }
+        return;
+      }
+      if (!vertical && first + kBlk <= a.c0) {
+        const int64_t row = a.ring_row0 + (int64_t)h * a.W + (first - (a.c0 - a.W));
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+          const int blk = (wid + i * NW) * 512;
+          const uint32_t r = (uint32_t)krow[i] * (D * 2);
+          dma_at(a.pool_k + row * D, r + kcolK[i] * 16, dK + blk);
+          dma_at(a.pool_v + row * D, r + kcolV[i] * 16, dV + blk);
+        }
+        return;
+      }
+      if (!vertical && first >= a.c0 && first + kBlk <= a.S && a.kv_ss <= (1 << 24)) {
+        const int64_t row = (int64_t)(first - a.c0) * a.kv_ss;
+#pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+          const int blk = (wid + i * NW) * 512;
+          const uint32_t r = (uint32_t)krow[i] * (uint32_t)(a.kv_ss * 2);
+          dma_at(kbase + row, r + kcolK[i] * 16, dK + blk);
+          dma_at(vbase + row, r + kcolV[i] * 16, dV + blk);
+        }
+        return;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int kt = min(krow[i], nval - 1);
