@@ -104,6 +104,9 @@ struct PrefillArgs {
   // bt + h*bt_sh, already offset past the local pages), band keys below c0
   // come from the ring (pool row ring_row0 + h*W + p - (c0 - W)).
   int c0, W;  // pages of the global cache are kPage tokens
+  // one-shot mode: every key row of k/v lies within 2^31 bytes of the head's
+  // base, so its byte offset fits 32 bits
+  int off32;
   const uint16_t* pool_k;
   const uint16_t* pool_v;
   const int32_t* bt;
@@ -253,6 +256,17 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) __attribute__((always_inline)) {
     const bool vertical = tl < n_vtiles;
     const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
+    if (!CHUNK && a.off32) {
+      // one-shot mode: every row is k/v row ix.k[i] (clamped when it was looked up)
+#pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const int blk = (wid + i * NW) * 512;
+        const uint32_t r = (uint32_t)ix.k[i] * (uint32_t)(a.kv_ss * 2);
+        dma_at(kbase, r + kcolK[i] * 16, dK + blk);
+        dma_at(vbase, r + kcolV[i] * 16, dV + blk);
+      }
+      return;
+    }
     if (CHUNK) {
       const int first = band_start + (tl - n_vtiles) * kBlk;  // band tiles: first key position
       if (vertical && nval == kBlk) {
@@ -564,6 +578,7 @@ extern "C" int wgkv_sparse_prefill_attn(
   a.scale_log2 = softmax_scale * kLog2e;
   a.c0 = 0;
   a.W = 0;
+  a.off32 = (int64_t)seq_len * kv_ss * 2 <= (int64_t)INT32_MAX;
   a.pool_k = a.pool_v = nullptr;
   a.bt = nullptr;
   a.bt_sh = 0;
