@@ -123,8 +123,12 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   constexpr int NW = 2 * HPW;      // waves
   constexpr int RPB = 64 / CH;     // key rows per 1 KB LDS block (one wave load instruction)
   constexpr int NBLK = kBlk / RPB; // 1 KB blocks per K (or V) tile
-  constexpr int KPT = NBLK / NW;   // blocks per wave and tile
-  static_assert(NBLK % NW == 0, "every wave loads whole 1 KB blocks");
+  // With four heads per workgroup only waves 0-3 load tiles: they are the
+  // older wave of each SIMD, win its issue arbitration and reach the tile
+  // barrier first, so the load issue moves off the younger waves' path.
+  constexpr int NL = HPW == 4 ? NW / 2 : NW;  // loading waves
+  constexpr int KPT = NBLK / NL;   // blocks per loading wave and tile
+  static_assert(NBLK % NL == 0, "every loading wave loads whole 1 KB blocks");
   // double buffers as four distinct LDS objects: the DMA into one buffer
   // provably does not alias the reads of the other, so no wait for the
   // in-flight tile is placed before them
@@ -193,7 +197,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   int krow[KPT], kcolK[KPT], kcolV[KPT];
 #pragma unroll
   for (int i = 0; i < KPT; ++i) {
-    const int row = (wid + i * NW) * RPB + lane / CH;
+    const int row = (wid + i * NL) * RPB + lane / CH;
     krow[i] = row;
     kcolK[i] = (lane % CH) ^ swz_k<D>(row);
     kcolV[i] = (lane % CH) ^ swz_v<D>(row);
@@ -218,12 +222,13 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   const int32_t __attribute__((address_space(4)))* bt_h =
       CHUNK ? (const int32_t __attribute__((address_space(4)))*)(a.bt + (int64_t)h * a.bt_sh) : nullptr;
   auto tile_idx = [&](int tl, Idx& ix) __attribute__((always_inline)) {
+    if (wid >= NL) return;
     if (tl < n_vtiles) {
       const int nval = min(kBlk, nv - tl * kBlk);
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
         if (CHUNK) {
-          const int first = (wid + i * NW) * RPB;  // first row of the block (uniform)
+          const int first = (wid + i * NL) * RPB;  // first row of the block (uniform)
           ix.k[i] = bt_h[(unsigned)(tl * kBlk + min(first, nval - 1)) / kPage];
         } else {
           ix.k[i] = cidx[tl * kBlk + min(krow[i], nval - 1)];
@@ -254,16 +259,19 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
     lds_dma16((const uint16_t*)((const char*)base + off), lds);
   };
   auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) __attribute__((always_inline)) {
+    if (wid >= NL) return;
     const bool vertical = tl < n_vtiles;
     const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
     if (!CHUNK && a.off32) {
       // one-shot mode: every row is k/v row ix.k[i] (clamped when it was looked up)
 #pragma unroll
       for (int i = 0; i < KPT; ++i) {
-        const int blk = (wid + i * NW) * 512;
+        const int blk = (wid + i * NL) * 512;
+        int ck = kcolK[i], cv = kcolV[i];
+        asm volatile("" : "+v"(ck), "+v"(cv));
         const uint32_t r = (uint32_t)ix.k[i] * (uint32_t)(a.kv_ss * 2);
-        dma_at(kbase, r + kcolK[i] * 16, dK + blk);
-        dma_at(vbase, r + kcolV[i] * 16, dV + blk);
+        dma_at(kbase, r + ck * 16, dK + blk);
+        dma_at(vbase, r + cv * 16, dV + blk);
       }
       return;
     }
@@ -272,11 +280,13 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
       if (vertical && nval == kBlk) {
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-          const int blk = (wid + i * NW) * 512;
+          const int blk = (wid + i * NL) * 512;
           const int64_t pg = (int64_t)ix.k[i] * (kPage * D * 2);
-          const uint32_t r = (uint32_t)(krow[i] % kPage) * (D * 2);
-          dma_at((const char*)a.pool_k + pg, r + kcolK[i] * 16, dK + blk);
-          dma_at((const char*)a.pool_v + pg, r + kcolV[i] * 16, dV + blk);
+          int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
+          asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));  // recomputed here, not hoisted out of the loop
+          const uint32_t r = (uint32_t)(kr % kPage) * (D * 2);
+          dma_at((const char*)a.pool_k + pg, r + ck * 16, dK + blk);
+          dma_at((const char*)a.pool_v + pg, r + cv * 16, dV + blk);
         }
         return;
       }
@@ -284,10 +294,12 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
         const int64_t row = a.ring_row0 + (int64_t)h * a.W + (first - (a.c0 - a.W));
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-          const int blk = (wid + i * NW) * 512;
-          const uint32_t r = (uint32_t)krow[i] * (D * 2);
-          dma_at(a.pool_k + row * D, r + kcolK[i] * 16, dK + blk);
-          dma_at(a.pool_v + row * D, r + kcolV[i] * 16, dV + blk);
+          const int blk = (wid + i * NL) * 512;
+          int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
+          asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));
+          const uint32_t r = (uint32_t)kr * (D * 2);
+          dma_at(a.pool_k + row * D, r + ck * 16, dK + blk);
+          dma_at(a.pool_v + row * D, r + cv * 16, dV + blk);
         }
         return;
       }
@@ -295,10 +307,12 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
         const int64_t row = (int64_t)(first - a.c0) * a.kv_ss;
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
-          const int blk = (wid + i * NW) * 512;
-          const uint32_t r = (uint32_t)krow[i] * (uint32_t)(a.kv_ss * 2);
-          dma_at(kbase + row, r + kcolK[i] * 16, dK + blk);
-          dma_at(vbase + row, r + kcolV[i] * 16, dV + blk);
+          const int blk = (wid + i * NL) * 512;
+          int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
+          asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));
+          const uint32_t r = (uint32_t)kr * (uint32_t)(a.kv_ss * 2);
+          dma_at(kbase + row, r + ck * 16, dK + blk);
+          dma_at(vbase + row, r + cv * 16, dV + blk);
         }
         return;
       }
@@ -306,7 +320,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
 #pragma unroll
     for (int i = 0; i < KPT; ++i) {
       const int kt = min(krow[i], nval - 1);
-      const int blk = (wid + i * NW) * 512;  // element offset of this wave's block (1 KB)
+      const int blk = (wid + i * NL) * 512;  // element offset of this wave's block (1 KB)
       if (CHUNK && vertical) {
         // tl * kBlk is a multiple of the page, so the slot is kt % kPage
         const int64_t page_base = (int64_t)ix.k[i] * (kPage * D);
