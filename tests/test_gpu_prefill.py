@@ -87,3 +87,36 @@ def test_long_prompt_sampled_rows(S, W, frac):
     ref = attention.sparse_prefill_rows(q, k, v, gm, W, rows).float()
     err = (out[:, :, rows] - ref).abs()
     assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_wide_kv_span_matches_contiguous(D):
+    """k/v whose rows span more than 2^31 bytes are loaded through the general
+    64-bit address path of the one-shot kernel; the same rows stored densely
+    take the 32-bit lane-offset path.  Both must give the same bits."""
+    import wgkv
+    print(f"[prefill wide span] D{D}", flush=True)
+    dev = torch.device("cuda:0")
+    B, Hkv, G, S, W = 1, 2, 4, 2048, 256
+    q, k, v, gm = make(B, Hkv, G, S, D, 700, seed=97 + D)
+    md = wgkv.generate_sparse_indices(gm.to(dev), W, B, Hkv, S)
+    qd = q.to(dev).transpose(1, 2)
+    kd = k.to(dev).transpose(1, 2).contiguous()  # (B, S, Hkv, D), token stride Hkv * D
+    vd = v.to(dev).transpose(1, 2).contiguous()
+    dense = wgkv.sparse_attn_func(qd, kd, vd, *md, causal=True)
+    T = 1 << 19  # token stride in elements: the rows span S * T * 2 = 2^31 bytes
+    assert S * T * 2 > 2**31 - 1
+    wide = []
+    for src in (kd, vd):
+        buf = torch.empty(B, S, T, dtype=torch.bfloat16, device=dev)
+        view = buf[:, :, :Hkv * D].view(B, S, Hkv, D)
+        view.copy_(src)
+        wide.append(view)
+    assert wide[0].stride(1) == T
+    out = wgkv.sparse_attn_func(qd, wide[0], wide[1], *md, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, dense)
+    mask = meta.ideal_mask(gm.numpy(), W, G)
+    ref64 = attention.masked_prefill(q, k, v, mask).float()
+    err = (out.transpose(1, 2).float().cpu() - ref64).abs()
+    assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
