@@ -188,11 +188,11 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
   const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
 
-  // Tile loading: wave w fills the 1 KB blocks w, w+NW, ... of the K and of
-  // the V tile; in block q, lane i loads key row q*RPB + i/CH, slice
+  // Tile loading: loading wave w fills the 1 KB blocks w, w+NL, ... of the K
+  // and of the V tile; in block q, lane i loads key row q*RPB + i/CH, slice
   // position i%CH, i.e. global slice (i%CH) ^ swz_k(row) for K and
-  // (i%CH) ^ swz_v(row) for V.  The keys of the next tile are looked up one
-  // tile ahead and its rows loaded one tile ahead, so both latencies overlap
+  // (i%CH) ^ swz_v(row) for V.  The keys of the next tile are looked up two
+  // tiles ahead and its rows loaded one tile ahead, so both latencies overlap
   // the current tile's arithmetic.
   int krow[KPT], kcolK[KPT], kcolV[KPT];
 #pragma unroll
