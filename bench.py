@@ -54,6 +54,10 @@ def parse():
                    help="with --e2e: one more eager run per mode that times attention (at this granularity), "
                         "MLP and LM head per phase, as the reference's --profile_attn_mlp --attn_granularity")
     p.add_argument("--e2e-profile-steps", type=int, default=32)
+    p.add_argument("--prefill-long-probe", action="store_true",
+                   help="run only one Llama-8B layer prefilled to 409,600 tokens in 4096-token chunks (30 %% "
+                        "admitted), time the last chunk's attention x5 and a 1 GiB torch copy, for rocprofv3 --pmc "
+                        "FETCH_SIZE passes over a long-context chunk (the copy calibrates the counter)")
     p.add_argument("--traffic-probe", action="store_true",
                    help="run only a 1 GiB torch copy x5 and the config-3 decode x5, for rocprofv3 --pmc "
                         "FETCH_SIZE / WRITE_SIZE passes (the copy calibrates the counters)")
@@ -495,6 +499,68 @@ def layer_section(dev, cpu_budget):
     }
 
 
+def prefill_long_probe(dev):
+    """The last 4096-token chunk of a 409,600-token prompt through one layer:
+    every 64-row block streams its head's ~119K admitted K/V rows, so the
+    chunk shows whether long-context chunks are bound by K/V re-reads (the
+    FETCH_SIZE counter of its kernel, against the bytes the row blocks stream)
+    or by the arithmetic."""
+    import torch
+    from wgkv import ops, workloads
+    from wgkv.cache import DualCache
+    from wgkv.layers import WGKVConfig
+
+    S, Hq, Hkv, D, W, CH = 409600, 32, 8, 128, 1024, 4096
+    w = workloads.prefill_llama(S=S, Hq=Hq, Hkv=Hkv, D=D, W=W, frac=0.3, device=dev)
+    pk, kk = w.pre_k.transpose(1, 2), w.k.transpose(1, 2)
+    mask = torch.empty(1, Hkv, S, dtype=torch.bool, device=dev)
+    scores = torch.empty(1, Hkv, S, dtype=torch.float32, device=dev)
+    out = torch.empty(S, Hq, D, dtype=torch.bfloat16, device=dev)
+    cfg = WGKVConfig(num_hidden_layers=1, num_attention_heads=Hq, num_key_value_heads=Hkv, head_dim=D,
+                     hidden_size=Hq * D, local_window_size=W, max_tokens_per_head=S + W,
+                     max_total_tokens=Hkv * (S + W) + 4096)
+    cache = DualCache()
+    cache.initialize(cfg, D, torch.bfloat16, dev)
+    last = None
+    for c0 in range(0, S, CH):
+        sl = slice(c0, c0 + CH)
+        w.gate.scores_and_mask(pk[:, :, sl], kk[:, :, sl], None, w.threshold, scores_out=scores[:, :, sl],
+                               mask_out=mask[:, :, sl])
+        st = ops.ChunkStep(cache, 0, w.q[0, sl], w.k[0, sl], w.v[0, sl], mask[0, :, sl], c0,
+                           softmax_scale=D ** -0.5, out=out[sl])
+        st.admit()
+        st.attend()
+        st.ring()
+        last = st
+    torch.cuda.synchronize()
+    # visible pairs of the last chunk's rows (the ideal mask, as workloads.visible_pairs)
+    m = mask[0].to(torch.int64)
+    cum = torch.cumsum(m, dim=1)
+    i = torch.arange(S - CH, S, device=dev)
+    start = torch.clamp((i // 64) * 64 - W + 1, min=0)
+    before = cum[:, start - 1]
+    pairs = float(((i - start + 1)[None, :] + before).sum().item())
+    flop = pairs * (Hq // Hkv) * 4 * D
+    streamed = 0.0  # K and V bytes the chunk's 64-row blocks stream (admitted columns + band, per block)
+    for r0 in range(S - CH, S, 64):
+        s0 = max(0, r0 - W + 1)
+        streamed += float(((cum[:, s0 - 1] if s0 > 0 else torch.zeros_like(cum[:, 0])) + (r0 + 64 - s0)).sum().item())
+    streamed *= D * 2 * 2
+    ms = time_op(last.attend, 5, 2)
+    src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    return {"prefill_long_probe": {
+        "workload": "last 4096-token chunk of a 409,600-token prompt, one Llama-8B layer (32 q / 8 KV heads, D 128, "
+                    "W 1024, 30 % admitted)",
+        "admitted_per_head_before_chunk": round(float(m[:, :S - CH].sum(dim=1).float().mean().item())),
+        "attention_ms": round(ms, 4), "tflop": round(flop / 1e12, 3),
+        "mfma_frac_bf16": round(flop / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+        "kv_bytes_streamed_by_row_blocks": int(streamed),
+        "copy_bytes_read": src.numel() * 2}}
+
+
 def e2e_section(args):
     """BASELINE config 5 (the reference's scripts/profiling.py run): a random-
     initialised bf16 Llama-3.1-8B-shaped model, uniform random token ids, the
@@ -597,6 +663,9 @@ def main():
         wgkv.paged_decode_attn(w.q, w.k_cache, w.v_cache, w.cache_seqlens, w.block_table,
                                w.softmax_scale, out=out)
 
+    if args.prefill_long_probe:
+        print(json.dumps(prefill_long_probe(dev)), flush=True)
+        return
     if args.traffic_probe:
         src = torch.ones(1 << 29, dtype=torch.bfloat16, device=dev)  # 1 GiB
         dst = torch.empty_like(src)
