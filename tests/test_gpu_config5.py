@@ -1,8 +1,10 @@
 """BASELINE config 5's model shape on the GPU: a random-initialised bf16
 Llama-3.1-8B-architecture stack (32 layers, hidden 4096, 32 q / 8 KV heads,
 head_dim 128, FFN 14336, vocab 128256) around the write-gated path, an 8K
-prompt in 4096-token chunks (the config's 400K prompt is timed by
-``bench.py --e2e``; the properties checked here do not depend on its length).
+prompt in 4096-token chunks, short enough to replay every layer's cache on
+the CPU oracle (tests/test_gpu_config5_400k.py checks the config's own 400K
+prompt by admitted counts, ring flags, page accounting, decode outputs and
+graph replays).
 
 Checked:
 * gated: every layer's logical cache (global lengths, global K/V in order,
