@@ -52,11 +52,12 @@ const char* wgkv_status_string(int status);
  * sequence (page i of the head = block_table[b,h,i]) are attended by the
  * Hq/Hkv query heads h_kv*G .. h_kv*G+G-1 with softmax(q.k * scale) v.  A head
  * with zero tokens yields zeros.  Supported: D in {64,128}, page_size in
- * {16,32,64}, G = Hq/Hkv in {1,2,3,4,8}, B*Hkv <= 2048.  Split planning happens
+ * {16,32,64}, G = Hq/Hkv in 1..8, B*Hkv <= 2048.  Split planning happens
  * on the device; out-of-range lengths are clamped to max_pages*page_size and
- * out-of-range page ids to the pool, so no access leaves the buffers.  One
- * kernel launch per call: the split partials of a head are merged by its last
- * chunk to finish.
+ * out-of-range page ids to the pool, so no access leaves the buffers.  With
+ * B*Hkv < 32 and G <= 4 a call is one kernel launch (the split partials of a
+ * head are merged by its last chunk to finish); otherwise it is two, the
+ * split kernel and a merge kernel.
  * The workspace (wgkv_paged_decode_workspace_bytes) holds per-head arrival
  * counters and the split partials: zero-fill it before its first call; every
  * call leaves the counters zero again.  Calls that share a workspace must be
@@ -212,6 +213,24 @@ int wgkv_decode_append_ring(
     void* quest_key_min, void* quest_key_max, int32_t* free_ids, int32_t* free_count,
     void* stream);
 
+/* Random admission flags (the random_sparsity ablation).
+ *
+ * Replaces get_random_g_scores (src/modeling_layers.py:1160-1166) where a
+ * decode step uses it: the deferred window refresh (:1177-1178) and the
+ * per-token scores of a decode step.  flags u8 (num_kv_heads, n) with row
+ * stride flags_stride_h: flags[h][i] = r >= bf16(random_sparsity) for a
+ * draw r in [0, 1) (a token is admitted iff its score, 1 or 0, exceeds
+ * g_threshold; so random_sparsity 0 admits every token and 1 none).  The
+ * draws come from a counter-based generator keyed by (seed, *draw_counter,
+ * h, i); each call that runs advances *draw_counter (a device int32) by one,
+ * so eager calls and replays of a captured call continue one sequence.  With
+ * active_flag != NULL the call does nothing unless *active_flag ==
+ * active_value (decided on the device).  One kernel launch; n*num_kv_heads
+ * of any size. */
+int wgkv_random_admission(uint8_t* flags, int64_t flags_stride_h, int32_t num_kv_heads, int32_t n,
+                          float random_sparsity, uint64_t seed, int32_t* draw_counter,
+                          const int32_t* active_flag, int32_t active_value, void* stream);
+
 /* ------------------------------------------------------------------------
  * Write-gate scores and admission flags.
  *
@@ -366,8 +385,9 @@ int wgkv_chunk_cache_update(
 /* q (chunk_len, Hq, D) and out with strides q_ss/q_sh, o_ss/o_sh; the
  * chunk's k/v (chunk_len, Hkv, D) with strides kv_ss/kv_sh; pool_k/pool_v
  * (pages*page_size, D) and block_table (L, Hkv, max_pages_per_head) of the
- * cache, column_count (Hkv, R_c) from stage 0.  Supported: D in {64,128},
- * G in {1,2,4,8}, page_size 16 (the reference's page, :1209-1216). */
+ * cache, column_count (Hkv, R_c) from stage 0.  Supported: D in {32,64,128},
+ * G = Hq/Hkv in 1..8, page_size 16, 32 or 64 (the reference's block_size,
+ * 16 by default, :1209-1216; a page must divide the kernel's 64-key tile). */
 int wgkv_chunk_prefill_attn(
     const void* q, int64_t q_ss, int64_t q_sh,
     const void* k, const void* v, int64_t kv_ss, int64_t kv_sh,

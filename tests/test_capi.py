@@ -87,3 +87,24 @@ def test_snapkv_and_gate_argument_checks_without_gpu():
 
     assert gate(0, 5) == _lib.ERR_ARG
     assert gate(1, 1) == _lib.ERR_UNSUPPORTED
+
+
+def test_random_admission_argument_checks_without_gpu():
+    """wgkv_random_admission rejects bad sizes, a sparsity outside [0, 1] and
+    missing buffers on the host, before any launch (the pointers here are
+    never dereferenced)."""
+    from wgkv import _lib
+    L = _lib.lib()
+    fake = 0x1000
+
+    def call(flags=fake, stride=8, H=2, n=8, p=0.5, counter=fake):
+        return L.wgkv_random_admission(flags, stride, H, n, p, 7, counter, None, 0, None)
+
+    assert call(flags=None) == _lib.ERR_ARG
+    assert call(counter=None) == _lib.ERR_ARG
+    assert call(n=0) == _lib.ERR_ARG
+    assert call(H=0) == _lib.ERR_ARG
+    assert call(stride=4) == _lib.ERR_ARG      # rows overlap
+    assert call(p=-0.1) == _lib.ERR_ARG
+    assert call(p=1.5) == _lib.ERR_ARG
+    assert call(p=float("nan")) == _lib.ERR_ARG

@@ -20,11 +20,11 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def new_cache(L, H, D, W, mtph, defer=False, total_tokens=None):
+def new_cache(L, H, D, W, mtph, defer=False, total_tokens=None, page=16):
     from wgkv.cache import DualCache
     from wgkv.layers import WGKVConfig
     cfg = WGKVConfig(num_hidden_layers=L, num_attention_heads=H, num_key_value_heads=H, head_dim=D,
-                     hidden_size=H * D, local_window_size=W, block_size=16, max_tokens_per_head=mtph,
+                     hidden_size=H * D, local_window_size=W, block_size=page, max_tokens_per_head=mtph,
                      max_total_tokens=total_tokens or L * H * mtph, g_defer=defer)
     c = DualCache()
     c.initialize(cfg, D, torch.bfloat16, DEV)
@@ -72,10 +72,11 @@ def chunked(c, q, k, v, pk, gm, chunks):
 
 
 def global_entries(c, l, h):
-    lb = c.local_window_size // c.block_size
+    P = c.block_size
+    lb = c.local_window_size // P
     n = int(c.global_lengths[l, h])
-    pages = c.block_table[l, h, lb:lb + (n + 15) // 16].long()
-    rows = (pages[:, None] * 16 + torch.arange(16, device=DEV)[None, :]).reshape(-1)[:n]
+    pages = c.block_table[l, h, lb:lb + (n + P - 1) // P].long()
+    rows = (pages[:, None] * P + torch.arange(P, device=DEV)[None, :]).reshape(-1)[:n]
     return c.block_pool_k[rows], c.block_pool_v[rows]
 
 
@@ -127,6 +128,31 @@ def test_chunked_equals_one_shot(L, H, G, D, W, chunks, frac, defer):
     assert_same_logical_cache(a, b)
     if len(chunks) == 1:
         assert torch.equal(a.block_table, b.block_table)  # one chunk = the one-shot allocation
+    for l in range(L):
+        assert torch.equal(got[l], ref[l]), (l, (got[l].float() - ref[l].float()).abs().max().item())
+
+
+@pytest.mark.parametrize("page", [32, 64])
+@pytest.mark.parametrize("L,H,G,D,W,chunks,frac,defer", [
+    (2, 2, 4, 64, 256, [512, 320, 1024, 333], 0.4, False),
+    (1, 4, 8, 128, 1024, [1024, 2048, 1500], 0.2, True),
+    (1, 3, 3, 32, 128, [128, 192, 700], 0.6, False),
+])
+def test_chunked_equals_one_shot_larger_pages(L, H, G, D, W, chunks, frac, defer, page):
+    """32- and 64-token pages (block_size of the reference's config): the
+    chunk kernels address a head's global entries page by page, so a 1 KB
+    block of four entries always lies in one page."""
+    print(f"[chunked prefill] page {page} L{L} H{H} G{G} D{D} W{W} chunks{chunks} admit{frac} defer{defer}",
+          flush=True)
+    S = sum(chunks)
+    q, k, v, pk, gm = make_prompt(L, H, G, S, D, frac, seed=S + W + G + page)
+    mtph = W + S
+    a = new_cache(L, H, D, W, mtph, defer, page=page)
+    ref = one_shot(a, q, k, v, pk, gm, W)
+    b = new_cache(L, H, D, W, mtph, defer, page=page)
+    got = chunked(b, q, k, v, pk, gm, chunks)
+    torch.cuda.synchronize()
+    assert_same_logical_cache(a, b)
     for l in range(L):
         assert torch.equal(got[l], ref[l]), (l, (got[l].float() - ref[l].float()).abs().max().item())
 

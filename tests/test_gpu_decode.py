@@ -137,12 +137,14 @@ def test_handle_matches_direct_call():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("heads", [(6, 2), (12, 4), (16, 2), (64, 8)])
+@pytest.mark.parametrize("heads", [(6, 2), (12, 4), (16, 2), (64, 8), (10, 2), (40, 8), (12, 2), (48, 8), (14, 2),
+                                   (56, 8), (7, 1)])
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("B", [1, 3])
 @pytest.mark.parametrize("max_len", [123, 4000])
-def test_grouped_heads_3_and_8(heads, D, B, max_len):
-    """G = 3 and G = 8 query heads per KV head (two MFMA head groups at G = 8)."""
+def test_grouped_heads_3_and_5_to_8(heads, D, B, max_len):
+    """G = 3 and G = 5..8 query heads per KV head (G > 4: two MFMA head
+    groups, the second partly zero rows for G = 5..7)."""
     q, k, v, sl, bt = reference_grid_case(heads, D, 16, B, max_len, seed=hash((heads, D, B, max_len, 38)) & 0xffff)
     run_and_compare(q, k, v, sl, bt, D ** -0.5, f"G{heads[0] // heads[1]} {heads} D{D} B{B} L{max_len}")
 

@@ -129,23 +129,33 @@ def test_graph_decode_matches_eager(gated, qwen3):
     assert ca.local_ptr == cb.local_ptr and ca.local_length == cb.local_length
 
 
-@pytest.mark.parametrize("defer", [True, False])
-def test_graph_decode_deferred_gating(defer):
+@pytest.mark.parametrize("defer,random_sparsity", [(True, None), (False, None), (True, 0.0), (True, 0.5),
+                                                   (False, 0.5)])
+def test_graph_decode_deferred_gating(defer, random_sparsity):
     """Deferred gating (the reference profiling harness's mode): 150 captured
     decode steps with a 64-token window re-gate each layer's window twice (on
     the steps that write slot 63, decided on the device) and equal the eager
     path -- which tests the slot on the host -- bit for bit: logits, tokens,
     flags, block tables and lengths.  With immediate gating the same run
-    gates every token."""
+    gates every token.  With random_sparsity (the reference's random-admission
+    ablation; 0.0 with g_expand 0 is its "full" recipe) the prompt is admitted
+    by torch.rand draws and the decode steps by the device's counter-based
+    draws, which the graph replays continue exactly as the eager steps."""
     from wgkv import e2e
     from wgkv.cache import DualCache
-    print(f"[e2e] graph decode, g_defer={defer}, 150 steps, W=64", flush=True)
+    print(f"[e2e] graph decode, g_defer={defer}, random_sparsity={random_sparsity}, 150 steps, W=64", flush=True)
     W, S, chunk, n = 64, 640, 256, 150
     m = tiny_model(True, S=S, steps=n, W=W, g_defer=defer)
     ids = torch.randint(0, 1000, (1, S), generator=torch.Generator().manual_seed(5)).to(DEV)
-    e2e.calibrate_gates(m, ids, 0.3, chunk=256)
+    if random_sparsity is None:
+        e2e.calibrate_gates(m, ids, 0.3, chunk=256)
+    else:
+        m.cfg.random_sparsity = random_sparsity
+        if random_sparsity == 0.0:
+            m.cfg.g_expand = 0.0
 
     def prefill():
+        torch.manual_seed(11)  # the prompt's random admission draws (torch.rand)
         c = DualCache()
         logits = None
         for c0 in range(0, S, chunk):
@@ -165,7 +175,10 @@ def test_graph_decode_deferred_gating(defer):
         if defer and not torch.equal(before, ca.local_is_global):
             refreshed += 1
             assert ca.local_ptr == 0, "flags may only change when slot W-1 was written"
-    if defer:
+    if random_sparsity == 0.0:
+        assert bool(ca.local_is_global.all()) and refreshed == 0
+        assert int(ca.global_lengths.min()) == S + n - W  # every token admitted
+    elif defer:
         assert refreshed == 2 and not torch.equal(flags0, ca.local_is_global)
     cb, tok_b = prefill()
     gd = e2e.GraphDecoder(m, cb, tok_b, S, warmup=2)

@@ -688,6 +688,9 @@ hipError_t launch_g(const DecodeArgs& a, int G, hipStream_t st) {
     case 2: return launch<D, 2>(a, st);
     case 3: return launch<D, 3>(a, st);
     case 4: return launch<D, 4>(a, st);
+    case 5: return launch<D, 5>(a, st);
+    case 6: return launch<D, 6>(a, st);
+    case 7: return launch<D, 7>(a, st);
     default: return launch<D, 8>(a, st);
   }
 }
@@ -771,7 +774,7 @@ extern "C" int wgkv_paged_decode_attn(
   if ((int64_t)batch * num_kv_heads > kMaxBH) return WGKV_ERR_UNSUPPORTED;
   const int G = num_q_heads / num_kv_heads;
   if (head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
-  if (G != 1 && G != 2 && G != 3 && G != 4 && G != 8) return WGKV_ERR_UNSUPPORTED;
+  if (G < 1 || G > kMaxG) return WGKV_ERR_UNSUPPORTED;
   int shift;
   if (page_size == 16) shift = 0;
   else if (page_size == 32) shift = 1;

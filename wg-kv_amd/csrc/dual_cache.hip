@@ -11,6 +11,8 @@
 // [(l*H + h)*W/page, ...) -- ring slot s of (l, h) is pool row (l*H + h)*W + s.
 // block_table (L, H, max_pages): local pages first, then global pages in
 // allocation order; unused entries hold the sentinel total_pages-1.
+#include <string.h>
+
 #include "wgkv_common.h"
 
 namespace {
@@ -545,4 +547,67 @@ extern "C" int wgkv_decode_append_ring(
                               advance, do_migrate, do_write, pool_k, pool_v, block_table, max_pages_per_head,
                               global_lengths, local_is_global, local_pre_key, next_free_block, cache_seqlens, status,
                               quest_key_min, quest_key_max, free_ids, free_count, stream);
+}
+
+// ---- random admission (the reference's random_sparsity ablation) -----------
+// get_random_g_scores (src/modeling_layers.py:1160-1166) draws r ~ U[0,1) per
+// token and admits it iff r >= random_sparsity; the deferred refresh applies
+// it to the whole window (:1177-1178).  Here the draws come from a
+// counter-based generator so that a decode step can make them on the device,
+// inside a captured graph, conditioned on a device flag: token (h, i) of draw
+// number c takes the SplitMix64 finaliser (Steele, Lea, Flood, "Fast
+// splittable pseudorandom number generators", OOPSLA 2014) of
+// seed + (c * 2^32 + h * n + i + 1) * golden-ratio increment, and r is its top
+// 24 bits / 2^24.  One workgroup per call: it reads the draw counter, writes
+// the flags, then advances the counter, so consecutive calls draw fresh
+// numbers and replays of a graph continue the same sequence as eager calls.
+namespace {
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(1024) void random_admission_kernel(uint8_t* flags, int64_t f_sh, int H, int n,
+                                                                float cut, uint64_t seed, int32_t* counter,
+                                                                const int32_t* active, int active_value) {
+  if (active != nullptr && *active != active_value) return;
+  __shared__ int s_c;
+  if (threadIdx.x == 0) s_c = *counter;
+  __syncthreads();
+  const uint64_t base = seed + ((uint64_t)(uint32_t)s_c << 32);
+  for (int j = threadIdx.x; j < H * n; j += blockDim.x) {
+    const int h = j / n, i = j - h * n;
+    const uint64_t z = splitmix64(base + (uint64_t)(j + 1) * 0x9E3779B97F4A7C15ull);
+    const float r = (float)(z >> 40) * (1.0f / 16777216.0f);
+    flags[(int64_t)h * f_sh + i] = r >= cut ? 1 : 0;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) *counter = s_c + 1;
+}
+
+// Round-to-nearest-even f32 -> bf16 -> f32 on the host (finite values).
+float host_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+}  // namespace
+
+extern "C" int wgkv_random_admission(uint8_t* flags, int64_t flags_stride_h, int32_t num_kv_heads, int32_t n,
+                                     float random_sparsity, uint64_t seed, int32_t* draw_counter,
+                                     const int32_t* active_flag, int32_t active_value, void* stream) {
+  if (!flags || !draw_counter || num_kv_heads <= 0 || n <= 0 || flags_stride_h < n) return WGKV_ERR_ARG;
+  if (!(random_sparsity >= 0.f && random_sparsity <= 1.f)) return WGKV_ERR_ARG;
+  // the reference compares its bf16 draws with the Python float, which the
+  // comparison rounds to bf16
+  const float cut = host_bf16(random_sparsity);
+  hipLaunchKernelGGL(random_admission_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, flags, flags_stride_h,
+                     num_kv_heads, n, cut, seed, draw_counter, active_flag, active_value);
+  return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }

@@ -29,7 +29,6 @@
 namespace {
 
 constexpr int kBlk = 64;     // query rows per block and keys per tile
-constexpr int kPage = 16;    // cache page (tokens) of the chunked instance
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 units a row maximum may grow before O / l are rescaled
 
@@ -103,7 +102,8 @@ struct PrefillArgs {
   // are logical indices into each head's paged global cache (block table row
   // bt + h*bt_sh, already offset past the local pages), band keys below c0
   // come from the ring (pool row ring_row0 + h*W + p - (c0 - W)).
-  int c0, W;  // pages of the global cache are kPage tokens
+  int c0, W;
+  int page_log2;  // pages of the global cache hold 1 << page_log2 tokens (16, 32 or 64)
   // one-shot mode: every key row of k/v lies within 2^31 bytes of the head's
   // base, so its byte offset fits 32 bits
   int off32;
@@ -217,8 +217,9 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   };
   // In chunked mode the 4 rows of a wave's 1 KB block are 4 consecutive
   // logical entries of the head's global cache, aligned to 4, so they lie in
-  // one 16-token page: the page id is one scalar load per block and the row
-  // address is that page's (scalar) base plus a 32-bit lane offset.
+  // one page (16, 32 or 64 tokens): the page id is one scalar load per block
+  // and the row address is that page's (scalar) base plus a 32-bit lane
+  // offset.
   const int32_t __attribute__((address_space(4)))* bt_h =
       CHUNK ? (const int32_t __attribute__((address_space(4)))*)(a.bt + (int64_t)h * a.bt_sh) : nullptr;
   auto tile_idx = [&](int tl, Idx& ix) __attribute__((always_inline)) {
@@ -229,7 +230,7 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
       for (int i = 0; i < KPT; ++i) {
         if (CHUNK) {
           const int first = (wid + i * NL) * RPB;  // first row of the block (uniform)
-          ix.k[i] = bt_h[(unsigned)(tl * kBlk + min(first, nval - 1)) / kPage];
+          ix.k[i] = bt_h[(unsigned)(tl * kBlk + min(first, nval - 1)) >> a.page_log2];
         } else {
           ix.k[i] = cidx[tl * kBlk + min(krow[i], nval - 1)];
         }
@@ -281,10 +282,11 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
 #pragma unroll
         for (int i = 0; i < KPT; ++i) {
           const int blk = (wid + i * NL) * 512;
-          const int64_t pg = (int64_t)ix.k[i] * (kPage * D * 2);
+          const int64_t pg = ((int64_t)ix.k[i] << a.page_log2) * (D * 2);
           int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
           asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));  // recomputed here, not hoisted out of the loop
-          const uint32_t r = (uint32_t)(kr % kPage) * (D * 2);
+          // tl * kBlk is a multiple of the page, so the row within the page is kr mod page
+          const uint32_t r = (uint32_t)(kr & ((1 << a.page_log2) - 1)) * (D * 2);
           dma_at((const char*)a.pool_k + pg, r + ck * 16, dK + blk);
           dma_at((const char*)a.pool_v + pg, r + cv * 16, dV + blk);
         }
@@ -322,9 +324,9 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
       const int kt = min(krow[i], nval - 1);
       const int blk = (wid + i * NL) * 512;  // element offset of this wave's block (1 KB)
       if (CHUNK && vertical) {
-        // tl * kBlk is a multiple of the page, so the slot is kt % kPage
-        const int64_t page_base = (int64_t)ix.k[i] * (kPage * D);
-        const int lane_row = (kt % kPage) * D;
+        // tl * kBlk is a multiple of the page, so the slot is kt mod page
+        const int64_t page_base = ((int64_t)ix.k[i] << a.page_log2) * D;
+        const int lane_row = (kt & ((1 << a.page_log2) - 1)) * D;
         lds_dma16(a.pool_k + page_base + (lane_row + kcolK[i] * 8), dK + blk);
         lds_dma16(a.pool_v + page_base + (lane_row + kcolV[i] * 8), dV + blk);
       } else {
@@ -592,6 +594,7 @@ extern "C" int wgkv_sparse_prefill_attn(
   a.scale_log2 = softmax_scale * kLog2e;
   a.c0 = 0;
   a.W = 0;
+  a.page_log2 = 4;
   a.off32 = (int64_t)seq_len * kv_ss * 2 <= (int64_t)INT32_MAX;
   a.pool_k = a.pool_v = nullptr;
   a.bt = nullptr;
@@ -615,7 +618,11 @@ extern "C" int wgkv_chunk_prefill_attn(
   if (chunk_len <= 0 || chunk_start < 0 || num_kv_heads <= 0 || num_q_heads % num_kv_heads) return WGKV_ERR_ARG;
   if (local_window <= 0 || local_window % kBlk || chunk_start % kBlk || page_size <= 0 || local_window % page_size)
     return WGKV_ERR_ARG;
-  if (page_size != kPage) return WGKV_ERR_UNSUPPORTED;
+  int page_log2;
+  if (page_size == 16) page_log2 = 4;
+  else if (page_size == 32) page_log2 = 5;
+  else if (page_size == 64) page_log2 = 6;
+  else return WGKV_ERR_UNSUPPORTED;  // pages must divide the 64-key tile
   if (chunk_start > 0 && chunk_start < local_window) return WGKV_ERR_ARG;  // the ring must be full
   const int G = num_q_heads / num_kv_heads;
   if (head_dim != 32 && head_dim != 64 && head_dim != 128) return WGKV_ERR_UNSUPPORTED;
@@ -642,6 +649,7 @@ extern "C" int wgkv_chunk_prefill_attn(
   a.scale_log2 = softmax_scale * kLog2e;
   a.c0 = chunk_start;
   a.W = local_window;
+  a.page_log2 = page_log2;
   a.pool_k = (const uint16_t*)pool_k;
   a.pool_v = (const uint16_t*)pool_v;
   a.bt = block_table + ((int64_t)layer * num_kv_heads) * max_pages_per_head + local_window / page_size;

@@ -93,6 +93,10 @@ SIGNATURES = {
         c_ptr, c_ptr, c_ptr,
         c_ptr, c_ptr, c_ptr, c_ptr,
         c_ptr]),
+    "wgkv_random_admission": (ctypes.c_int, [
+        c_ptr, c_i64, c_i32, c_i32,
+        c_f32, ctypes.c_uint64, c_ptr,
+        c_ptr, c_i32, c_ptr]),
     "wgkv_gate_scores": (ctypes.c_int, [
         c_ptr, c_i64, c_i64, c_i64,
         c_ptr, c_i64, c_i64, c_i64,

@@ -86,6 +86,10 @@ class DualCache:
         self.device_ring = False
         self.next_free_block_dev = torch.full((1,), n_local, **i32)
         self.status = torch.zeros(1, **i32)
+        # random_sparsity ablation: decode-step draws per layer so far (device
+        # counters of the counter-based generator) and its seed
+        self.random_draws = torch.zeros(L, **i32)
+        self.random_seed = int(getattr(config, "random_seed", 0))
         self.cache_seqlens = torch.zeros(L, 1, H, **i32)   # decode lengths, one row per layer
         self.gated_kv_initialized = True
 

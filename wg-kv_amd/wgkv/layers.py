@@ -48,6 +48,8 @@ class WGKVConfig:
     max_total_tokens: Optional[int] = None
     max_tokens_per_head: Optional[int] = None
     random_sparsity: Optional[float] = None
+    # seed of the decode-step random draws (random_sparsity); not a reference field
+    random_seed: int = 0
     g_fast_path: bool = False
     g_defer: bool = False
     use_triton_kernel: bool = False
@@ -83,6 +85,22 @@ def get_random_g_scores(self, batch_size, kv_seq_len, device):
     """src/modeling_layers.py:1160-1166: 1 where U[0,1) >= random_sparsity."""
     r = torch.rand(batch_size, self.config.num_key_value_heads, kv_seq_len, dtype=torch.bfloat16, device=device)
     return (r >= self.config.random_sparsity).to(torch.bfloat16)
+
+
+def decode_random_admission(self, past_key_value, flags, active=None):
+    """A decode step's get_random_g_scores(...) > g_threshold
+    (src/modeling_layers.py:1160-1166 with :1465): flags (H, n) bool <- admit
+    iff r >= random_sparsity, for draws r in [0, 1) made on the device by a
+    counter-based generator (seed ``cache.random_seed``, one counter per
+    layer), so that a captured decode step draws exactly as the eager one.
+    The reference draws with torch.rand; its values cannot be reproduced
+    bit for bit, only the rule.  g_threshold < 1 is assumed, as for every
+    score of 1 to admit."""
+    c = past_key_value
+    if not self.config.g_threshold < 1.0:
+        raise AssertionError("random admission scores are 0 or 1; g_threshold must be below 1")
+    ops.random_admission(flags, self.config.random_sparsity, c.random_seed,
+                         c.random_draws[self.layer_idx:self.layer_idx + 1], active=active)
 
 
 def snapkv_record_queries(self, past_key_value, query_states):
@@ -137,11 +155,11 @@ def refresh_local_is_global(self, past_key_value, device, on_device=False):
     layer = self.layer_idx
     H, W, D = c.num_kv_heads, c.local_window_size, c.head_dim
     if self.config.random_sparsity is not None:
-        if on_device:
-            raise NotImplementedError("deferred gating with random_sparsity draws on the host; "
-                                      "it cannot run with device_ring")
-        g = get_random_g_scores(self, 1, W, device)
-        c.local_is_global[layer] = g[0] > self.config.g_threshold
+        # :1177-1178 -- admitted iff r >= random_sparsity (the score 1 or 0
+        # against g_threshold); the draws are made on the device, so eager
+        # steps and graph replays continue one sequence
+        decode_random_admission(self, c, c.local_is_global[layer],
+                                active=(c.ring_state[2:], W - 1) if on_device else None)
         return
     if self.config.g_expand != 0.0:
         start = layer * H * W
@@ -318,7 +336,12 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
     if cfg.use_baseline:
         g_mask = _all_admitted(batch_size, cfg.num_key_value_heads, kv_seq_len, device)
     elif not (kv_seq_len == 1 and cfg.g_defer):
-        if cfg.random_sparsity is not None:
+        if cfg.random_sparsity is not None and kv_seq_len == 1 and past_key_value is not None \
+                and getattr(past_key_value, "gated_kv_initialized", False):
+            # a decode step's draws on the device (graph-capturable)
+            g_mask = torch.empty(batch_size, cfg.num_key_value_heads, kv_seq_len, dtype=torch.bool, device=device)
+            decode_random_admission(self, past_key_value, g_mask[0])
+        elif cfg.random_sparsity is not None:
             g_scores = get_random_g_scores(self, batch_size, kv_seq_len, device)
         elif cfg.g_expand != 0.0:
             g_scores, g_mask = self.g_predictors.scores_and_mask(pre_key, key_states, value_states, cfg.g_threshold)
@@ -341,6 +364,6 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
 
 
 __all__ = [
-    "WGKVConfig", "DualCache", "get_random_g_scores", "refresh_local_is_global", "migrate_local_kv_to_global",
+    "WGKVConfig", "DualCache", "get_random_g_scores", "decode_random_admission", "refresh_local_is_global", "migrate_local_kv_to_global",
     "prefill_wrapper", "decode_wrapper", "self_attn_forward_patch_inference", "self_attn_forward_patch",
 ]

@@ -254,6 +254,26 @@ def decode_append(cache, layer, key=None, value=None, g_mask=None, pre_key=None,
         _lib.check(st, "wgkv_decode_append")
 
 
+def random_admission(flags, random_sparsity, seed, draw_counter, active=None):
+    """wgkv_random_admission: flags (H, n) bool device tensor (n contiguous)
+    <- r >= bf16(random_sparsity) for counter-based draws r in [0, 1)
+    (get_random_g_scores, src/modeling_layers.py:1160-1166, made on the
+    device); ``draw_counter`` is a device int32 (one element) the call
+    advances; ``active`` = (device int32 tensor, value): the launch does
+    nothing unless the tensor's first element equals value."""
+    if flags.dim() != 2 or flags.dtype != torch.bool or flags.stride(1) != 1:
+        raise AssertionError("flags must be a (H, n) bool tensor with n contiguous")
+    if draw_counter.dtype != torch.int32 or not draw_counter.is_cuda:
+        raise TypeError("draw_counter must be a device int32 tensor")
+    _require_cuda(flags)
+    H, n = flags.shape
+    st = _lib.lib().wgkv_random_admission(
+        _ptr(flags.view(torch.uint8)), flags.stride(0), H, n, float(random_sparsity), int(seed) & (2 ** 64 - 1),
+        _ptr(draw_counter), _ptr(active[0]) if active is not None else None,
+        int(active[1]) if active is not None else 0, _lib.stream_handle(flags.device))
+    _lib.check(st, "wgkv_random_admission")
+
+
 # ---------------------------------------------------------------------------
 # kernel (3): sparse (vertical-slash) causal prefill attention
 # ---------------------------------------------------------------------------
