@@ -567,7 +567,7 @@ def e2e_section(args):
     prompt prefilled in 4096-token chunks, then greedy decode steps; once with
     the learned gate (bias calibrated to admit ``--e2e-admit`` of the first
     chunk per head and layer) and once with every token admitted (the
-    reference's use_baseline run).  Prefill time (TTFT), mean decode step
+    reference's "full" recipe: g_expand 0, random_sparsity 0.0).  Prefill time (TTFT), mean decode step
     (TPOT; each step one replay of a captured HIP graph of the whole model's
     decode step), tokens/s, cached tokens per (layer, head) and KV memory."""
     import torch
@@ -599,13 +599,18 @@ def e2e_section(args):
            "data": "synthetic: random-init bf16 weights, uniform random token ids",
            "gating": ("deferred (g_defer, as scripts/profiling.py:212-213): decode steps re-gate the window "
                       "when its last slot is written" if ec.g_defer else "every token"),
+           "full_run": "g_expand 0, random_sparsity 0.0 (README.md:128-136): every token admitted",
            "decode": "each step one replay of a captured HIP graph of the whole model's step"}
     log("calibrating the gates")
     e2e.calibrate_gates(model, ids, args.e2e_admit)
     # pass-through (phase "warmup") until a run switches them on; graph runs never do
     timers = e2e.install_timing(model, args.e2e_profile) if args.e2e_profile else None
     for name, gated in (("gated", True), ("full", False)):
-        model.cfg.use_baseline = not gated
+        # the full run is the reference's own recipe (README.md:128-136:
+        # --g_expand 0 --random_sparsity 0.0, with g_defer forced on by
+        # profiling.py:211-213): every token admitted by the random rule
+        model.cfg.g_expand = ec.g_expand if gated else 0.0
+        model.cfg.random_sparsity = None if gated else 0.0
         # the gated pool holds the expected admitted share with margin; the full pool every token
         per_head = S + steps + 2 * W if not gated else int(S * min(1.0, 1.5 * args.e2e_admit)) + steps + 2 * W
         model.cfg.max_tokens_per_head = S + steps + 2 * W

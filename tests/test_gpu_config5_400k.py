@@ -16,9 +16,10 @@ Gated run:
   own pages (max-abs 2e-2, mean-abs 2e-3); a second prefill of the same
   prompt decoded by replays of the captured HIP graph gives the eager steps'
   logits and tokens bit for bit.
-Full run (every token admitted): every (layer, head) holds the S - W tokens
-that left the ring, all ring flags are set, and each decode step promotes
-one more token."""
+Full run (the reference's recipe: g_expand 0, random_sparsity 0.0, so every
+token is admitted): every (layer, head) holds the S - W tokens that left the
+ring, all ring flags are set, and each decode step promotes one more
+token."""
 import math
 
 import pytest
@@ -60,7 +61,10 @@ def _size_pool(m, gated):
     W = m.cfg.local_window_size
     L, H = m.cfg.num_hidden_layers, m.cfg.num_key_value_heads
     per_head = S + STEPS + 2 * W if not gated else int(S * min(1.0, 1.5 * ADMIT)) + STEPS + 2 * W
-    m.cfg.use_baseline = not gated
+    # the full run: the reference's recipe (README.md:128-136), every token
+    # admitted by the random rule at random_sparsity 0.0, no gate
+    m.cfg.g_expand = 4.0 if gated else 0.0
+    m.cfg.random_sparsity = None if gated else 0.0
     m.cfg.max_tokens_per_head = S + STEPS + 2 * W
     m.cfg.max_total_tokens = L * H * per_head
 
@@ -242,5 +246,5 @@ def test_config5_400k_full(model):
         say(f"full: every (layer, head) holds the {S - W} tokens that left the ring, then one more per step")
         del cache
     finally:
-        m.cfg.use_baseline = False
+        m.cfg.g_expand, m.cfg.random_sparsity = 4.0, None
         torch.cuda.empty_cache()

@@ -8,8 +8,9 @@ decode step's one-row products run on wgkv_gemv (with the SwiGLU product and
 the residual adds fused).  The prompt is
 prefilled in chunks through the cache's chunk continuation and then decoded
 greedily, as profiling.py does (argmax of the last logits, :146-147).  The
-"full" run admits every token (``use_baseline``, src/modeling_layers.py:1556),
-so the same kernels compute dense causal attention over the whole prefix.
+"full" run admits every token -- ``use_baseline`` (src/modeling_layers.py:1556)
+or the reference's README recipe, g_expand 0 with random_sparsity 0.0 -- so
+the same kernels compute dense causal attention over the whole prefix.
 
 Reported as profiling.py reports (:395-410): prefill time and throughput,
 average tokens per (layer, head) in the cache before and after decoding
