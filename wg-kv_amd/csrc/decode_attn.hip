@@ -488,10 +488,31 @@ void decode_split_kernel(DecodeArgs a) {
   if constexpr (!kFused) return;  // decode_merge_kernel follows
 
   // ---- the last chunk of the head to arrive merges its partials -------------
-  // Each wave waits for its partial stores to complete (they write through
-  // to the device's point of coherence) before the workgroup counts its
-  // arrival; the last to arrive resets the counter for the next call.
+  // Why the partials are visible to the last arriver without release /
+  // acquire fences (this is gfx950 hardware ordering, not the HIP memory
+  // model, whose relaxed atomics order nothing across addresses):
+  //  1. every partial is an agent-scope store (sc1): it is written through
+  //     the XCD's L2 to the device's point of coherence;
+  //  2. on gfx950 stores are counted by vmcnt, which drops only when the
+  //     memory system acknowledges the write, so after vmcnt(0) this wave's
+  //     partials are at the point of coherence;
+  //  3. the barrier holds thread 0's arrival atomic until every wave of the
+  //     workgroup has passed its vmcnt(0);
+  //  4. the arrival counter is an agent-scope atomic, performed at the point
+  //     of coherence, so the workgroup that reads n_bh - 1 comes after every
+  //     other chunk's arrival, hence after all their partial stores;
+  //  5. the last arriver reads the partials with sc1 loads, which are not
+  //     served from a possibly stale copy in its own XCD's L2.
+  // The signal fences are compiler-only barriers: they keep the compiler
+  // from sinking the partial stores below the wait or hoisting the merge's
+  // loads above the arrival.  A device-scope release/acquire pair would
+  // write back and invalidate the whole L2 (1.7x slower in a trial).
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the fused decode merge relies on gfx950 store acknowledgement and sc1 ordering"
+#endif
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __syncthreads();
   if (threadIdx.x == 0) {
     const int prev = __hip_atomic_fetch_add(&a.counter[bh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -501,6 +522,7 @@ void decode_split_kernel(DecodeArgs a) {
   }
   __syncthreads();
   if (!s_last) return;
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 
   // Thread t sums the float4 quad t % NQ of the head's (G, D) output over the
   // chunks grp, grp + GROUPS, ... of the head (grp = t / NQ), all loads of a

@@ -140,390 +140,436 @@ __global__ __launch_bounds__(128 * HPW) void sparse_prefill_kernel(PrefillArgs a
   const int32_t __attribute__((address_space(4)))* bofs =
       (const int32_t __attribute__((address_space(4)))*)a.block_offset;
 
-  const int r = blockIdx.x;
-  const int bh = blockIdx.y;
-  const int b = bh / a.Hkv, h = bh - b * a.Hkv;
   const int t = threadIdx.x;
   const int lane = t & 63, wid = __builtin_amdgcn_readfirstlane(t >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int hq = h * a.G + blockIdx.z * HPW + (wid >> 1);
-  const int lrow0 = r * kBlk + (wid & 1) * 32;   // first query row of this wave (tensor row)
-  const int row0 = (CHUNK ? a.c0 : 0) + lrow0;   // its position
-  const int nrows = a.S - (CHUNK ? a.c0 : 0);    // query rows in the tensors
+  // Persistent workgroups: the grid holds as many workgroups as are resident
+  // at once, and workgroup w serves the items w and, in alternate rounds,
+  // counting from the other end (a snake order).  Items run from the last
+  // row block to the first: a row block sees at least as many admitted
+  // columns and band keys as any earlier one, so the order is heaviest
+  // first and the snake pairs heavy items with light ones -- no second
+  // round of dispatch with a ragged tail.  Within a round consecutive items
+  // are the (sequence, KV head) pairs of one row block, and workgroups are
+  // dealt to the XCDs round-robin, so an XCD serves one KV head per round
+  // (at B*Hkv = 8) and its L2 holds that head's K/V.
+  const int nbh = a.B * a.Hkv;
+  const int nbz = nbh * (a.G / HPW);
+  const int n_items = a.R * nbz;
+  for (int round = 0;; ++round) {
+    const int w = (round & 1) ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int item = round * (int)gridDim.x + w;
+    if (item >= n_items) break;
+    if (round) __syncthreads();  // every wave is done with the previous item's tiles
+    const int rb = item / nbz, rest = item - rb * nbz;
+    const int r = a.R - 1 - rb;
+    const int bh = rest % nbh;
+    const int b = bh / a.Hkv, h = bh - b * a.Hkv;
+    const int hq = h * a.G + (rest / nbh) * HPW + (wid >> 1);
+    const int lrow0 = r * kBlk + (wid & 1) * 32;   // first query row of this wave (tensor row)
+    const int row0 = (CHUNK ? a.c0 : 0) + lrow0;   // its position
+    const int nrows = a.S - (CHUNK ? a.c0 : 0);    // query rows in the tensors
 
-  // queries as the B operand: lane (row n, slice g) of row tile rt, k-step j
-  bf16x8_t qb[2][KS];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int s = min(lrow0 + rt * 16 + n, nrows - 1);
-    const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)s * a.q_ss + (int64_t)hq * a.q_sh;
-#pragma unroll
-    for (int j = 0; j < KS; ++j) qb[rt][j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + (j * 4 + g) * 8));
-  }
-
-  float m_run[2] = {-INFINITY, -INFINITY};
-  // row sums of the (bf16) probabilities, accumulated by the matrix core as
-  // ones . P^T: every entry of lsum[rt] holds the sum of query row rt*16+n
-  f32x4_t lsum[2] = {(f32x4_t){0.f, 0.f, 0.f, 0.f}, (f32x4_t){0.f, 0.f, 0.f, 0.f}};
-  const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
-  f32x4_t o[DT][2];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) o[dt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-
-  const int nv = a.column_count[((int64_t)b * a.Hkv + h) * a.R + r];
-  int nb, band_start = 0;
-  if (CHUNK) {
-    // band of global row block rg: [max(0, rg*64 - W + 1), rg*64 + 64) in 64-key tiles
-    const int rg = a.c0 / kBlk + r;
-    band_start = max(0, rg * kBlk - a.W + 1);
-    nb = (min(rg * kBlk + kBlk, a.S) - band_start + kBlk - 1) / kBlk;
-  } else {
-    nb = a.block_count[r];
-  }
-  const int n_vtiles = (nv + kBlk - 1) / kBlk;
-  const int ntiles = n_vtiles + nb;
-  const int32_t* cidx = a.column_index + (int64_t)b * a.ci_sb + (int64_t)h * a.ci_sh;
-  const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
-  const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
-
-  // Tile loading: loading wave w fills the 1 KB blocks w, w+NL, ... of the K
-  // and of the V tile; in block q, lane i loads key row q*RPB + i/CH, slice
-  // position i%CH, i.e. global slice (i%CH) ^ swz_k(row) for K and
-  // (i%CH) ^ swz_v(row) for V.  The keys of the next tile are looked up two
-  // tiles ahead and its rows loaded one tile ahead, so both latencies overlap
-  // the current tile's arithmetic.
-  int krow[KPT], kcolK[KPT], kcolV[KPT];
-#pragma unroll
-  for (int i = 0; i < KPT; ++i) {
-    const int row = (wid + i * NL) * RPB + lane / CH;
-    krow[i] = row;
-    kcolK[i] = (lane % CH) ^ swz_k<D>(row);
-    kcolV[i] = (lane % CH) ^ swz_v<D>(row);
-  }
-  // A tile's rows are fetched in two stages.  Two tiles ahead, tile_idx
-  // loads the indirections -- the admitted columns' positions or, in chunked
-  // mode, the page ids of the global-cache entries (band rows need none) --
-  // into registers; one tile ahead, tile_load turns them into row addresses
-  // and loads the rows.  Keeping the dependent index loads a tile ahead of
-  // the row loads means no wait for an index also waits for the rows issued
-  // before it (memory counters retire in order).
-  struct Idx {
-    // per item: one-shot mode, the column or band position of the lane's
-    // row; chunked mode, admitted columns, the page id of the wave's 1 KB
-    // block (uniform; band rows need no index in chunked mode)
-    int k[KPT];
-  };
-  // In chunked mode the 4 rows of a wave's 1 KB block are 4 consecutive
-  // logical entries of the head's global cache, aligned to 4, so they lie in
-  // one page (16, 32 or 64 tokens): the page id is one scalar load per block
-  // and the row address is that page's (scalar) base plus a 32-bit lane
-  // offset.
-  const int32_t __attribute__((address_space(4)))* bt_h =
-      CHUNK ? (const int32_t __attribute__((address_space(4)))*)(a.bt + (int64_t)h * a.bt_sh) : nullptr;
-  auto tile_idx = [&](int tl, Idx& ix) __attribute__((always_inline)) {
-    if (wid >= NL) return;
-    if (tl < n_vtiles) {
-      const int nval = min(kBlk, nv - tl * kBlk);
-#pragma unroll
-      for (int i = 0; i < KPT; ++i) {
-        if (CHUNK) {
-          const int first = (wid + i * NL) * RPB;  // first row of the block (uniform)
-          ix.k[i] = bt_h[(unsigned)(tl * kBlk + min(first, nval - 1)) >> a.page_log2];
-        } else {
-          ix.k[i] = cidx[tl * kBlk + min(krow[i], nval - 1)];
-        }
-      }
-    } else if (!CHUNK) {
-      const int b0 = bofs[r * a.bo_width + (tl - n_vtiles)];
-#pragma unroll
-      for (int i = 0; i < KPT; ++i) ix.k[i] = min(b0 + krow[i], a.S - 1);
+    // queries as the B operand: lane (row n, slice g) of row tile rt, k-step j
+    bf16x8_t qb[2][KS];
+  #pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int s = min(lrow0 + rt * 16 + n, nrows - 1);
+      const uint16_t* qrow = a.q + (int64_t)b * a.q_sb + (int64_t)s * a.q_ss + (int64_t)hq * a.q_sh;
+  #pragma unroll
+      for (int j = 0; j < KS; ++j) qb[rt][j] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(qrow + (j * 4 + g) * 8));
     }
-  };
-  // row start of key x of tile tl in the K (or V) source (not the chunked
-  // mode's admitted columns, which tile_load addresses by page)
-  auto row_ptr = [&](bool vertical, int x, const uint16_t* tensor_base, const uint16_t* pool) -> const uint16_t* {
-    if (vertical) return tensor_base + (int64_t)x * a.kv_ss;
-    if (CHUNK && x < a.c0) return pool + (a.ring_row0 + (int64_t)h * a.W + (x - (a.c0 - a.W))) * D;
-    return tensor_base + (int64_t)(x - (CHUNK ? a.c0 : 0)) * a.kv_ss;
-  };
-  // Chunked mode: a tile that needs no clamping is loaded from a scalar
-  // base plus a 32-bit lane offset -- within a page (admitted columns),
-  // within the ring (band rows before the chunk) or within the chunk's k/v
-  // (band rows of the chunk; 32-bit while 63 rows of the k/v stride fit).
-  // The general path below serves the last admitted tile, the band tile
-  // that straddles the chunk start and the tile that runs past the sequence
-  // end.  This keeps the per-lane 64-bit address arithmetic, which held the
-  // load issue of a tile at ~500 cycles per wave, off the common tiles.
-  auto dma_at = [&](const void* base, uint32_t off, uint16_t* lds) __attribute__((always_inline)) {
-    lds_dma16((const uint16_t*)((const char*)base + off), lds);
-  };
-  auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) __attribute__((always_inline)) {
-    if (wid >= NL) return;
-    const bool vertical = tl < n_vtiles;
-    const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
-    if (!CHUNK && a.off32) {
-      // one-shot mode: every row is k/v row ix.k[i] (clamped when it was looked up)
-#pragma unroll
-      for (int i = 0; i < KPT; ++i) {
-        const int blk = (wid + i * NL) * 512;
-        int ck = kcolK[i], cv = kcolV[i];
-        asm volatile("" : "+v"(ck), "+v"(cv));
-        const uint32_t r = (uint32_t)ix.k[i] * (uint32_t)(a.kv_ss * 2);
-        dma_at(kbase, r + ck * 16, dK + blk);
-        dma_at(vbase, r + cv * 16, dV + blk);
-      }
-      return;
-    }
+
+    float m_run[2] = {-INFINITY, -INFINITY};
+    // row sums of the (bf16) probabilities, accumulated by the matrix core as
+    // ones . P^T: every entry of lsum[rt] holds the sum of query row rt*16+n
+    f32x4_t lsum[2] = {(f32x4_t){0.f, 0.f, 0.f, 0.f}, (f32x4_t){0.f, 0.f, 0.f, 0.f}};
+    const bf16x8_t ones = __builtin_bit_cast(bf16x8_t, (u32x4_t){0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+    f32x4_t o[DT][2];
+  #pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+  #pragma unroll
+      for (int rt = 0; rt < 2; ++rt) o[dt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+
+    const int nv = a.column_count[((int64_t)b * a.Hkv + h) * a.R + r];
+    int nb, band_start = 0;
     if (CHUNK) {
-      const int first = band_start + (tl - n_vtiles) * kBlk;  // band tiles: first key position
-      if (vertical && nval == kBlk) {
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-          const int blk = (wid + i * NL) * 512;
-          const int64_t pg = ((int64_t)ix.k[i] << a.page_log2) * (D * 2);
-          int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
-          asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));  // recomputed here, not hoisted out of the loop
-          // tl * kBlk is a multiple of the page, so the row within the page is kr mod page
-          const uint32_t r = (uint32_t)(kr & ((1 << a.page_log2) - 1)) * (D * 2);
-          dma_at((const char*)a.pool_k + pg, r + ck * 16, dK + blk);
-          dma_at((const char*)a.pool_v + pg, r + cv * 16, dV + blk);
-        }
-        return;
-      }
-      if (!vertical && first + kBlk <= a.c0) {
-        const int64_t row = a.ring_row0 + (int64_t)h * a.W + (first - (a.c0 - a.W));
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-          const int blk = (wid + i * NL) * 512;
-          int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
-          asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));
-          const uint32_t r = (uint32_t)kr * (D * 2);
-          dma_at(a.pool_k + row * D, r + ck * 16, dK + blk);
-          dma_at(a.pool_v + row * D, r + cv * 16, dV + blk);
-        }
-        return;
-      }
-      if (!vertical && first >= a.c0 && first + kBlk <= a.S && a.kv_ss <= (1 << 24)) {
-        const int64_t row = (int64_t)(first - a.c0) * a.kv_ss;
-#pragma unroll
-        for (int i = 0; i < KPT; ++i) {
-          const int blk = (wid + i * NL) * 512;
-          int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
-          asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));
-          const uint32_t r = (uint32_t)kr * (uint32_t)(a.kv_ss * 2);
-          dma_at(kbase + row, r + ck * 16, dK + blk);
-          dma_at(vbase + row, r + cv * 16, dV + blk);
-        }
-        return;
-      }
+      // band of global row block rg: [max(0, rg*64 - W + 1), rg*64 + 64) in 64-key tiles
+      const int rg = a.c0 / kBlk + r;
+      band_start = max(0, rg * kBlk - a.W + 1);
+      nb = (min(rg * kBlk + kBlk, a.S) - band_start + kBlk - 1) / kBlk;
+    } else {
+      nb = a.block_count[r];
     }
-#pragma unroll
+    const int n_vtiles = (nv + kBlk - 1) / kBlk;
+    const int ntiles = n_vtiles + nb;
+    const int32_t* cidx = a.column_index + (int64_t)b * a.ci_sb + (int64_t)h * a.ci_sh;
+    const uint16_t* kbase = a.k + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
+    const uint16_t* vbase = a.v + (int64_t)b * a.kv_sb + (int64_t)h * a.kv_sh;
+
+    // Tile loading: loading wave w fills the 1 KB blocks w, w+NL, ... of the K
+    // and of the V tile; in block q, lane i loads key row q*RPB + i/CH, slice
+    // position i%CH, i.e. global slice (i%CH) ^ swz_k(row) for K and
+    // (i%CH) ^ swz_v(row) for V.  The keys of the next tile are looked up two
+    // tiles ahead and its rows loaded one tile ahead, so both latencies overlap
+    // the current tile's arithmetic.
+    int krow[KPT], kcolK[KPT], kcolV[KPT];
+  #pragma unroll
     for (int i = 0; i < KPT; ++i) {
-      const int kt = min(krow[i], nval - 1);
-      const int blk = (wid + i * NL) * 512;  // element offset of this wave's block (1 KB)
-      if (CHUNK && vertical) {
-        // tl * kBlk is a multiple of the page, so the slot is kt mod page
-        const int64_t page_base = ((int64_t)ix.k[i] << a.page_log2) * D;
-        const int lane_row = (kt & ((1 << a.page_log2) - 1)) * D;
-        lds_dma16(a.pool_k + page_base + (lane_row + kcolK[i] * 8), dK + blk);
-        lds_dma16(a.pool_v + page_base + (lane_row + kcolV[i] * 8), dV + blk);
-      } else {
-        const int x = CHUNK ? min(band_start + (tl - n_vtiles) * kBlk + krow[i], a.S - 1) : ix.k[i];
-        lds_dma16(row_ptr(vertical, x, kbase, a.pool_k) + kcolK[i] * 8, dK + blk);
-        lds_dma16(row_ptr(vertical, x, vbase, a.pool_v) + kcolV[i] * 8, dV + blk);
-      }
+      const int row = (wid + i * NL) * RPB + lane / CH;
+      krow[i] = row;
+      kcolK[i] = (lane % CH) ^ swz_k<D>(row);
+      kcolV[i] = (lane % CH) ^ swz_v<D>(row);
     }
-  };
-  // Per-lane LDS element offsets of the fragments (the slice permutations
-  // above, resolved once): K row kt*16+n, slice j*4+g sits at slice
-  // (j*4+g) ^ swz_k(n); the transpose read of lane n in group g (row
-  // 4g + n/4 + 16u + 32s, d slice 2*dt + (n&3)/2, half n&1) finds its slice at
-  // (2*dt + (n&3)/2) ^ swz_v(4g + n/4).
-  int koff[KS];
-#pragma unroll
-  for (int j = 0; j < KS; ++j) koff[j] = n * D + ((j * 4 + g) ^ swz_k<D>(n)) * 8;
-  const int vrow = 4 * g + (n >> 2);
-  int voff[DT];
-#pragma unroll
-  for (int dt = 0; dt < DT; ++dt)
-    voff[dt] = vrow * D + ((2 * dt + ((n & 3) >> 1)) ^ swz_v<D>(vrow)) * 8 + (n & 1) * 4;
-
-  Idx idx_next;
-  if (ntiles > 0) {
-    Idx i0;
-    tile_idx(0, i0);
-    tile_load(0, i0, sK0, sV0);
-    if (ntiles > 1) tile_idx(1, idx_next);
-  }
-
-  // one 64-key tile: K and V of the tile in (sK, sV); the next tile's rows go to (nK, nV)
-  auto step = [&](int tile, const uint16_t* sK, const uint16_t* sV, uint16_t* nK,
-                  uint16_t* nV) __attribute__((always_inline)) {
-    const bool vert = tile < n_vtiles;
-    int band0 = 0, nvalid = kBlk;
-    if (vert) nvalid = min(kBlk, nv - tile * kBlk);
-    else band0 = CHUNK ? band_start + (tile - n_vtiles) * kBlk : bofs[r * a.bo_width + (tile - n_vtiles)];
-
-    // this wave's loads of the tile (and of the next tile's indices) have
-    // landed; the barrier publishes every wave's and frees the other buffer
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
-    __syncthreads();
-    // K fragments of k-step j+1 are read while the MFMAs of k-step j run;
-    // those of k-step 0 before the next tile's loads are issued
-    bf16x8_t kf[2][4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-      kf[0][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[0]]));
-    __builtin_amdgcn_sched_barrier(0);
-    // the next tile's rows stream into the other buffer under this tile's arithmetic
-    if (tile + 1 < ntiles) {
-      tile_load(tile + 1, idx_next, nK, nV);
-      if (tile + 2 < ntiles) tile_idx(tile + 2, idx_next);
-    }
-
-    // ---- S^T = K Q^T: key tiles kt (16 keys) x row tiles rt ------------------
-    f32x4_t sc[4][2];
-    // k-step outer: the 8 accumulators are independent chains, so
-    // consecutive MFMAs never wait on each other
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < KS; ++j) {
-      if (j + 1 < KS)
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-          kf[(j + 1) & 1][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[j + 1]]));
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-          sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j & 1][kt], qb[rt][j], sc[kt][rt], 0, 0, 0);
-    }
-    // tiles whose 64 keys are all visible to all 32 rows of the wave skip masking
-    const bool full = vert ? nvalid == kBlk : (band0 + kBlk - 1 <= row0 && band0 + kBlk <= a.S);
-    // ---- online softmax (lane: query row rt*16+n, keys kt*16+4g+i) -------------
-    // Row maxima are taken on the raw scores (the scale is positive) and the
-    // scale is folded into the exponent's FMA.  The reference maximum m_run of
-    // a row moves only when a tile's maximum exceeds it by more than 8 (log2
-    // units), so p <= 2^8 and the O / l rescale runs on few tiles.
-    float mxs[2];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      if (!full) {
-        // visible keys of this row are kk < lim
-        const int qrow = row0 + rt * 16 + n;
-        const int lim = vert ? nvalid : min(a.S - band0, qrow - band0 + 1);
-#pragma unroll
-        for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kk = kt * 16 + 4 * g + i;
-            sc[kt][rt][i] = kk < lim ? sc[kt][rt][i] : -INFINITY;
+    // A tile's rows are fetched in two stages.  Two tiles ahead, tile_idx
+    // loads the indirections -- the admitted columns' positions or, in chunked
+    // mode, the page ids of the global-cache entries (band rows need none) --
+    // into registers; one tile ahead, tile_load turns them into row addresses
+    // and loads the rows.  Keeping the dependent index loads a tile ahead of
+    // the row loads means no wait for an index also waits for the rows issued
+    // before it (memory counters retire in order).
+    struct Idx {
+      // per item: one-shot mode, the column or band position of the lane's
+      // row; chunked mode, admitted columns, the page id of the wave's 1 KB
+      // block (uniform; band rows need no index in chunked mode)
+      int k[KPT];
+    };
+    // In chunked mode the 4 rows of a wave's 1 KB block are 4 consecutive
+    // logical entries of the head's global cache, aligned to 4, so they lie in
+    // one page (16, 32 or 64 tokens): the page id is one scalar load per block
+    // and the row address is that page's (scalar) base plus a 32-bit lane
+    // offset.
+    const int32_t __attribute__((address_space(4)))* bt_h =
+        CHUNK ? (const int32_t __attribute__((address_space(4)))*)(a.bt + (int64_t)h * a.bt_sh) : nullptr;
+    auto tile_idx = [&](int tl, Idx& ix) __attribute__((always_inline)) {
+      if (wid >= NL) return;
+      if (tl < n_vtiles) {
+        const int nval = min(kBlk, nv - tl * kBlk);
+  #pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+          if (CHUNK) {
+            const int first = (wid + i * NL) * RPB;  // first row of the block (uniform)
+            ix.k[i] = bt_h[(unsigned)(tl * kBlk + min(first, nval - 1)) >> a.page_log2];
+          } else {
+            ix.k[i] = cidx[tl * kBlk + min(krow[i], nval - 1)];
           }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-        mx = fmax_ieee(mx, fmax_ieee(fmax_ieee(sc[kt][rt][0], sc[kt][rt][1]), fmax_ieee(sc[kt][rt][2], sc[kt][rt][3])));
-      mxs[rt] = mx;  // this lane's 16 keys of the row
-    }
-    // A row needs the rescale iff one of its four lanes' maxima exceeds
-    // m_run by the slack (the scale is positive, so scaling commutes with
-    // the max); only then are the row maxima reduced across the lanes.
-    if (__builtin_amdgcn_ballot_w64(mxs[0] * a.scale_log2 > m_run[0] + kRescaleSlack ||
-                                    mxs[1] * a.scale_log2 > m_run[1] + kRescaleSlack) != 0) {
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) mxs[rt] = xor32_max(xor16_max(mxs[rt])) * a.scale_log2;
-      const bool need0 = mxs[0] > m_run[0] + kRescaleSlack;
-      const bool need1 = mxs[1] > m_run[1] + kRescaleSlack;
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const bool need = rt == 0 ? need0 : need1;
-        const float mnew = need ? mxs[rt] : m_run[rt];
-        const float alpha = mnew == m_run[rt] ? 1.f : fast_exp2(m_run[rt] - mnew);
-        m_run[rt] = mnew;
-        lsum[rt] *= alpha;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
-      }
-    }
-    bf16x8_t pb[2][2];  // [rt][k-step of 32 keys]
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];  // rows with nothing visible keep p = 0
-      uint32_t pw[8];
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; i += 2) {
-          const float p0 = fast_exp2(fmaf(sc[kt][rt][i], a.scale_log2, -mref));
-          const float p1 = fast_exp2(fmaf(sc[kt][rt][i + 1], a.scale_log2, -mref));
-          pw[kt * 2 + i / 2] = pack_bf16x2(p0, p1);
         }
-      // k-step s covers key tiles 2s (slots 0-3) and 2s+1 (slots 4-7)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4_t w = (u32x4_t){pw[4 * s], pw[4 * s + 1], pw[4 * s + 2], pw[4 * s + 3]};
-        pb[rt][s] = __builtin_bit_cast(bf16x8_t, w);
+      } else if (!CHUNK) {
+        const int b0 = bofs[r * a.bo_width + (tl - n_vtiles)];
+  #pragma unroll
+        for (int i = 0; i < KPT; ++i) ix.k[i] = min(b0 + krow[i], a.S - 1);
       }
-    }
-    // ---- O^T += V^T P^T ------------------------------------------------------
-    // The A operand (lane: d = dt*16 + n, keys 32s+4g+0..3 and 32s+16+4g+0..3,
-    // the key order of pb) comes from two transpose reads of the row-major V
-    // tile: within each 16-lane group, lane n addresses row kb + n/4 at column
-    // d0 + 4*(n%4), and receives V[kb+k][d0+n] for k = 0..3.
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const uint16_t* vrd = sV + voff[dt] + s * 32 * D;
-        const v4i16_t lo = lds_read_tr16(vrd);
-        const v4i16_t hi = lds_read_tr16(vrd + 16 * D);
-        const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-          o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[rt][s], o[dt][rt], 0, 0, 0);
+    };
+    // row start of key x of tile tl in the K (or V) source (not the chunked
+    // mode's admitted columns, which tile_load addresses by page)
+    auto row_ptr = [&](bool vertical, int x, const uint16_t* tensor_base, const uint16_t* pool) -> const uint16_t* {
+      if (vertical) return tensor_base + (int64_t)x * a.kv_ss;
+      if (CHUNK && x < a.c0) return pool + (a.ring_row0 + (int64_t)h * a.W + (x - (a.c0 - a.W))) * D;
+      return tensor_base + (int64_t)(x - (CHUNK ? a.c0 : 0)) * a.kv_ss;
+    };
+    // Chunked mode: a tile that needs no clamping is loaded from a scalar
+    // base plus a 32-bit lane offset -- within a page (admitted columns),
+    // within the ring (band rows before the chunk) or within the chunk's k/v
+    // (band rows of the chunk; 32-bit while 63 rows of the k/v stride fit).
+    // The general path below serves the last admitted tile, the band tile
+    // that straddles the chunk start and the tile that runs past the sequence
+    // end.  This keeps the per-lane 64-bit address arithmetic, which held the
+    // load issue of a tile at ~500 cycles per wave, off the common tiles.
+    auto dma_at = [&](const void* base, uint32_t off, uint16_t* lds) __attribute__((always_inline)) {
+      lds_dma16((const uint16_t*)((const char*)base + off), lds);
+    };
+    auto tile_load = [&](int tl, const Idx& ix, uint16_t* dK, uint16_t* dV) __attribute__((always_inline)) {
+      if (wid >= NL) return;
+      const bool vertical = tl < n_vtiles;
+      const int nval = vertical ? min(kBlk, nv - tl * kBlk) : kBlk;
+      if (!CHUNK && a.off32) {
+        // one-shot mode: every row is k/v row ix.k[i] (clamped when it was looked up)
+  #pragma unroll
+        for (int i = 0; i < KPT; ++i) {
+          const int blk = (wid + i * NL) * 512;
+          int ck = kcolK[i], cv = kcolV[i];
+          asm volatile("" : "+v"(ck), "+v"(cv));
+          const uint32_t r = (uint32_t)ix.k[i] * (uint32_t)(a.kv_ss * 2);
+          dma_at(kbase, r + ck * 16, dK + blk);
+          dma_at(vbase, r + cv * 16, dV + blk);
+        }
+        return;
       }
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rt][s], lsum[rt], 0, 0, 0);
-    }
-  };
-  for (int tile = 0; tile < ntiles; tile += 2) {
-    step(tile, sK0, sV0, sK1, sV1);
-    if (tile + 1 < ntiles) step(tile + 1, sK1, sV1, sK0, sV0);
-  }
+      if (CHUNK) {
+        const int first = band_start + (tl - n_vtiles) * kBlk;  // band tiles: first key position
+        if (vertical && nval == kBlk) {
+  #pragma unroll
+          for (int i = 0; i < KPT; ++i) {
+            const int blk = (wid + i * NL) * 512;
+            const int64_t pg = ((int64_t)ix.k[i] << a.page_log2) * (D * 2);
+            int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
+            asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));  // recomputed here, not hoisted out of the loop
+            // tl * kBlk is a multiple of the page, so the row within the page is kr mod page
+            const uint32_t r = (uint32_t)(kr & ((1 << a.page_log2) - 1)) * (D * 2);
+            dma_at((const char*)a.pool_k + pg, r + ck * 16, dK + blk);
+            dma_at((const char*)a.pool_v + pg, r + cv * 16, dV + blk);
+          }
+          return;
+        }
+        if (!vertical && first + kBlk <= a.c0) {
+          const int64_t row = a.ring_row0 + (int64_t)h * a.W + (first - (a.c0 - a.W));
+  #pragma unroll
+          for (int i = 0; i < KPT; ++i) {
+            const int blk = (wid + i * NL) * 512;
+            int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
+            asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));
+            const uint32_t r = (uint32_t)kr * (D * 2);
+            dma_at(a.pool_k + row * D, r + ck * 16, dK + blk);
+            dma_at(a.pool_v + row * D, r + cv * 16, dV + blk);
+          }
+          return;
+        }
+        if (!vertical && first >= a.c0 && first + kBlk <= a.S && a.kv_ss <= (1 << 24)) {
+          const int64_t row = (int64_t)(first - a.c0) * a.kv_ss;
+  #pragma unroll
+          for (int i = 0; i < KPT; ++i) {
+            const int blk = (wid + i * NL) * 512;
+            int kr = krow[i], ck = kcolK[i], cv = kcolV[i];
+            asm volatile("" : "+v"(kr), "+v"(ck), "+v"(cv));
+            const uint32_t r = (uint32_t)kr * (uint32_t)(a.kv_ss * 2);
+            dma_at(kbase + row, r + ck * 16, dK + blk);
+            dma_at(vbase + row, r + cv * 16, dV + blk);
+          }
+          return;
+        }
+      }
+  #pragma unroll
+      for (int i = 0; i < KPT; ++i) {
+        const int kt = min(krow[i], nval - 1);
+        const int blk = (wid + i * NL) * 512;  // element offset of this wave's block (1 KB)
+        if (CHUNK && vertical) {
+          // tl * kBlk is a multiple of the page, so the slot is kt mod page
+          const int64_t page_base = ((int64_t)ix.k[i] << a.page_log2) * D;
+          const int lane_row = (kt & ((1 << a.page_log2) - 1)) * D;
+          lds_dma16(a.pool_k + page_base + (lane_row + kcolK[i] * 8), dK + blk);
+          lds_dma16(a.pool_v + page_base + (lane_row + kcolV[i] * 8), dV + blk);
+        } else {
+          const int x = CHUNK ? min(band_start + (tl - n_vtiles) * kBlk + krow[i], a.S - 1) : ix.k[i];
+          lds_dma16(row_ptr(vertical, x, kbase, a.pool_k) + kcolK[i] * 8, dK + blk);
+          lds_dma16(row_ptr(vertical, x, vbase, a.pool_v) + kcolV[i] * 8, dV + blk);
+        }
+      }
+    };
+    // Per-lane LDS element offsets of the fragments (the slice permutations
+    // above, resolved once): K row kt*16+n, slice j*4+g sits at slice
+    // (j*4+g) ^ swz_k(n); the transpose read of lane n in group g (row
+    // 4g + n/4 + 16u + 32s, d slice 2*dt + (n&3)/2, half n&1) finds its slice at
+    // (2*dt + (n&3)/2) ^ swz_v(4g + n/4).
+    int koff[KS];
+  #pragma unroll
+    for (int j = 0; j < KS; ++j) koff[j] = n * D + ((j * 4 + g) ^ swz_k<D>(n)) * 8;
+    const int vrow = 4 * g + (n >> 2);
+    int voff[DT];
+  #pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      voff[dt] = vrow * D + ((2 * dt + ((n & 3) >> 1)) ^ swz_v<D>(vrow)) * 8 + (n & 1) * 4;
 
-  // ---- normalise and store: lane holds O[row rt*16+n][dt*16 + 4g + i] -------
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const float l = lsum[rt][0];
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    const int s = lrow0 + rt * 16 + n;
-    if (s < nrows) {
-      uint16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) {
-        const uint32_t w0 = pack_bf16x2(o[dt][rt][0] * inv, o[dt][rt][1] * inv);
-        const uint32_t w1 = pack_bf16x2(o[dt][rt][2] * inv, o[dt][rt][3] * inv);
-        *(uint64_t*)(orow + dt * 16 + 4 * g) = (uint64_t)w0 | ((uint64_t)w1 << 32);
+    Idx idx_next;
+    if (ntiles > 0) {
+      Idx i0;
+      tile_idx(0, i0);
+      tile_load(0, i0, sK0, sV0);
+      if (ntiles > 1) tile_idx(1, idx_next);
+    }
+
+    // one 64-key tile: K and V of the tile in (sK, sV); the next tile's rows go to (nK, nV)
+    auto step = [&](int tile, const uint16_t* sK, const uint16_t* sV, uint16_t* nK,
+                    uint16_t* nV) __attribute__((always_inline)) {
+      const bool vert = tile < n_vtiles;
+      int band0 = 0, nvalid = kBlk;
+      if (vert) nvalid = min(kBlk, nv - tile * kBlk);
+      else band0 = CHUNK ? band_start + (tile - n_vtiles) * kBlk : bofs[r * a.bo_width + (tile - n_vtiles)];
+
+      // this wave's loads of the tile (and of the next tile's indices) have
+      // landed; the barrier publishes every wave's and frees the other buffer
+      __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+      __syncthreads();
+      // K fragments of k-step j+1 are read while the MFMAs of k-step j run;
+      // those of k-step 0 before the next tile's loads are issued
+      bf16x8_t kf[2][4];
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        kf[0][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[0]]));
+      __builtin_amdgcn_sched_barrier(0);
+      // the next tile's rows stream into the other buffer under this tile's arithmetic
+      if (tile + 1 < ntiles) {
+        tile_load(tile + 1, idx_next, nK, nV);
+        if (tile + 2 < ntiles) tile_idx(tile + 2, idx_next);
+      }
+
+      // ---- S^T = K Q^T: key tiles kt (16 keys) x row tiles rt ------------------
+      f32x4_t sc[4][2];
+      // k-step outer: the 8 accumulators are independent chains, so
+      // consecutive MFMAs never wait on each other
+  #pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+        for (int rt = 0; rt < 2; ++rt) sc[kt][rt] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        if (j + 1 < KS)
+  #pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+            kf[(j + 1) & 1][kt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&sK[kt * 16 * D + koff[j + 1]]));
+        __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            sc[kt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[j & 1][kt], qb[rt][j], sc[kt][rt], 0, 0, 0);
+      }
+      // tiles whose 64 keys are all visible to all 32 rows of the wave skip masking
+      const bool full = vert ? nvalid == kBlk : (band0 + kBlk - 1 <= row0 && band0 + kBlk <= a.S);
+      // ---- online softmax (lane: query row rt*16+n, keys kt*16+4g+i) -------------
+      // Row maxima are taken on the raw scores (the scale is positive) and the
+      // scale is folded into the exponent's FMA.  The reference maximum m_run of
+      // a row moves only when a tile's maximum exceeds it by more than 8 (log2
+      // units), so p <= 2^8 and the O / l rescale runs on few tiles.
+      float mxs[2];
+  #pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        if (!full) {
+          // visible keys of this row are kk < lim
+          const int qrow = row0 + rt * 16 + n;
+          const int lim = vert ? nvalid : min(a.S - band0, qrow - band0 + 1);
+  #pragma unroll
+          for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int kk = kt * 16 + 4 * g + i;
+              sc[kt][rt][i] = kk < lim ? sc[kt][rt][i] : -INFINITY;
+            }
+        }
+        float mx = -INFINITY;
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+          mx = fmax_ieee(mx, fmax_ieee(fmax_ieee(sc[kt][rt][0], sc[kt][rt][1]), fmax_ieee(sc[kt][rt][2], sc[kt][rt][3])));
+        mxs[rt] = mx;  // this lane's 16 keys of the row
+      }
+      // A row needs the rescale iff one of its four lanes' maxima exceeds
+      // m_run by the slack (the scale is positive, so scaling commutes with
+      // the max); only then are the row maxima reduced across the lanes.
+      if (__builtin_amdgcn_ballot_w64(mxs[0] * a.scale_log2 > m_run[0] + kRescaleSlack ||
+                                      mxs[1] * a.scale_log2 > m_run[1] + kRescaleSlack) != 0) {
+  #pragma unroll
+        for (int rt = 0; rt < 2; ++rt) mxs[rt] = xor32_max(xor16_max(mxs[rt])) * a.scale_log2;
+        const bool need0 = mxs[0] > m_run[0] + kRescaleSlack;
+        const bool need1 = mxs[1] > m_run[1] + kRescaleSlack;
+  #pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const bool need = rt == 0 ? need0 : need1;
+          const float mnew = need ? mxs[rt] : m_run[rt];
+          const float alpha = mnew == m_run[rt] ? 1.f : fast_exp2(m_run[rt] - mnew);
+          m_run[rt] = mnew;
+          lsum[rt] *= alpha;
+  #pragma unroll
+          for (int dt = 0; dt < DT; ++dt) o[dt][rt] *= alpha;
+        }
+      }
+      bf16x8_t pb[2][2];  // [rt][k-step of 32 keys]
+  #pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const float mref = m_run[rt] == -INFINITY ? 0.f : m_run[rt];  // rows with nothing visible keep p = 0
+        uint32_t pw[8];
+  #pragma unroll
+        for (int kt = 0; kt < 4; ++kt)
+  #pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+            const float p0 = fast_exp2(fmaf(sc[kt][rt][i], a.scale_log2, -mref));
+            const float p1 = fast_exp2(fmaf(sc[kt][rt][i + 1], a.scale_log2, -mref));
+            pw[kt * 2 + i / 2] = pack_bf16x2(p0, p1);
+          }
+        // k-step s covers key tiles 2s (slots 0-3) and 2s+1 (slots 4-7)
+  #pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          const u32x4_t w = (u32x4_t){pw[4 * s], pw[4 * s + 1], pw[4 * s + 2], pw[4 * s + 3]};
+          pb[rt][s] = __builtin_bit_cast(bf16x8_t, w);
+        }
+      }
+      // ---- O^T += V^T P^T ------------------------------------------------------
+      // The A operand (lane: d = dt*16 + n, keys 32s+4g+0..3 and 32s+16+4g+0..3,
+      // the key order of pb) comes from two transpose reads of the row-major V
+      // tile: within each 16-lane group, lane n addresses row kb + n/4 at column
+      // d0 + 4*(n%4), and receives V[kb+k][d0+n] for k = 0..3.
+  #pragma unroll
+      for (int s = 0; s < 2; ++s) {
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint16_t* vrd = sV + voff[dt] + s * 32 * D;
+          const v4i16_t lo = lds_read_tr16(vrd);
+          const v4i16_t hi = lds_read_tr16(vrd + 16 * D);
+          const bf16x8_t vf = __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  #pragma unroll
+          for (int rt = 0; rt < 2; ++rt)
+            o[dt][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pb[rt][s], o[dt][rt], 0, 0, 0);
+        }
+  #pragma unroll
+        for (int rt = 0; rt < 2; ++rt) lsum[rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pb[rt][s], lsum[rt], 0, 0, 0);
+      }
+    };
+    for (int tile = 0; tile < ntiles; tile += 2) {
+      step(tile, sK0, sV0, sK1, sV1);
+      if (tile + 1 < ntiles) step(tile + 1, sK1, sV1, sK0, sV0);
+    }
+
+    // ---- normalise and store: lane holds O[row rt*16+n][dt*16 + 4g + i] -------
+  #pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const float l = lsum[rt][0];
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      const int s = lrow0 + rt * 16 + n;
+      if (s < nrows) {
+        uint16_t* orow = a.out + (int64_t)b * a.o_sb + (int64_t)s * a.o_ss + (int64_t)hq * a.o_sh;
+  #pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const uint32_t w0 = pack_bf16x2(o[dt][rt][0] * inv, o[dt][rt][1] * inv);
+          const uint32_t w1 = pack_bf16x2(o[dt][rt][2] * inv, o[dt][rt][3] * inv);
+          *(uint64_t*)(orow + dt * 16 + 4 * g) = (uint64_t)w0 | ((uint64_t)w1 << 32);
+        }
       }
     }
   }
 }
 
+int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Persistent grid: the workgroups resident at once (occupancy of the
+// instance times the CUs), at most one per item.
+template <int D, int HPW, bool CHUNK>
+hipError_t launch_persistent(const PrefillArgs& a, hipStream_t st) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, sparse_prefill_kernel<D, HPW, CHUNK>, 128 * HPW, 0) !=
+            hipSuccess ||
+        nb <= 0)
+      nb = 1;
+    per_cu = nb;
+  }
+  const int64_t items = (int64_t)a.R * a.B * a.Hkv * (a.G / HPW);
+  const int grid = (int)(items < (int64_t)per_cu * cu_count() ? items : (int64_t)per_cu * cu_count());
+  hipLaunchKernelGGL((sparse_prefill_kernel<D, HPW, CHUNK>), dim3(grid), dim3(128 * HPW), 0, st, a);
+  return hipGetLastError();
+}
+
 template <int D, int HPW>
 hipError_t launch(const PrefillArgs& a, hipStream_t st, bool chunked) {
-  const dim3 grid(a.R, a.B * a.Hkv, a.G / HPW);
-  if (chunked)
-    hipLaunchKernelGGL((sparse_prefill_kernel<D, HPW, true>), grid, dim3(128 * HPW), 0, st, a);
-  else
-    hipLaunchKernelGGL((sparse_prefill_kernel<D, HPW, false>), grid, dim3(128 * HPW), 0, st, a);
-  return hipGetLastError();
+  return chunked ? launch_persistent<D, HPW, true>(a, st) : launch_persistent<D, HPW, false>(a, st);
 }
 
 // Query heads per workgroup: the largest of 4, 2, 1 that divides G and lets
