@@ -84,6 +84,9 @@ class DualCache:
         # for graph-captured decode steps
         self.ring_state = torch.zeros(3, **i32)
         self.device_ring = False
+        # deferred gating: when set, decode steps leave the window re-gate to
+        # the caller (layers.refresh_windows after a step that wrote slot W-1)
+        self.refresh_by_caller = False
         self.next_free_block_dev = torch.full((1,), n_local, **i32)
         self.status = torch.zeros(1, **i32)
         # random_sparsity ablation: decode-step draws per layer so far (device

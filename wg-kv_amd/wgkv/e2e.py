@@ -217,8 +217,10 @@ class GraphDecoder:
     its device ring pointers; the token and the position live in device
     tensors the step itself advances.  The ring must already be full (any
     prompt of at least W tokens).  With deferred gating every layer's window
-    re-gate is in the graph and runs only on the step that writes the ring's
-    last slot (decided on the device from the ring state)."""
+    is re-gated after the steps that write the ring's last slot: a second
+    captured graph (the re-gate of all layers) is replayed after those steps
+    only, which the host knows from its mirror of the ring pointers, so the
+    other steps launch no re-gate at all."""
 
     def __init__(self, model, cache, token, pos, warmup=2):
         dev = token.device
@@ -227,12 +229,27 @@ class GraphDecoder:
         self.pos = torch.tensor([[pos]], dtype=torch.int64, device=dev)
         if cache.local_length != cache.local_window_size:
             raise AssertionError("graph decode needs a full ring")
+        cfg = model.cfg
+        # decode steps carry no admission mask (and re-gate the window) with
+        # deferred gating, unless every token is admitted (use_baseline)
+        self.regate = (bool(cfg.g_defer) and not cfg.use_baseline
+                       and (cfg.random_sparsity is not None or cfg.g_expand != 0.0))
         cache.use_device_ring(True)
+        cache.refresh_by_caller = self.regate
+        self.attn = [layer.self_attn for layer in model.layers]
+        if self.regate and cfg.random_sparsity is None:
+            for attn in self.attn:  # the gates' packed weights exist before any capture
+                gp = attn.g_predictors
+                if cache.block_pool_k.dtype == torch.bfloat16:
+                    gp.packed_weights(gp.precision(torch.bfloat16))
         side = torch.cuda.Stream(device=dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
             for _ in range(warmup):  # real decode steps: workspaces and library state before capture
+                wrote_last = self._writes_last_slot()
                 self._step()
+                if wrote_last:
+                    self._regate()
         torch.cuda.current_stream(dev).wait_stream(side)
         self.warm_tokens = warmup
         host = (cache.local_ptr, cache.local_length)
@@ -240,6 +257,20 @@ class GraphDecoder:
         with torch.cuda.graph(self.graph):
             self.logits = self._step()
         cache.local_ptr, cache.local_length = host  # capture ran the host side once, the device side not
+        self.regate_graph = None
+        if self.regate:
+            self.regate_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.regate_graph):
+                self._regate()
+
+    def _writes_last_slot(self):
+        c = self.cache
+        insert = c.local_length if c.local_length < c.local_window_size else c.local_ptr
+        return self.regate and insert == c.local_window_size - 1
+
+    def _regate(self):
+        from .layers import refresh_windows
+        refresh_windows(self.attn, self.cache, self.tok.device)
 
     def _step(self):
         logits = self.model.forward_at(self.tok, self.pos, self.cache)
@@ -248,8 +279,12 @@ class GraphDecoder:
         return logits
 
     def step(self):
-        """Replay one step; returns the (device) token it produced."""
+        """Replay one step (and, after a step that wrote the ring's last slot,
+        the windows' re-gate); returns the (device) token it produced."""
+        wrote_last = self._writes_last_slot()
         self.graph.replay()
+        if wrote_last:
+            self.regate_graph.replay()
         self.cache.advance_host_ring()
         return self.tok
 

@@ -170,6 +170,18 @@ def refresh_local_is_global(self, past_key_value, device, on_device=False):
                                           active=(c.ring_state[2:], W - 1) if on_device else None)
 
 
+def refresh_windows(attention_layers, past_key_value, device):
+    """The deferred re-gate of every layer's window (refresh_local_is_global,
+    src/modeling_layers.py:1169-1180), for a caller that set
+    ``cache.refresh_by_caller`` and runs it after a decode step that wrote the
+    ring's last slot.  Equivalent to the per-layer refresh inside the step:
+    a layer's flags are next read by the promotion at the start of the next
+    step, and its window's keys and values do not change after its own write
+    within the step."""
+    for attn in attention_layers:
+        refresh_local_is_global(attn, past_key_value, device)
+
+
 def migrate_local_kv_to_global(self, past_key_value, device, local_blocks_per_head):
     """src/modeling_layers.py:674-763 on the device (no host syncs unless
     check_capacity_decode asks for the reference's per-step overflow assert)."""
@@ -245,7 +257,9 @@ def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, valu
                       pre_key=pre_key[0, :, 0] if g_mask is None else None,
                       migrate=False, write=True, cache_seqlens=seqlens[0], advance=last)
     if g_mask is None:
-        if c.device_ring:
+        if c.refresh_by_caller:
+            pass  # the caller re-gates the windows after the step (refresh_windows)
+        elif c.device_ring:
             refresh_local_is_global(self, c, device, on_device=True)  # runs only if slot W-1 was written
         elif insert_pos == W - 1:
             refresh_local_is_global(self, c, device)
@@ -364,6 +378,7 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
 
 
 __all__ = [
-    "WGKVConfig", "DualCache", "get_random_g_scores", "decode_random_admission", "refresh_local_is_global", "migrate_local_kv_to_global",
+    "WGKVConfig", "DualCache", "get_random_g_scores", "decode_random_admission", "refresh_local_is_global",
+    "refresh_windows", "migrate_local_kv_to_global",
     "prefill_wrapper", "decode_wrapper", "self_attn_forward_patch_inference", "self_attn_forward_patch",
 ]
