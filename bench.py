@@ -68,7 +68,7 @@ def parse():
 # WRITE_SIZE passes over `bench.py --traffic-probe`, each scaled by what the
 # counter reads for a 1 GiB device copy in the same program; the summary with
 # the commands and raw counter values is DECODE_TRAFFIC_SOURCE
-DECODE_TRAFFIC_BYTES = 1347609197
+DECODE_TRAFFIC_BYTES = 1347606162
 DECODE_TRAFFIC_SOURCE = "profiles/decode_attn_traffic_b8_128k.md"
 
 

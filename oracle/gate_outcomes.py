@@ -45,8 +45,8 @@ rounded addition or fused multiply-add errs by at most u = 2**-24 times its
 result, so a chain of accumulations into c_1, ..., c_n errs by at most
 u * sum |c_s|, and a tree in which every term passes through at most d
 roundings errs by at most u * d * sum |terms|.  Each bound is multiplied by
-``SAFETY`` (2) to cover second-order terms and the rounding of the bound
-itself.  A matrix-core step (``v_mfma_*``) is charged as if it summed its
+``SAFETY`` (1.01) to cover second-order terms (relative size about n * u)
+and the rounding of the bound itself.  A matrix-core step (``v_mfma_*``) is charged as if it summed its
 products sequentially in float32 (``l1_internal`` roundings per product),
 which covers any internal order.
 """
