@@ -462,12 +462,20 @@ __host__ __device__ constexpr int planes_of(int prec) { return prec ? 1 : kPlane
 constexpr int kActE0 = 127 - 16;  // biased exponent of 2^-16
 constexpr int kActBinades = 20;
 constexpr int kActTab = 2 * kActBinades * 128;  // entries per activation
+// Entry (sign, binade e, 7 mantissa bits m) sits at sign * kActBinades * 128 +
+// e * 128 + m, so for a bf16 value with bits b the byte offset within the
+// sign's half is 2 * ((b & 0x7fff) - (kActE0 << 7)): in [0, kActBytes)
+// exactly for the table's range (in 16-bit arithmetic it wraps past it for
+// smaller magnitudes, zero included), plus kActBytes for b < 0.
+constexpr int kActBytes = kActBinades * 128 * 2;
+constexpr int kActBias2 = (kActE0 << 7) * 2;
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ int act_index(float h) {
-  const uint32_t u = __float_as_uint(h);
-  const int e = (int)((u >> 23) & 0xff) - kActE0;
-  if ((unsigned)e >= (unsigned)kActBinades) return -1;
-  return (int)(u >> 31) * (kActBinades * 128) + e * 128 + (int)((u >> 16) & 127);
+// Two f32 -> a bf16 pair (round to nearest even) in one v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float lo, float hi) {
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, bf16x2_t));
 }
 
 __global__ void gate_act_table_kernel(uint16_t* __restrict__ tab) {
@@ -525,10 +533,11 @@ __global__ void gate_pack_kernel(const float* __restrict__ w1, const float* wn0,
 // four; per 32-input k-step it reads the four 64-token A fragments from LDS
 // and the 4 x 3 packed B fragments of the next k-step from global memory.
 // Two waves per SIMD (two workgroups per CU) hide each other's loads and
-// GELU epilogues.  PREC is GateArgs::prec (three planes for fp32 parameters,
-// one for bf16 parameters).
+// GELU epilogues.  fp32 parameters only (PREC 0, three planes); bf16
+// parameters run gate_bf16p_kernel.
 template <int D, int NIN, int PREC>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_bf16_kernel(GateArgs a, const u32x4_t* __restrict__ packed) {
+  static_assert(PREC == 0, "three planes: fp32 parameters (bf16 parameters run gate_bf16p_kernel)");
   constexpr int NP = planes_of(PREC);
   constexpr int K = NIN * D;
   constexpr int KS = K / 32;
@@ -538,7 +547,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   constexpr int NLD = 16 / RPL;  // wave loads per input for the wave's 16 tokens
   __shared__ __attribute__((aligned(16))) uint16_t ys[kTok * LDY];
   __shared__ float s_part[4][kTok];
-  __shared__ __attribute__((aligned(16))) uint16_t s_act[PREC ? kActTab : 8];
   if (inactive(a)) return;
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
   const int nbh = a.B * a.H;
@@ -546,10 +554,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
   const int bh = lid % nbh, tile = lid / nbh;
   const int b = bh / a.H, h = bh - b * a.H;
   const int s0 = tile * kTok;
-  if (PREC) {  // this activation's table (after the weight plane) -> LDS; read after the barrier below
-    const u32x4_t* tab = (const u32x4_t*)(packed + (int64_t)a.H * (a.inner / 16) * KS * NP * 64) + a.act * (kActTab / 8);
-    for (int i = threadIdx.x; i < kActTab / 8; i += kThreads) ((u32x4_t*)s_act)[i] = tab[i];
-  }
 
   // ---- normalised inputs -> LDS (bf16) ------------------------------------
   {
@@ -585,13 +589,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
           const float scale = 1.0f / sqrtf(ss / (float)D + 1e-6f);
 #pragma unroll
           for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(f[2 * e] * scale, f[2 * e + 1] * scale);  // cast back to bf16 (:128)
-          if (PREC) {  // times the bf16 norm weight, rounded (:128)
-            const f32x4_t w0 = *(const f32x4_t*)(a.w_norm[i] + c * 8);
-            const f32x4_t w1v = *(const f32x4_t*)(a.w_norm[i] + c * 8 + 4);
-            const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1v[0], w1v[1], w1v[2], w1v[3]};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(wv[2 * e] * bf16lo(y[e]), wv[2 * e + 1] * bf16hi(y[e]));
-          }
         }
         const int m = wid * 16 + u * RPL + lane / LPR;
         *(u32x4_t*)(&ys[m * LDY + i * D + c * 8]) = y;
@@ -619,32 +616,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
       for (int j = 0; j < 4; ++j) c[mt][j] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
-    if constexpr (NP == 1) {
-      // one plane: the B fragments are requested PD k-steps ahead, so the
-      // weight loads' latency is paid about once per group, not per k-step
-      constexpr int PD = KS < 4 ? KS : 4;
-      u32x4_t bq[KS][4];
-#pragma unroll
-      for (int ks = 0; ks < PD; ++ks)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) bq[ks][j] = ph[((int64_t)tj[j] * KS + ks) * 64];
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        if (ks + PD < KS)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) bq[ks + PD][j] = ph[((int64_t)tj[j] * KS + ks + PD) * 64];
-        bf16x8_t ax[4];
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          ax[mt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&ys[(mt * 16 + n) * LDY + ks * 32 + kg * 8]));
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            c[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt], __builtin_bit_cast(bf16x8_t, bq[ks][j]), c[mt][j], 0, 0, 0);
-        __builtin_amdgcn_sched_barrier(0);  // keep each k-step's loads in place (registers)
-      }
-    } else {
+    {
     u32x4_t bw[4][NP];
 #pragma unroll
     for (int j = 0; j < 4; ++j)
@@ -686,15 +658,247 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float z = layer_out(c[mt][j][i], bias, PREC);
-          float y;
-          if (PREC) {
-            const int ti = act_index(z);
-            y = bf16lo(s_act[ti < 0 ? 0 : ti]);
-            if (ti < 0) y = activation(z, a.act, PREC);
-          } else {
-            y = activation(z, a.act, PREC);
-          }
-          logit[mt][i] = fmaf(wo, y, logit[mt][i]);
+          logit[mt][i] = fmaf(wo, activation(z, a.act, PREC), logit[mt][i]);
+        }
+    }
+  }
+  finish_tile(a, logit, s_part, lane, wid, b, h, s0);
+}
+
+// ---- one weight plane (bf16 parameters) -----------------------------------
+// The tile, inputs, MFMA arithmetic and per-lane summation order of
+// gate_bf16_kernel with one plane (wave w: 16-column tiles w + 4m in groups
+// of four), with an epilogue that works on pairs of values: the two rows
+// i, i+1 of a column are rounded to bf16 by one v_cvt_pk_bf16_f32, their
+// table offsets computed with packed 16-bit arithmetic, and all 64 table
+// reads of a group issued before any result is used, so the LDS latency is
+// paid once per group, not once per value (the reads themselves stay at
+// random addresses: bank conflicts are most of the kernel's LDS time).  One
+// packed maximum over the group's offsets tells whether any value lies
+// outside the table; only then are those values computed by activation().
+// The weight fragments are requested PQ k-steps ahead, across group
+// boundaries, and the first group's, with the activation table and the norm
+// weights, before the inputs.
+template <int D, int NIN>
+struct TileInputs {
+  static constexpr int LPR = D / 8;     // lanes per input row
+  static constexpr int RPL = 64 / LPR;  // rows per wave load
+  static constexpr int NLD = 16 / RPL;  // wave loads per input for the wave's 16 tokens
+  u32x4_t v[NIN][NLD];
+  f32x4_t wn[NIN][2];
+};
+
+template <int D, int NIN>
+__device__ __forceinline__ void load_tile_inputs(const GateArgs& a, int b, int h, int s0, int lane, int wid,
+                                                 TileInputs<D, NIN>& t) {
+  using T = TileInputs<D, NIN>;
+  const int c = lane % T::LPR;
+  if (a.rms)
+#pragma unroll
+    for (int i = 0; i < NIN; ++i) {
+      t.wn[i][0] = *(const f32x4_t*)(a.w_norm[i] + c * 8);
+      t.wn[i][1] = *(const f32x4_t*)(a.w_norm[i] + c * 8 + 4);
+    }
+#pragma unroll
+  for (int i = 0; i < NIN; ++i)
+#pragma unroll
+    for (int u = 0; u < T::NLD; ++u) {
+      const int s = min(s0 + wid * 16 + u * T::RPL + lane / T::LPR, a.S - 1);  // rows past S are computed and discarded
+      const uint16_t* row = (const uint16_t*)a.in[i] + (int64_t)b * a.sb[i] + (int64_t)h * a.sh[i] + (int64_t)s * a.ss[i];
+      t.v[i][u] = *(const u32x4_t*)(row + c * 8);
+    }
+}
+
+// y = bf16(x * rsqrt(mean(x^2) + 1e-6)) (:128), times the bf16 norm weight
+// rounded to bf16, as gate_bf16_kernel with bf16 parameters.
+template <int D, int NIN, int LDY>
+__device__ __forceinline__ void store_tile_inputs(const GateArgs& a, int lane, int wid, const TileInputs<D, NIN>& t,
+                                                  uint16_t* ys) {
+  using T = TileInputs<D, NIN>;
+  const int c = lane % T::LPR;
+#pragma unroll
+  for (int i = 0; i < NIN; ++i)
+#pragma unroll
+    for (int u = 0; u < T::NLD; ++u) {
+      u32x4_t y = t.v[i][u];
+      if (a.rms) {
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          f[2 * e] = bf16lo(y[e]);
+          f[2 * e + 1] = bf16hi(y[e]);
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+        ss += dpp_f32<WGKV_DPP_QP_1032>(ss);
+        ss += dpp_f32<WGKV_DPP_QP_2301>(ss);
+        ss += dpp_f32<WGKV_DPP_ROW_HALF_MIRROR>(ss);
+        if (T::LPR == 16) ss += dpp_f32<WGKV_DPP_ROW_MIRROR>(ss);
+        const float scale = 1.0f / sqrtf(ss / (float)D + 1e-6f);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(f[2 * e] * scale, f[2 * e + 1] * scale);
+        const float wv[8] = {t.wn[i][0][0], t.wn[i][0][1], t.wn[i][0][2], t.wn[i][0][3],
+                             t.wn[i][1][0], t.wn[i][1][1], t.wn[i][1][2], t.wn[i][1][3]};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = pack_bf16x2(wv[2 * e] * bf16lo(y[e]), wv[2 * e + 1] * bf16hi(y[e]));
+      }
+      const int m = wid * 16 + u * T::RPL + lane / T::LPR;
+      *(u32x4_t*)(&ys[m * LDY + i * D + c * 8]) = y;
+    }
+}
+
+template <int D, int NIN, int PREC>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void gate_bf16p_kernel(GateArgs a, const u32x4_t* __restrict__ packed) {
+  static_assert(PREC == 1 || PREC == 2, "one plane: bf16 parameters");
+  constexpr int K = NIN * D;
+  constexpr int KS = K / 32;
+  constexpr int LDY = K + 8;
+  constexpr int NTAB = kActTab / 8;                      // 16-byte slices of the table
+  constexpr int TPT = (NTAB + kThreads - 1) / kThreads;  // per thread
+  __shared__ __attribute__((aligned(16))) uint16_t ys[kTok * LDY];
+  __shared__ float s_part[4][kTok];
+  __shared__ __attribute__((aligned(16))) uint16_t s_act[kActTab];
+  if (inactive(a)) return;
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int nbh = a.B * a.H;
+  const int lid = blockIdx.x + blockIdx.y * gridDim.x;  // XCD-aware order, as gate_kernel
+  const int bh = lid % nbh, tile = lid / nbh;
+  const int b = bh / a.H, h = bh - b * a.H;
+  const int s0 = tile * kTok;
+  const int n = lane & 15, kg = lane >> 4;
+  const int ntot = a.inner / 16;
+  const u32x4_t* ph = packed + (int64_t)h * ntot * KS * 64 + lane;
+  const float* b1h = a.b1 + (int64_t)h * a.inner;
+  const float* w2h = a.w2 + (int64_t)h * a.inner;
+  constexpr int TG = 4;                    // tiles per group
+  constexpr int PQ = KS % 2 == 0 ? 2 : 1;  // k-steps of weight fragments in flight
+  const int nw = (ntot - wid + 3) >> 2;    // this wave's tiles: wid + 4m, m < nw
+  const int ng = (nw + TG - 1) / TG;
+  // tile j of group g; past the wave's last tile, tile wid again (computed, never used)
+  auto tile_of = [&](int g, int j) { const int m = TG * g + j; return m < nw ? wid + 4 * m : wid; };
+
+  // ---- requests that do not depend on the inputs --------------------------
+  u32x4_t tab_r[TPT];
+  {
+    const u32x4_t* tab = packed + (int64_t)a.H * ntot * KS * 64 + a.act * NTAB;  // this activation's table
+#pragma unroll
+    for (int r = 0; r < TPT; ++r) {
+      const int i = threadIdx.x + r * kThreads;
+      tab_r[r] = tab[i < NTAB ? i : 0];
+    }
+  }
+  u32x4_t bq[PQ][TG];  // k-step ks of a group in slot ks % PQ
+#pragma unroll
+  for (int ks = 0; ks < PQ; ++ks)
+#pragma unroll
+    for (int jj = 0; jj < TG; ++jj) bq[ks][jj] = ph[((int64_t)tile_of(0, jj) * KS + ks) * 64];
+
+  // ---- normalised inputs -> LDS -------------------------------------------
+  {
+    TileInputs<D, NIN> in;
+    load_tile_inputs<D, NIN>(a, b, h, s0, lane, wid, in);
+#pragma unroll
+    for (int r = 0; r < TPT; ++r) {
+      const int i = threadIdx.x + r * kThreads;
+      if (i < NTAB) ((u32x4_t*)s_act)[i] = tab_r[r];
+    }
+    store_tile_inputs<D, NIN, LDY>(a, lane, wid, in, ys);
+  }
+  __syncthreads();
+
+  float logit[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) logit[mt][i] = 0.f;
+  for (int g = 0; g < ng; ++g) {
+    int tn[TG], tx[TG];
+    float bo[TG], wo[TG];
+#pragma unroll
+    for (int jj = 0; jj < TG; ++jj) {
+      tn[jj] = tile_of(g, jj);
+      tx[jj] = tile_of(g + 1, jj);
+      const int col = tn[jj] * 16 + n;
+      bo[jj] = b1h[col];
+      wo[jj] = w2h[col];
+    }
+    f32x4_t c[4][TG];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+      for (int jj = 0; jj < TG; ++jj) c[mt][jj] = (f32x4_t){0.f, 0.f, 0.f, 0.f};
+    // the A fragments are the same for every group: an opaque base keeps the
+    // compiler from hoisting all of them out of the group loop (128 registers)
+    int abase = n * LDY + kg * 8;
+    asm volatile("" : "+v"(abase));
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      bf16x8_t ax[4];
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+        ax[mt] = __builtin_bit_cast(bf16x8_t, *(const u32x4_t*)(&ys[mt * 16 * LDY + abase + ks * 32]));
+      // the slot's next k-step: this group's ks + PQ, else the next group's
+      const int slot = ks % PQ;
+      u32x4_t bcur[TG];
+#pragma unroll
+      for (int jj = 0; jj < TG; ++jj) {
+        bcur[jj] = bq[slot][jj];
+        bq[slot][jj] = ks + PQ < KS ? ph[((int64_t)tn[jj] * KS + ks + PQ) * 64] : ph[((int64_t)tx[jj] * KS + ks + PQ - KS) * 64];
+      }
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int jj = 0; jj < TG; ++jj)
+          c[mt][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ax[mt], __builtin_bit_cast(bf16x8_t, bcur[jj]), c[mt][jj], 0, 0, 0);
+    }
+    // the group's 64 values of this lane as 32 bf16 pairs (rows i, i+1 of the
+    // lane's column in tile jj): the layer outputs z and their table entries;
+    // dmax = the largest table offset (offsets >= kActBytes lie outside)
+    uint32_t zz[32], tvp[32];
+    u16x2_t dmax = {0, 0};
+#pragma unroll
+    for (int p = 0; p < 32; ++p) {
+      const int mt = p >> 3, jj = (p >> 1) & 3, i = (p & 1) * 2;
+      uint32_t z2;
+      if (PREC == 1) {
+        const uint32_t r = cvt_pk_bf16(c[mt][jj][i], c[mt][jj][i + 1]);
+        z2 = cvt_pk_bf16(bf16lo(r) + bo[jj], bf16hi(r) + bo[jj]);
+      } else {
+        z2 = cvt_pk_bf16(c[mt][jj][i] + bo[jj], c[mt][jj][i + 1] + bo[jj]);
+      }
+      zz[p] = z2;
+      // byte offset of bf16(act(z)) in the table, per 16-bit half
+      const u16x2_t zv = __builtin_bit_cast(u16x2_t, z2);
+      const u16x2_t d2 = (u16x2_t)(zv << 1) - (u16x2_t)kActBias2;
+      dmax = __builtin_elementwise_max(dmax, d2);
+      const u16x2_t off = (u16x2_t)(zv >> 15) * (u16x2_t)kActBytes + __builtin_elementwise_min(d2, (u16x2_t)(kActBytes - 2));
+      const char* tb = (const char*)s_act;
+      u16x2_t t;
+      t.x = *(const uint16_t*)(tb + off.x);
+      t.y = *(const uint16_t*)(tb + off.y);
+      tvp[p] = __builtin_bit_cast(uint32_t, t);
+    }
+    if (max(dmax.x, dmax.y) >= kActBytes) {  // rare: some value lies outside the table
+#pragma unroll
+      for (int p = 0; p < 32; ++p) {
+        const u16x2_t zv = __builtin_bit_cast(u16x2_t, zz[p]);
+        const u16x2_t d2 = (u16x2_t)(zv << 1) - (u16x2_t)kActBias2;
+        if (d2.x >= kActBytes) tvp[p] = (tvp[p] & 0xffff0000u) | (__float_as_uint(activation(bf16lo(zz[p]), a.act, PREC)) >> 16);
+        if (d2.y >= kActBytes) tvp[p] = (tvp[p] & 0xffffu) | (__float_as_uint(activation(bf16hi(zz[p]), a.act, PREC)) & 0xffff0000u);
+      }
+    }
+    // w2 multiply-adds in the lane's column order (tiles 4g, 4g+1, ...)
+#pragma unroll
+    for (int jj = 0; jj < TG; ++jj) {
+      if (TG * g + jj >= nw) break;
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; i += 2) {
+          const uint32_t t = tvp[mt * 8 + jj * 2 + i / 2];
+          logit[mt][i] = fmaf(wo[jj], bf16lo(t), logit[mt][i]);
+          logit[mt][i + 1] = fmaf(wo[jj], bf16hi(t), logit[mt][i + 1]);
         }
     }
   }
@@ -820,8 +1024,8 @@ extern "C" int wgkv_gate_scores(
 #define WGKV_GATE_BF16(DD, NN)                                                                              \
   do {                                                                                                      \
     if (precision == 0) hipLaunchKernelGGL((gate_bf16_kernel<DD, NN, 0>), grid, dim3(kThreads), 0, st, a, pk); \
-    else if (precision == 1) hipLaunchKernelGGL((gate_bf16_kernel<DD, NN, 1>), grid, dim3(kThreads), 0, st, a, pk); \
-    else hipLaunchKernelGGL((gate_bf16_kernel<DD, NN, 2>), grid, dim3(kThreads), 0, st, a, pk);             \
+    else if (precision == 1) hipLaunchKernelGGL((gate_bf16p_kernel<DD, NN, 1>), grid, dim3(kThreads), 0, st, a, pk); \
+    else hipLaunchKernelGGL((gate_bf16p_kernel<DD, NN, 2>), grid, dim3(kThreads), 0, st, a, pk);             \
   } while (0)
       if (head_dim == 128) {
         if (n_in == 1) WGKV_GATE_BF16(128, 1);

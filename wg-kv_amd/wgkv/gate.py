@@ -107,6 +107,33 @@ class GatingPredictor(nn.Module):
         self.__dict__["_packed_cache"] = (key, packed)
         return packed
 
+    def _launch_plan(self, dtype, device, packed_path):
+        """The parameter part of wgkv_gate_scores' arguments (fp32 copies,
+        packed weights, arithmetic), made once and remade when a parameter
+        is replaced or changes version.  The parameters are read through the
+        modules' own dictionaries: a chunked prompt calls the gate once per
+        chunk and layer, and nn.Module attribute lookups cost more host time
+        than the rest of the call."""
+        mods = self._modules
+        c1, c2 = mods["conv1"]._parameters, mods["conv2"]._parameters
+        params = [c1["weight"], c1["bias"], c2["weight"], c2["bias"]]
+        for name in ("pre_key_norm", "post_key_norm", "value_norm"):
+            m = mods[name]
+            if isinstance(m, GatingRMSNorm):
+                params.append(m._parameters["weight"])
+        key = (dtype, device, packed_path) + tuple((id(q), q._version) for q in params)
+        hit = self.__dict__.get("_plan")
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        wn = self._norm_weights()
+        prec = self.precision(dtype)
+        packed = self.packed_weights(prec) if packed_path else None
+        plan = _GateParams(wn[0], wn[1], wn[2], self._f32(self.conv1.weight), self._f32(self.conv1.bias),
+                           self._f32(self.conv2.weight), self._f32(self.conv2.bias), self.inner_dim, self.act,
+                           self.g_rms, 0.0 if self.g_fast_path else float(self.g_epsilon), packed, prec)
+        self.__dict__["_plan"] = (key, plan)
+        return plan
+
     def scores_and_mask(self, pre_key, post_key, value, threshold, scores_out=None, mask_out=None, want_scores=True,
                         active=None):
         """(B, H, S, D) inputs -> (scores f32 (B,H,S) or None, mask bool (B,H,S)).
@@ -115,20 +142,12 @@ class GatingPredictor(nn.Module):
         B, H, S, D = post_key.shape
         if H != self.num_kv_heads or D != self.head_dim:
             raise AssertionError("gate input shape does not match the predictor")
-        wn = self._norm_weights()
-        w1 = self._f32(self.conv1.weight)
-        prec = self.precision(post_key.dtype)
-        packed = None
-        if post_key.dtype == torch.bfloat16 and S > 4 and post_key.is_cuda:
-            packed = self.packed_weights(prec)
-        return gate_scores_and_mask(
-            pre_key if "pre_k" in self.g_inputs else None, post_key if "post_k" in self.g_inputs else None,
-            value if "v" in self.g_inputs else None, wn[0], wn[1], wn[2],
-            w1, self._f32(self.conv1.bias), self._f32(self.conv2.weight),
-            self._f32(self.conv2.bias), self.inner_dim, self.act, self.g_rms,
-            0.0 if self.g_fast_path else float(self.g_epsilon), threshold,
-            like=post_key, scores_out=scores_out, mask_out=mask_out, want_scores=want_scores, w1_packed=packed,
-            active=active, precision=prec)
+        dt = post_key.dtype
+        plan = self._launch_plan(dt, post_key.device, dt == torch.bfloat16 and S > 4 and post_key.is_cuda)
+        ins = self.g_inputs
+        return _run_gate(plan, pre_key if "pre_k" in ins else None, post_key if "post_k" in ins else None,
+                         value if "v" in ins else None, threshold, post_key, scores_out, mask_out, want_scores,
+                         active)
 
     def forward(self, pre_key, post_key, value):
         """Scores (B, H, S) as the reference's forward returns them: float32,
@@ -162,6 +181,21 @@ def pack_weights(w_pre, w_post, w_v, w1, g_inputs, rms, num_kv_heads, head_dim, 
     return packed
 
 
+class _GateParams:
+    """wgkv_gate_scores' parameter arguments, checked once: the fp32 tensors
+    are held so the pointers stay valid."""
+
+    def __init__(self, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, w1_packed, precision):
+        for w in (w_pre, w_post, w_v, w1, b1, w2, b2):
+            if w is not None and (w.dtype != torch.float32 or not w.is_contiguous()):
+                raise TypeError("gate parameters must be contiguous fp32")
+        self.keep = (w_pre, w_post, w_v, w1, b1, w2, b2, w1_packed)
+        self.ptrs = (_ptr(w_pre), _ptr(w_post), _ptr(w_v), _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2))
+        self.inner = int(inner)
+        self.tail = (int(act), int(bool(rms)), int(precision), float(clamp_min))
+        self.packed = _ptr(w1_packed)
+
+
 def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms,
                          clamp_min, threshold, like=None, scores_out=None, mask_out=None, want_scores=True,
                          w1_packed=None, active=None, precision=0):
@@ -178,7 +212,11 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
     fast / Conv1d path rounding, threshold compared in bf16; w1_packed made
     with the same precision).  Returns (scores f32 (B,H,S) or None, mask bool
     (B,H,S))."""
-    ins = {"pre_k": pre_key, "post_k": post_key, "v": value}
+    plan = _GateParams(w_pre, w_post, w_v, w1, b1, w2, b2, inner, act, rms, clamp_min, w1_packed, precision)
+    return _run_gate(plan, pre_key, post_key, value, threshold, like, scores_out, mask_out, want_scores, active)
+
+
+def _run_gate(plan, pre_key, post_key, value, threshold, like, scores_out, mask_out, want_scores, active):
     ref = like if like is not None else next(t for t in (post_key, pre_key, value) if t is not None)
     B, H, S, D = ref.shape
     dt = ref.dtype
@@ -186,21 +224,19 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
         raise TypeError("gate inputs must be bf16 or fp32")
     bits = 0
     args = []
-    for name in ("pre_k", "post_k", "v"):
-        t = ins[name]
+    for bit, t in ((1, pre_key), (2, post_key), (4, value)):
         if t is not None:
             if t.dtype != dt or t.shape != ref.shape or t.stride(3) != 1:
                 raise AssertionError("gate inputs must share shape/dtype with a contiguous last dim")
-            _require_cuda(t)
-            bits |= _INPUT_BITS[name]
-            args += [_ptr(t), t.stride(0), t.stride(1), t.stride(2)]
+            if not t.is_cuda:
+                _require_cuda(t)
+            bits |= bit
+            st = t.stride()
+            args += (t.data_ptr(), st[0], st[1], st[2])
         else:
-            args += [None, 0, 0, 0]
+            args += (None, 0, 0, 0)
     if bits == 0:
         raise AssertionError("the gate needs at least one input")
-    for w in (w_pre, w_post, w_v, w1, b1, w2, b2):
-        if w is not None and (w.dtype != torch.float32 or not w.is_contiguous()):
-            raise TypeError("gate parameters must be contiguous fp32")
     dev = ref.device
     scores = None
     if want_scores:
@@ -209,17 +245,22 @@ def gate_scores_and_mask(pre_key, post_key, value, w_pre, w_post, w_v, w1, b1, w
     mk = mask.view(torch.uint8)
     if active is not None and (active[0].dtype != torch.int32 or not active[0].is_cuda):
         raise TypeError("active must be a device int32 tensor")
-    ws = _decode_workspace(dev, B, H, int(inner)) if S <= 4 else None
+    ws = _decode_workspace(dev, B, H, plan.inner) if S <= 4 else None
+    if scores is not None:
+        sst = scores.stride()
+        sargs = (scores.data_ptr(), sst[0], sst[1])
+    else:
+        sargs = (None, 0, 0)
+    mst = mk.stride()
     st = _lib.lib().wgkv_gate_scores(
         *args,
         0 if dt == torch.bfloat16 else 1, bits,
-        _ptr(w_pre), _ptr(w_post), _ptr(w_v),
-        _ptr(w1), _ptr(b1), _ptr(w2), _ptr(b2),
-        B, H, S, D, int(inner),
-        int(act), int(bool(rms)), int(precision), float(clamp_min), float(threshold),
-        _ptr(scores), scores.stride(0) if scores is not None else 0, scores.stride(1) if scores is not None else 0,
-        _ptr(mk), mk.stride(0), mk.stride(1),
-        _ptr(w1_packed),
+        *plan.ptrs,
+        B, H, S, D, plan.inner,
+        *plan.tail, float(threshold),
+        *sargs,
+        mk.data_ptr(), mst[0], mst[1],
+        plan.packed,
         _ptr(active[0]) if active is not None else None, int(active[1]) if active is not None else 0,
         _ptr(ws), 0 if ws is None else ws.numel(),
         _lib.stream_handle(dev))
