@@ -55,21 +55,25 @@ struct NormArgs {
 // the mean of squares is summed per thread, over each wave, then over the
 // four waves in order.  emit_res(ch, h chunk) and emit(ch, out chunk) receive
 // the results.
-template <bool RES, typename EmitOut, typename EmitRes>
-WGKV_DEVICE void rms_norm_row(const uint16_t* x, const uint16_t* res, const uint16_t* w, int hidden, float eps,
-                              float* s_sum, EmitOut emit, EmitRes emit_res) {
+// rms_norm_row_from takes the thread's chunks already loaded (xc, and rc
+// with RES) and gets the norm weight's chunk c (chunk index ch) from
+// wchunk(c, ch): the GEMV prologue requests all of them before its weight
+// slices.  NC chunks per thread must cover the row (hidden <= 8 * NC * 256).
+template <bool RES, int NC, typename WChunk, typename EmitOut, typename EmitRes>
+WGKV_DEVICE void rms_norm_row_from(const u32x4_t (&xc)[NC], const u32x4_t (&rc)[NC], WChunk wchunk, int hidden,
+                                   float eps, float* s_sum, EmitOut emit, EmitRes emit_res) {
   const int t = threadIdx.x;
   const int nch = hidden / 8;
-  float h[kNormChunks][8];
+  float h[NC][8];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < kNormChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int ch = t + c * kNormThreads;
     if (ch < nch) {
-      unpack8(*(const u32x4_t*)(x + ch * 8), h[c]);
+      unpack8(xc[c], h[c]);
       if (RES) {
         float r[8];
-        unpack8(*(const u32x4_t*)(res + ch * 8), r);
+        unpack8(rc[c], r);
 #pragma unroll
         for (int i = 0; i < 8; ++i) h[c][i] = rb(h[c][i] + r[i]);
         emit_res(ch, pack8(h[c]));
@@ -86,16 +90,35 @@ WGKV_DEVICE void rms_norm_row(const uint16_t* x, const uint16_t* res, const uint
   for (int wv = 0; wv < kNormThreads / 64; ++wv) tot += s_sum[wv];
   const float scale = rsqrtf(tot / (float)hidden + eps);
 #pragma unroll
-  for (int c = 0; c < kNormChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int ch = t + c * kNormThreads;
     if (ch < nch) {
       float wv[8], y[8];
-      unpack8(*(const u32x4_t*)(w + ch * 8), wv);
+      unpack8(wchunk(c, ch), wv);
 #pragma unroll
       for (int i = 0; i < 8; ++i) y[i] = wv[i] * rb(h[c][i] * scale);
       emit(ch, pack8(y));
     }
   }
+}
+
+template <int NC>
+WGKV_DEVICE void load_norm_chunks(const uint16_t* p, int hidden, u32x4_t (&c)[NC]) {
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    const int ch = threadIdx.x + i * kNormThreads;
+    if (ch < hidden / 8) c[i] = *(const u32x4_t*)(p + ch * 8);
+  }
+}
+
+template <bool RES, typename EmitOut, typename EmitRes>
+WGKV_DEVICE void rms_norm_row(const uint16_t* x, const uint16_t* res, const uint16_t* w, int hidden, float eps,
+                              float* s_sum, EmitOut emit, EmitRes emit_res) {
+  u32x4_t xc[kNormChunks], rc[kNormChunks];
+  load_norm_chunks(x, hidden, xc);
+  if (RES) load_norm_chunks(res, hidden, rc);
+  rms_norm_row_from<RES, kNormChunks>(
+      xc, rc, [&](int, int ch) { return *(const u32x4_t*)(w + ch * 8); }, hidden, eps, s_sum, emit, emit_res);
 }
 
 template <bool RES>
@@ -274,6 +297,7 @@ WGKV_DEVICE float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v_t, a), __builtin_bit_cast(bf16x2v_t, b), c, false);
 }
 
+template <bool XPRE>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   extern __shared__ u32x4_t xs[];
   __shared__ float s_sum[kGemvWaves];
@@ -296,7 +320,18 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   const u32x4_t* w0 = (const u32x4_t*)(a.w + (int64_t)r0 * a.w_rs);
   const u32x4_t* w1 = (const u32x4_t*)(a.w + (int64_t)r1 * a.w_rs);
   const int ns = a.K / 8;
-  // the first slices of the rows are requested before x is staged
+  // XPRE (the norm prologue, K <= 4096): x, the norm's residual and its
+  // weight are requested first, then the first slices of the rows.  Vector memory loads
+  // complete in order, so the norm then runs while the row slices are still
+  // in flight; requested after them (the other instance: no norm, or longer
+  // rows) x waits for the slices, which costs only the staging there.
+  constexpr int kXPre = 2;  // 16-byte chunks per thread: 2 * 8 * 256 = 4096 elements
+  u32x4_t xc[kXPre], rc[kXPre], wc[kXPre];
+  if constexpr (XPRE) {
+    load_norm_chunks(a.x, a.K, xc);
+    if (a.norm_res) load_norm_chunks(a.norm_res, a.K, rc);
+    load_norm_chunks(a.norm_w, a.K, wc);
+  }
   u32x4_t b0[kGemvBatch], b1[kGemvBatch];
 #pragma unroll
   for (int u = 0; u < kGemvBatch; ++u) {
@@ -306,12 +341,16 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   }
   if (a.norm_w) {
     auto to_lds = [&](int ch, u32x4_t v) { xs[ch] = v; };
-    if (a.norm_res) {
-      rms_norm_row<true>(a.x, a.norm_res, a.norm_w, a.K, a.eps, s_sum, to_lds, [&](int ch, u32x4_t v) {
-        if (blockIdx.x == 0) ((u32x4_t*)a.norm_res_out)[ch] = v;
-      });
+    auto to_res = [&](int ch, u32x4_t v) {
+      if (blockIdx.x == 0) ((u32x4_t*)a.norm_res_out)[ch] = v;
+    };
+    if constexpr (XPRE) {
+      auto wpre = [&](int c, int) { return wc[c]; };
+      if (a.norm_res) rms_norm_row_from<true, kXPre>(xc, rc, wpre, a.K, a.eps, s_sum, to_lds, to_res);
+      else rms_norm_row_from<false, kXPre>(xc, rc, wpre, a.K, a.eps, s_sum, to_lds, [](int, u32x4_t) {});
     } else {
-      rms_norm_row<false>(a.x, nullptr, a.norm_w, a.K, a.eps, s_sum, to_lds, [](int, u32x4_t) {});
+      if (a.norm_res) rms_norm_row<true>(a.x, a.norm_res, a.norm_w, a.K, a.eps, s_sum, to_lds, to_res);
+      else rms_norm_row<false>(a.x, nullptr, a.norm_w, a.K, a.eps, s_sum, to_lds, [](int, u32x4_t) {});
     }
   } else {
     for (int sl = threadIdx.x; sl < ns; sl += 64 * kGemvWaves) xs[sl] = ((const u32x4_t*)a.x)[sl];
@@ -525,7 +564,10 @@ extern "C" int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int3
   a.hd = mode == 3 ? head_dim : 2;
   const int npairs = mode == 2 ? n : mode == 3 ? n / 2 : (n + 1) / 2;
   const int blocks = (npairs + kGemvWaves - 1) / kGemvWaves;
-  hipLaunchKernelGGL(gemv_kernel, dim3(blocks), dim3(64 * kGemvWaves), (size_t)k * 2, (hipStream_t)stream, a);
+  if (norm_weight && k <= 4096)
+    hipLaunchKernelGGL(gemv_kernel<true>, dim3(blocks), dim3(64 * kGemvWaves), (size_t)k * 2, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(gemv_kernel<false>, dim3(blocks), dim3(64 * kGemvWaves), (size_t)k * 2, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
