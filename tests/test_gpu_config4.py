@@ -18,6 +18,8 @@ Checked:
   the same mask on the CPU."""
 import numpy as np
 import pytest
+
+import parity_log
 import torch
 
 from oracle import attention
@@ -98,8 +100,8 @@ def test_config4_chunked_pipeline():
     refo = attention.sparse_prefill_rows(qh, kh, vh, mask.cpu(), W, rows, D ** -0.5)
     got = out[rows].float().cpu().transpose(0, 1)[None]  # (1, Hq, rows, D)
     err = (got.double() - refo).abs()
-    print(f"[config 4] {len(rows)} sampled rows vs fp64: max_abs {err.max().item():.2e} "
-          f"mean_abs {err.mean().item():.2e}", flush=True)
+    parity_log.report(f"[config 4] {len(rows)} sampled rows vs fp64: max_abs {err.max().item():.2e} "
+          f"mean_abs {err.mean().item():.2e}")
     assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
 
     # the logical cache against the oracle's replay of the mask
@@ -117,5 +119,5 @@ def test_config4_chunked_pipeline():
         r = (ids[:, None] * 16 + torch.arange(16)[None]).reshape(-1)[:n]
         ka, va = global_entries(cache, 0, h)
         assert torch.equal(ka.cpu(), orc.block_pool_k[r]) and torch.equal(va.cpu(), orc.block_pool_v[r]), h
-    print(f"[config 4] logical cache equals the oracle replay; global lengths "
-          f"{cache.global_lengths[0].tolist()}", flush=True)
+    parity_log.report(f"[config 4] logical cache equals the oracle replay; global lengths "
+          f"{cache.global_lengths[0].tolist()}")

@@ -25,6 +25,8 @@ import math
 import pytest
 import torch
 
+import parity_log
+
 from oracle import attention
 
 pytestmark = pytest.mark.gpu
@@ -34,6 +36,10 @@ S, CHUNK, STEPS, ADMIT = 400000, 4096, 6, 0.30
 
 def say(msg):
     print(f"[config 5 400K] {msg}", flush=True)
+
+
+def record(msg):
+    parity_log.report(f"[config 5 400K] {msg}")
 
 
 @pytest.fixture(scope="module")
@@ -140,7 +146,7 @@ def _check_layer_output(cache, layer_idx, q, seqlens, table, out, scale):
         tb[0, h, :t.numel()] = t
     ref = attention.paged_decode(q.cpu(), kc, vc, seqlens.cpu(), tb, scale)
     err = (out.float().cpu() - ref).abs()
-    say(f"layer {layer_idx} step-1 decode vs fp32 oracle over {int(seqlens.sum())} cached tokens: "
+    record(f"layer {layer_idx} step-1 decode vs fp32 oracle over {int(seqlens.sum())} cached tokens: "
         f"max_abs {err.max().item():.2e} mean_abs {err.mean().item():.2e}")
     assert err.max().item() <= 2e-2 and err.mean().item() <= 2e-3
 
@@ -164,7 +170,7 @@ def test_config5_400k_gated(model):
     n_local = L * H * W // cache.block_size
     pages = int(((gl + cache.block_size - 1) // cache.block_size).sum())
     assert cache.next_free_block == n_local + pages
-    say(f"gated: global lengths equal the admitted counts (per head {int(gl.min())}..{int(gl.max())}, "
+    record(f"gated: global lengths equal the admitted counts (per head {int(gl.min())}..{int(gl.max())}, "
         f"mean {gl.double().mean().item():.0f}); ring flags equal the last {W} mask bits; "
         f"{pages} global pages handed out")
 
@@ -218,7 +224,7 @@ def test_config5_400k_gated(model):
         assert torch.equal(gd.logits.float(), eager_logits[i]), i
     torch.cuda.synchronize()
     cb.raise_if_failed("400K graph decode")
-    say(f"gated: graph steps 2..{STEPS - 1} equal eager bit for bit")
+    record(f"gated: graph steps 2..{STEPS - 1} equal eager bit for bit")
     del gd, cb
     torch.cuda.empty_cache()
 
@@ -243,7 +249,7 @@ def test_config5_400k_full(model):
         torch.cuda.synchronize()
         cache.raise_if_failed("400K full decode")
         assert int(cache.global_lengths.min()) == S - W + 2 and int(cache.global_lengths.max()) == S - W + 2
-        say(f"full: every (layer, head) holds the {S - W} tokens that left the ring, then one more per step")
+        record(f"full: every (layer, head) holds the {S - W} tokens that left the ring, then one more per step")
         del cache
     finally:
         m.cfg.g_expand, m.cfg.random_sparsity = 4.0, None

@@ -9,6 +9,8 @@ import os
 
 import numpy as np
 import pytest
+
+import parity_log
 import torch
 
 import scenarios
@@ -45,10 +47,10 @@ def compare(scores, mask, ref, thr, label, ambiguous=None):
     clean = ~amb
     dmax_clean = d[clean].max() if clean.any() else 0.0
     dmax_amb = d[amb].max() if amb.any() else 0.0
-    print(f"[gate parity] {label}: max|dg| {dmax_clean:.2e} (ambiguous tokens {dmax_amb:.2e}); "
+    parity_log.report(f"[gate parity] {label}: max|dg| {dmax_clean:.2e} (ambiguous tokens {dmax_amb:.2e}); "
           f"near-threshold (|g-tau|<1e-6) {int(near.sum())}; bf16-ambiguous {int(amb.sum())}; "
           f"flips among near {int((flips & near).sum())}, ambiguous {int((flips & amb & ~near).sum())}, "
-          f"other {int((flips & ~near & ~amb).sum())}", flush=True)
+          f"other {int((flips & ~near & ~amb).sum())}")
     assert dmax_clean <= 2e-6
     assert dmax_amb <= 1e-3
     assert not (flips & ~near & ~amb).any()

@@ -23,6 +23,8 @@ import os
 
 import numpy as np
 import pytest
+
+import parity_log
 import torch
 
 import scenarios
@@ -57,9 +59,9 @@ def check(label, scores, mask, gold, thr, lo, hi, max_flagged_frac=0.04):
     flips = m != (gold > thr)
     inside = (s >= lo) & (s <= hi)
     n = gold.numel()
-    print(f"[gate bf16] {label}: {n} tokens, flagged {int(flagged.sum())}, scores differ {int(diff.sum())} "
+    parity_log.report(f"[gate bf16] {label}: {n} tokens, flagged {int(flagged.sum())}, scores differ {int(diff.sum())} "
           f"(all flagged: {not bool((diff & ~flagged).any())}), admission flips {int(flips.sum())}, "
-          f"admitted {(gold > thr).double().mean().item():.3f}", flush=True)
+          f"admitted {(gold > thr).double().mean().item():.3f}")
     assert bool(inside.all()), f"{int((~inside).sum())} scores outside the range the kernel's arithmetic allows"
     assert not bool((diff & ~flagged).any()), "a score pinned to the reference's differs"
     assert torch.equal(m, s > thr), "admission does not follow the kernel's score"
@@ -155,7 +157,7 @@ def test_activation_table_within_float32_bounds(act):
     lo, hi = gout.activation_bounds(act)
     lo, hi = lo[bits], hi[bits]
     differ = got != torch_tab
-    print(f"[gate bf16] {act} table: {n_tab} entries, {int(differ.sum())} differ from torch, "
-          f"{int((lo != hi).sum())} with two or more float32 outcomes", flush=True)
+    parity_log.report(f"[gate bf16] {act} table: {n_tab} entries, {int(differ.sum())} differ from torch, "
+          f"{int((lo != hi).sum())} with two or more float32 outcomes")
     assert bool(((got >= lo) & (got <= hi)).all()), "a table entry outside the float32 bounds"
     assert not bool((differ & (lo == hi)).any())
