@@ -190,7 +190,7 @@ def test_many_chunks_batch1():
 
 def test_shared_workspace_across_shapes():
     """The per-head arrival counters live in the one shared workspace: calls
-    that alternate between 12-wave workgroups (batch 1, few heads) and 4-wave
+    that alternate between 8-wave workgroups (batch 1, few heads) and 4-wave
     ones (B*Hkv >= 32), and between head_dim 128 and 64, each match the
     oracle, and repeating the first call gives the same bits (every call
     leaves its counters zero for the next)."""

@@ -7,9 +7,12 @@
 // One workgroup owns one chunk, and its waves take 64-token "quads" (4
 // sub-pages) in turn.  Every K/V byte of the cache is read exactly once, for
 // all G query heads of the KV head together.  Workgroups have 4 waves (three
-// per CU) or, when the batch has few heads (B*Hkv < 32, G <= 4), 12 waves
+// per CU) or, when the batch has few heads (B*Hkv < 32, G <= 4), 8 waves
 // (one per CU), so that a head is cut into ~CUs/(B*Hkv) chunks rather than
-// three times as many.
+// three times as many.  (8 rather than 12 waves: the 2048 waves dispatch
+// sooner, and two per SIMD keep enough K/V loads in flight -- batch 1 at
+// 128K 23.6 -> 22.9 us, 8 heads of ~80K tokens 55.8 -> 53.6 us, at 32K
+// 13.5 -> 13.7 us.)
 //
 // Per quad and wave:
 //   * K is read in the MFMA B-operand layout (lane n%16 = token row, lane/16
@@ -26,7 +29,7 @@
 // writes its output directly.  Otherwise the chunk stores (m, l, acc)
 // partials, which are combined with the log-sum-exp rule in a fixed chunk
 // order (so the result does not depend on which chunk finishes first):
-//   * 12-wave workgroups: with device-coherent stores; the chunk counts its
+//   * 8-wave workgroups: with device-coherent stores; the chunk counts its
 //     arrival on the head's counter, and the last chunk of the head to
 //     arrive merges the head's ~30 partials (one round of loads) and resets
 //     the counter -- one launch per call, ~2 us less at batch 1 than a
@@ -51,11 +54,11 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.f;  // log2 units a running maximum may lag the scores
 
 // Resident workgroups per CU: with 4 waves, G <= 4 fits three (158 VGPRs at
-// D=128, G=4), G = 8 (two head groups, 83 KB of LDS) one; a 12-wave
-// workgroup (G <= 4) fills a CU alone (three waves per SIMD).
+// D=128, G=4), G = 8 (two head groups, 83 KB of LDS) one; an 8-wave
+// workgroup (G <= 4) fills a CU alone (two waves per SIMD).
 constexpr int wg_per_cu(int G, int NW) { return NW > 4 ? 1 : (G > 4 ? 1 : 3); }
 constexpr int waves_per_simd(int G, int NW) { return NW > 4 ? NW / 4 : wg_per_cu(G, NW); }
-// Batches with fewer heads than this (and G <= 4) take 12-wave workgroups.
+// Batches with fewer heads than this (and G <= 4) take 8-wave workgroups.
 constexpr int kWideBelowBH = 32;
 
 struct DecodeArgs {
@@ -81,7 +84,7 @@ struct DecodeArgs {
   float* part_l;
   float* part_acc;
   // arrival counters, one per (b, h): zero before a call, zero after it
-  // (12-wave workgroups)
+  // (8-wave workgroups)
   int* counter;
   // [B*Hkv + 1] first chunk of each (b,h) and the chunk count, written by
   // the split kernel for decode_merge_kernel (4-wave workgroups)
@@ -108,7 +111,7 @@ struct Plan {
 
 // Sub-pages per chunk: the total over the chunk slots, rounded up to a
 // multiple of 16 (4-wave workgroups: at least one quad per wave) or of 4
-// (12-wave workgroups: chunks stay quad-aligned, and the ~CU-count chunks of
+// (8-wave workgroups: chunks stay quad-aligned, and the ~CU-count chunks of
 // a batch-1 call fill the CUs evenly), at least 16.
 template <int NW>
 __device__ __forceinline__ int chunk_subpages(int total, int target) {
@@ -268,7 +271,7 @@ void decode_split_kernel(DecodeArgs a) {
   constexpr int NV = 64 / RPI;     // V loads per quad
   constexpr int NG = (G + 3) / 4;  // groups of 4 query heads (MFMA A operands)
   static_assert(G <= kMaxG, "query heads per KV head");
-  static_assert(NW == 4 || (NW == 12 && G <= 4), "4-wave workgroups, or 12-wave ones for G <= 4");
+  static_assert(NW == 4 || (NW == 8 && G <= 4), "4-wave workgroups, or 8-wave ones for G <= 4");
 
   constexpr bool kFused = NW > 4;  // the last chunk of a head merges (see top)
   // s_buf: each wave's (RPI, G, D) accumulators, then the fused merge's
@@ -286,7 +289,7 @@ void decode_split_kernel(DecodeArgs a) {
     __shared__ int s_tmp[kPlanThreads];
     pl = a.B * a.Hkv <= kWaveBH ? plan_wave<NW>(a, w) : plan_block(a, w, s_pref, s_tmp);
   } else {
-    pl = plan_wave<NW>(a, w);  // the host takes 12 waves only for B*Hkv < 32
+    pl = plan_wave<NW>(a, w);  // the host takes 8 waves only for B*Hkv < 32
   }
   if (w >= pl.n_chunks) return;
   const int bh = pl.bh;
@@ -527,8 +530,9 @@ void decode_split_kernel(DecodeArgs a) {
   // Thread t sums the float4 quad t % NQ of the head's (G, D) output over the
   // chunks grp, grp + GROUPS, ... of the head (grp = t / NQ), all loads of a
   // batch issued before the (branch-free) online update consumes them; the
-  // groups are then combined through LDS in group order.  12-wave workgroups
-  // read the ~30 partials of a batch-1 head in one round of loads.
+  // groups are then combined through LDS in group order.  8-wave workgroups
+  // read the ~32 partials of a batch-1 head (G = 4, D = 128) in one round of
+  // loads.
   constexpr int NQ = G * D / 4;
   constexpr int GROUPS = kThreads / NQ;
   constexpr int kBatch = 8;
@@ -684,7 +688,7 @@ hipError_t launch_nw(DecodeArgs a, hipStream_t st) {
   const int BH = a.B * a.Hkv;
   const int slots = min(kMaxSlots, cu_count() * wg_per_cu(G, NW));
   // The plan makes at most target_chunks + BH chunks (one remainder per
-  // head; 12-wave plans stay within target_chunks).  With three workgroups
+  // head; 8-wave plans stay within target_chunks).  With three workgroups
   // per CU a few chunks beyond the slots only fill the first free slots
   // (aiming at slots - BH measured 0.5 % slower at batch 8).
   a.target_chunks = slots;
@@ -698,7 +702,7 @@ hipError_t launch_nw(DecodeArgs a, hipStream_t st) {
 template <int D, int G>
 hipError_t launch(const DecodeArgs& a, hipStream_t st) {
   if constexpr (G <= 4) {
-    if (a.B * a.Hkv < kWideBelowBH) return launch_nw<D, G, 12>(a, st);
+    if (a.B * a.Hkv < kWideBelowBH) return launch_nw<D, G, 8>(a, st);
   }
   return launch_nw<D, G, 4>(a, st);
 }
