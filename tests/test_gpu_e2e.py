@@ -86,6 +86,24 @@ def test_run_reports():
     assert r.kv_mib > 0 and r.model_mib > 0
 
 
+@pytest.mark.parametrize("qwen3", [False, True])
+def test_post_attention_norm_in_mlp_is_bit_identical(qwen3):
+    """A decode row's post-attention RMSNorm (with the residual add) run in
+    the workgroups of the gate/up product gives the logits of the separate
+    norm launch bit for bit, step after step."""
+    print(f"[e2e] post-attention norm inside the MLP qwen3={qwen3}", flush=True)
+    m = tiny_model(True, **({"qk_norm": True, "g_expand": 1.5} if qwen3 else {}))
+    ids = torch.randint(0, 1000, (1, 400), generator=torch.Generator().manual_seed(6)).to(DEV)
+    outs = {}
+    for fused in (True, False):
+        for layer in m.layers:
+            layer.post_norm_in_mlp = fused
+        outs[fused], _, toks = prefill_then_decode(m, ids, 256, 6, feed=outs.get("toks"))
+        outs.setdefault("toks", toks)
+    for i, (a, b) in enumerate(zip(outs[True], outs[False])):
+        assert torch.equal(a, b), (i, (a - b).abs().max())
+
+
 @pytest.mark.parametrize("gated,qwen3", [(True, False), (False, False), (True, True)])
 def test_graph_decode_matches_eager(gated, qwen3):
     """A captured decode step replayed 6 times (with eager host work and

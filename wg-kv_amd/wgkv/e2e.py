@@ -74,11 +74,24 @@ class MLP(nn.Module):
         self.up_proj.weight = nn.Parameter(w[n:], requires_grad=False)
         self._gate_up = w
 
-    def forward(self, x, residual=None):
+    def forward(self, x, residual=None, norm=None):
         """down(silu(gate(x)) * up(x)) (+ residual, the decoder's add after
         the MLP).  A decode step's row: two launches (the stacked gate/up
-        product with SwiGLU, the down product with the residual add)."""
+        product with SwiGLU, the down product with the residual add).  With
+        norm (the post-attention RMSNorm) x is the attention output and the
+        MLP's input is norm(x + residual), whose sum is also the residual the
+        down product adds; for a decode row the norm and the add run in the
+        workgroups of the gate/up product, bit for bit the separate norm."""
         gu = self._gate_up
+        if norm is not None:
+            if (gu is not None and gu.device == x.device and residual is not None
+                    and model_ops.rms_norm_linear_usable(x, norm.weight, gu, residual)):
+                act, h = model_ops.rms_norm_linear(x, norm.weight, norm.eps, gu, residual=residual, mode=2)
+                return model_ops.linear(act, self.down_proj.weight, residual=h)
+            if residual is None:
+                x = norm(x)
+            else:
+                x, residual = norm(x, residual=residual)
         if gu is not None and gu.device == x.device and model_ops.gemv_usable(x, gu):
             return model_ops.linear(model_ops.swiglu_linear(x, gu), self.down_proj.weight, residual=residual)
         # prompts: one GEMM for gate and up (hipBLASLt at 4096 rows: 635 us
@@ -103,6 +116,9 @@ class DecoderLayer(nn.Module):
         self.self_attn = LlamaAttention(cfg, idx, qk_norm=qk_norm)
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size)
         self.mlp = MLP(cfg.hidden_size, inter)
+        # a decode row's post-attention norm runs inside the MLP's first
+        # product; off when a timer must see it with the attention
+        self.post_norm_in_mlp = True
 
     def rmsnorm_and_self_attn(self, x, pos_emb, cache):
         """Input norm, attention, residual add and the post-attention norm
@@ -114,6 +130,9 @@ class DecoderLayer(nn.Module):
         return x, mlp_in
 
     def forward(self, x, pos_emb, cache):
+        if self.post_norm_in_mlp and x.numel() == x.shape[-1]:
+            h, _, _ = self.self_attn(3, x, pos_emb, None, cache, input_norm=self.input_layernorm)
+            return self.mlp(h, residual=x, norm=self.post_attention_layernorm)
         residual, h = self.rmsnorm_and_self_attn(x, pos_emb, cache)
         return self.mlp(h, residual=residual)  # residual + mlp(h)
 
@@ -375,6 +394,7 @@ def install_timing(model, granularity="kernel"):
     for layer in model.layers:
         a = layer.self_attn
         if granularity == "rms_linear_attn":
+            layer.post_norm_in_mlp = False
             layer.rmsnorm_and_self_attn = t.timed("attn", layer.rmsnorm_and_self_attn)
         elif granularity == "linear_attn":
             a.forward = t.timed("attn", a.forward)

@@ -165,6 +165,15 @@ def rms_norm_linear(x, norm_weight, eps, weight, residual=None, mode=0):
     return y, h
 
 
+def rms_norm_linear_usable(x, norm_weight, weight, residual=None):
+    """rms_norm_linear takes this row, norm weight, product weight and
+    residual (the norm prologue handles rows of up to 8192 elements)."""
+    return (gemv_usable(x, weight) and usable(norm_weight) and norm_weight.is_contiguous()
+            and norm_weight.numel() == x.shape[-1] <= 8192 and norm_weight.data_ptr() % 16 == 0
+            and (residual is None or (usable(residual) and residual.is_contiguous()
+                                      and residual.numel() == x.numel() and residual.data_ptr() % 16 == 0)))
+
+
 def qkv_rope_usable(x, w_qkv, cos, sin, norm_weight=None):
     return (gemv_usable(x, w_qkv) and usable(cos, sin) and cos.numel() == sin.numel() == cos.shape[-1]
             and cos.is_contiguous() and sin.is_contiguous()
