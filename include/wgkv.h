@@ -564,6 +564,30 @@ int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int32_t k, cons
                  const void* cos, const void* sin, void* k_raw,
                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream);
 
+/* wgkv_qkv_rope_ring_write -- wgkv_gemv_ex mode 3 (optional norm_weight
+ * prologue; n = (num_q_heads + 2 num_kv_heads) * head_dim rows) whose
+ * workgroups also do the decode step's ring write of a layer under deferred
+ * gating, i.e. what wgkv_decode_append_ring does with no mask, no promotion
+ * and no advance (decode_wrapper's write, src/modeling_layers.py:1390-1407,
+ * and the attention lengths, :1429-1432): with (local_ptr, local_length) =
+ * ring_state[0..1] and slot = local_length < W ? local_length : local_ptr,
+ * the rotated k, v and the unrotated k of KV head h go to ring row
+ * (layer, h, slot) of pool_k, pool_v (token rows of head_dim, the ring at
+ * rows ((layer * num_kv_heads + h) * W + slot)) and local_pre_key
+ * (num_layers, num_kv_heads, W, head_dim); cache_seqlens (the layer's
+ * num_kv_heads values) = min(local_length + 1, W) + global_lengths[layer *
+ * num_kv_heads + h]; ring_state[2] = slot.  The ring pointers are not
+ * advanced.  A promotion that reads the slot (the first layer's) must run
+ * before the call.  num_kv_heads <= 64.  No counterpart in the reference,
+ * which writes the ring after its projections: one launch fewer per layer
+ * for graph-captured decode steps. */
+int wgkv_qkv_rope_ring_write(const void* w, int64_t w_row_stride, int32_t k, const void* x, void* y,
+                             const void* norm_weight, float eps, const void* cos, const void* sin, void* k_raw,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t layer, int32_t num_layers, int32_t local_window, int32_t* ring_state,
+                             void* pool_k, void* pool_v, void* local_pre_key,
+                             const int32_t* global_lengths, int32_t* cache_seqlens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

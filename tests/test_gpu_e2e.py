@@ -11,16 +11,16 @@ pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
 
 
-def tiny_model(gated=True, S=1000, steps=8, W=128, **kw):
+def tiny_model(gated=True, S=1000, steps=8, W=128, layers=2, **kw):
     from wgkv import e2e
-    ec = e2e.E2EConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+    ec = e2e.E2EConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=layers, num_attention_heads=4,
                        num_key_value_heads=2, vocab_size=1024, rope_theta=10000.0, local_window_size=W, **kw)
     torch.manual_seed(0)
     prev = torch.get_default_dtype()
     torch.set_default_dtype(torch.bfloat16)
     with torch.device(DEV):
         m = e2e.LlamaLite(ec, gated=gated, max_tokens_per_head=S + steps + 2 * W,
-                          max_total_tokens=2 * 2 * (S + steps + 2 * W))
+                          max_total_tokens=layers * 2 * (S + steps + 2 * W))
     torch.set_default_dtype(prev)
     m.init_weights(seed=0, std=0.05)
     return m
@@ -158,12 +158,15 @@ def test_graph_decode_deferred_gating(defer, random_sparsity):
     gates every token.  With random_sparsity (the reference's random-admission
     ablation; 0.0 with g_expand 0 is its "full" recipe) the prompt is admitted
     by torch.rand draws and the decode steps by the device's counter-based
-    draws, which the graph replays continue exactly as the eager steps."""
-    from wgkv import e2e
+    draws, which the graph replays continue exactly as the eager steps.
+    Four layers: with deferred gating the captured steps of the two middle
+    layers write the ring from the q/k/v projection's launch
+    (ring_write_in_projection), the eager steps by the append."""
+    from wgkv import e2e, layers
     from wgkv.cache import DualCache
     print(f"[e2e] graph decode, g_defer={defer}, random_sparsity={random_sparsity}, 150 steps, W=64", flush=True)
     W, S, chunk, n = 64, 640, 256, 150
-    m = tiny_model(True, S=S, steps=n, W=W, g_defer=defer)
+    m = tiny_model(True, S=S, steps=n, W=W, layers=4, g_defer=defer)
     ids = torch.randint(0, 1000, (1, S), generator=torch.Generator().manual_seed(5)).to(DEV)
     if random_sparsity is None:
         e2e.calibrate_gates(m, ids, 0.3, chunk=256)
@@ -210,6 +213,15 @@ def test_graph_decode_deferred_gating(defer, random_sparsity):
     assert torch.equal(ca.local_is_global, cb.local_is_global)
     assert torch.equal(ca.global_lengths, cb.global_lengths) and torch.equal(ca.block_table, cb.block_table)
     assert cb.ring_state[:2].tolist() == [cb.local_ptr, cb.local_length]
+    rows = 4 * 2 * W  # the rings of every (layer, head): the pools' first token rows
+    assert torch.equal(ca.block_pool_k[:rows], cb.block_pool_k[:rows])
+    assert torch.equal(ca.block_pool_v[:rows], cb.block_pool_v[:rows])
+    assert torch.equal(ca.cache_seqlens, cb.cache_seqlens)
+    if defer:
+        assert torch.equal(ca.local_pre_key, cb.local_pre_key)
+        # the captured middle layers wrote the ring from the projection, the eager ones did not
+        assert [layers.ring_write_in_projection(l.self_attn, cb) for l in m.layers] == [False, True, True, False]
+        assert not layers.ring_write_in_projection(m.layers[1].self_attn, ca)
 
 
 @pytest.mark.parametrize("granularity", ["rms_linear_attn", "kernel", "predictor"])

@@ -171,6 +171,65 @@ def test_qkv_rope_equals_product_then_rope(with_norm, Hq, Hkv, D):
     assert torch.equal(kraw.transpose(1, 2), k)
 
 
+@pytest.mark.parametrize("ring_full", [False, True])
+@pytest.mark.parametrize("Hq,Hkv,D,layer", [(32, 8, 128, 5), (8, 2, 64, 1)])
+def test_qkv_ring_write_equals_projection_then_append(ring_full, Hq, Hkv, D, layer):
+    """wgkv_qkv_rope_ring_write gives wgkv_gemv_ex mode 3's q/k/v and
+    unrotated k, and writes the ring row, pre-RoPE key, attention lengths and
+    slot that wgkv_decode_append_ring without a mask, promotion or advance
+    writes from them -- bit for bit, every other byte of the pools left as
+    it was, the ring pointers unchanged.  Ring not yet full (slot = length)
+    and full (slot = the oldest)."""
+    from types import SimpleNamespace
+    from wgkv import model_ops, ops
+    from wgkv.attention import LlamaRotaryEmbedding
+    print(f"[model_ops] qkv ring write Hq{Hq} Hkv{Hkv} D{D} layer {layer} full={ring_full}", flush=True)
+    g = torch.Generator().manual_seed(31 + D + int(ring_full))
+    L, W, page = layer + 2, 64, 16
+    hidden = 4096 if D == 128 else 512
+    n = (Hq + 2 * Hkv) * D
+    x = torch.randn(1, 1, hidden, generator=g).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(n, hidden, generator=g) * 0.05).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(DEV)
+    rot = LlamaRotaryEmbedding(D, 500000.0, device=DEV)
+    cos, sin = rot(x, torch.tensor([[4321]], device=DEV))
+    total_pages = L * Hkv * W // page + 16
+    i32 = dict(dtype=torch.int32, device=DEV)
+
+    def cache():
+        g2 = torch.Generator().manual_seed(7)
+        return SimpleNamespace(
+            num_layers=L, num_kv_heads=Hkv, head_dim=D, local_window_size=W, block_size=page,
+            max_tokens_per_head=10 ** 6, total_blocks=total_pages, device_ring=True,
+            block_pool_k=torch.randn(total_pages * page, D, generator=g2).to(torch.bfloat16).to(DEV),
+            block_pool_v=torch.randn(total_pages * page, D, generator=g2).to(torch.bfloat16).to(DEV),
+            local_pre_key=torch.randn(L, Hkv, W, D, generator=g2).to(torch.bfloat16).to(DEV),
+            global_lengths=torch.randint(0, 5000, (L * Hkv,), generator=g2).to(**i32),
+            block_table=torch.zeros(L, Hkv, 4, **i32),
+            local_is_global=torch.zeros(L, Hkv, W, dtype=torch.bool, device=DEV),
+            next_free_block_dev=torch.zeros(1, **i32), status=torch.zeros(1, **i32),
+            ring_state=torch.tensor([37, W, -1] if ring_full else [0, 21, -1], **i32),
+            seqlens=torch.full((Hkv,), -5, **i32))
+
+    a, b = cache(), cache()
+    buf_a, kraw_a = model_ops.qkv_rope(x, w, cos, sin, Hq, Hkv, D, nw, 1e-5, ring=(a, layer, a.seqlens))
+    buf_b, kraw_b = model_ops.qkv_rope(x, w, cos, sin, Hq, Hkv, D, nw, 1e-5)
+    ops.decode_append(b, layer, buf_b[0, 0, Hq:Hq + Hkv], buf_b[0, 0, Hq + Hkv:], g_mask=None,
+                      pre_key=kraw_b[0, 0], migrate=False, write=True, cache_seqlens=b.seqlens, advance=False)
+    torch.cuda.synchronize()
+    assert torch.equal(buf_a, buf_b) and torch.equal(kraw_a, kraw_b)
+    for name in ("block_pool_k", "block_pool_v", "local_pre_key", "seqlens", "ring_state", "status",
+                 "local_is_global", "global_lengths", "block_table"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    slot = 37 if ring_full else 21
+    assert a.ring_state.tolist() == ([37, W, slot] if ring_full else [0, 21, slot])
+    cur = W if ring_full else 22
+    assert a.seqlens.tolist() == (cur + a.global_lengths[layer * Hkv:(layer + 1) * Hkv]).tolist()
+    rows = (layer * Hkv + torch.arange(Hkv, device=DEV)) * W + slot
+    assert torch.equal(a.block_pool_k[rows], buf_a[0, 0, Hq:Hq + Hkv])
+    assert torch.equal(a.local_pre_key[layer, :, slot], kraw_a[0, 0])
+
+
 @pytest.mark.parametrize("S,D", [(1, 128), (300, 128), (77, 64)])
 def test_rope_with_qwen3_head_norms_matches_torch(S, D):
     """Qwen3's per-head q_norm / k_norm fused into the RoPE launch against

@@ -290,6 +290,19 @@ struct GemvArgs {
   const uint16_t* sin;
   uint16_t* kraw;
   int hq, hkv, hd;
+  // mode 3, optional: the decode step's ring write of the new token (the
+  // deferred-gating append of the dual cache), ring != nullptr.  ring[0..1]
+  // = (local_ptr, local_length) of the window of W slots; ring_k / ring_v /
+  // ring_pk are the layer's (Hkv, W, D) ring rows in the K pool, the V pool
+  // and the pre-RoPE key store; glen / seqlens the layer's Hkv global lengths
+  // and attention lengths.
+  int32_t* ring;
+  uint16_t* ring_k;
+  uint16_t* ring_v;
+  uint16_t* ring_pk;
+  const int32_t* glen;
+  int32_t* seqlens;
+  int W;
 };
 
 typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2v_t;
@@ -316,6 +329,14 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   } else {
     r0 = 2 * p;
     r1 = min(2 * p + 1, a.N - 1);
+  }
+  // the ring slot this step writes (decode_append_kernel's rule), requested
+  // with the other inputs so the epilogue does not wait for it
+  int slot = 0, cur = 0;
+  if (a.ring) {
+    const int lp = a.ring[0], ll = a.ring[1];
+    slot = ll < a.W ? ll : lp;
+    cur = ll < a.W ? ll + 1 : a.W;
   }
   const u32x4_t* w0 = (const u32x4_t*)(a.w + (int64_t)r0 * a.w_rs);
   const u32x4_t* w1 = (const u32x4_t*)(a.w + (int64_t)r1 * a.w_rs);
@@ -381,6 +402,12 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   }
   acc0 = wave_sum(acc0);
   acc1 = wave_sum(acc1);
+  if (a.ring && pair == a.hq * half) {
+    // the wave of the first k pair: attention lengths (current window + the
+    // global length) and the slot written, for the step's later decisions
+    if (lane < a.hkv) a.seqlens[lane] = cur + a.glen[lane];
+    if (lane == 0) a.ring[2] = slot;
+  }
   if (lane != 0 || pair >= npairs) return;
   if (a.mode == 2) {
     const float g = rb(acc0), u = rb(acc1);
@@ -393,15 +420,31 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     if (head < a.hq + a.hkv) {
       const float c0 = bf16lo(a.cos[d]), s0 = bf16lo(a.sin[d]);
       const float c1 = bf16lo(a.cos[d + half]), s1 = bf16lo(a.sin[d + half]);
-      a.y[r0] = f32_to_bf16(rb(v0 * c0) + rb(-v1 * s0));
-      a.y[r1] = f32_to_bf16(rb(v1 * c1) + rb(v0 * s1));
+      const uint16_t y0 = f32_to_bf16(rb(v0 * c0) + rb(-v1 * s0));
+      const uint16_t y1 = f32_to_bf16(rb(v1 * c1) + rb(v0 * s1));
+      a.y[r0] = y0;
+      a.y[r1] = y1;
       if (head >= a.hq) {
-        a.kraw[r0 - a.hq * a.hd] = f32_to_bf16(v0);
-        a.kraw[r1 - a.hq * a.hd] = f32_to_bf16(v1);
+        const uint16_t k0 = f32_to_bf16(v0), k1 = f32_to_bf16(v1);
+        a.kraw[r0 - a.hq * a.hd] = k0;
+        a.kraw[r1 - a.hq * a.hd] = k1;
+        if (a.ring) {
+          const int64_t row = ((int64_t)(head - a.hq) * a.W + slot) * a.hd;
+          a.ring_k[row + d] = y0;
+          a.ring_k[row + d + half] = y1;
+          a.ring_pk[row + d] = k0;
+          a.ring_pk[row + d + half] = k1;
+        }
       }
     } else {
-      a.y[r0] = f32_to_bf16(v0);
-      a.y[r1] = f32_to_bf16(v1);
+      const uint16_t y0 = f32_to_bf16(v0), y1 = f32_to_bf16(v1);
+      a.y[r0] = y0;
+      a.y[r1] = y1;
+      if (a.ring) {
+        const int64_t row = ((int64_t)(head - a.hq - a.hkv) * a.W + slot) * a.hd;
+        a.ring_v[row + d] = y0;
+        a.ring_v[row + d + half] = y1;
+      }
     }
     return;
   }
@@ -525,11 +568,14 @@ extern "C" int wgkv_silu_mul(const void* gate, int64_t gate_row_stride, const vo
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
-                            int32_t mode, const void* residual,
-                            const void* norm_weight, const void* norm_residual, void* norm_residual_out, float eps,
-                            const void* cos, const void* sin, void* k_raw,
-                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream) {
+namespace {
+
+// wgkv_gemv_ex with the ring fields of GemvArgs (all null / 0 without the ring write)
+int gemv_ex_launch(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+                   int32_t mode, const void* residual,
+                   const void* norm_weight, const void* norm_residual, void* norm_residual_out, float eps,
+                   const void* cos, const void* sin, void* k_raw,
+                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, const GemvArgs& ring, void* stream) {
   if (!w || !x || !y || n <= 0 || k <= 0 || mode < 0 || mode > 3) return WGKV_ERR_ARG;
   if (mode == 1 && !residual) return WGKV_ERR_ARG;
   if ((norm_residual == nullptr) != (norm_residual_out == nullptr) || (norm_residual && !norm_weight))
@@ -562,6 +608,13 @@ extern "C" int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int3
   a.hq = num_q_heads;
   a.hkv = num_kv_heads;
   a.hd = mode == 3 ? head_dim : 2;
+  a.ring = ring.ring;
+  a.ring_k = ring.ring_k;
+  a.ring_v = ring.ring_v;
+  a.ring_pk = ring.ring_pk;
+  a.glen = ring.glen;
+  a.seqlens = ring.seqlens;
+  a.W = ring.W;
   const int npairs = mode == 2 ? n : mode == 3 ? n / 2 : (n + 1) / 2;
   const int blocks = (npairs + kGemvWaves - 1) / kGemvWaves;
   if (norm_weight && k <= 4096)
@@ -569,6 +622,40 @@ extern "C" int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int3
   else
     hipLaunchKernelGGL(gemv_kernel<false>, dim3(blocks), dim3(64 * kGemvWaves), (size_t)k * 2, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int wgkv_gemv_ex(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,
+                            int32_t mode, const void* residual,
+                            const void* norm_weight, const void* norm_residual, void* norm_residual_out, float eps,
+                            const void* cos, const void* sin, void* k_raw,
+                            int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, void* stream) {
+  return gemv_ex_launch(w, w_row_stride, n, k, x, y, mode, residual, norm_weight, norm_residual, norm_residual_out,
+                        eps, cos, sin, k_raw, num_q_heads, num_kv_heads, head_dim, GemvArgs{}, stream);
+}
+
+extern "C" int wgkv_qkv_rope_ring_write(const void* w, int64_t w_row_stride, int32_t k, const void* x, void* y,
+                                        const void* norm_weight, float eps, const void* cos, const void* sin,
+                                        void* k_raw, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t layer, int32_t num_layers, int32_t local_window, int32_t* ring_state,
+                                        void* pool_k, void* pool_v, void* local_pre_key,
+                                        const int32_t* global_lengths, int32_t* cache_seqlens, void* stream) {
+  if (!ring_state || !pool_k || !pool_v || !local_pre_key || !global_lengths || !cache_seqlens) return WGKV_ERR_ARG;
+  if (layer < 0 || layer >= num_layers || local_window <= 0 || num_kv_heads <= 0) return WGKV_ERR_ARG;
+  if (num_kv_heads > 64) return WGKV_ERR_UNSUPPORTED;  // one wave writes the attention lengths
+  const int64_t base = (int64_t)layer * num_kv_heads * local_window * head_dim;
+  GemvArgs r = {};
+  r.ring = ring_state;
+  r.ring_k = (uint16_t*)pool_k + base;
+  r.ring_v = (uint16_t*)pool_v + base;
+  r.ring_pk = (uint16_t*)local_pre_key + base;
+  r.glen = global_lengths + (int64_t)layer * num_kv_heads;
+  r.seqlens = cache_seqlens;
+  r.W = local_window;
+  return gemv_ex_launch(w, w_row_stride, (num_q_heads + 2 * num_kv_heads) * head_dim, k, x, y, 3, nullptr,
+                        norm_weight, nullptr, nullptr, eps, cos, sin, k_raw, num_q_heads, num_kv_heads, head_dim, r,
+                        stream);
 }
 
 extern "C" int wgkv_gemv(const void* w, int64_t w_row_stride, int32_t n, int32_t k, const void* x, void* y,

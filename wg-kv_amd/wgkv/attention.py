@@ -94,6 +94,9 @@ class LlamaAttention(nn.Module):
         self.decode_kernel_handle = torch_ops.paged_decode_attn_handle  # torch.ops.wgkv.paged_decode_attn
         self.decode_kernel_executor = lambda func: func()
         self._qkv_weight = None
+        # a decode step's ring write done by the q/k/v projection's launch
+        # where layers.ring_write_in_projection allows it
+        self.ring_write_fused = True
 
     @torch.no_grad()
     def fuse_qkv(self):
@@ -123,8 +126,14 @@ class LlamaAttention(nn.Module):
         if (w is not None and w.device == hidden_states.device and not self.qk_norm and cos.dim() == 3
                 and model_ops.qkv_rope_usable(hidden_states, w, cos, sin, nw)):
             Hq, Hkv = self.config.num_attention_heads, self.config.num_key_value_heads
+            c = past_key_value
+            ring = None
+            if self.ring_write_fused and layers.ring_write_in_projection(self, c):
+                ring = (c, self.layer_idx, c.cache_seqlens[self.layer_idx][0])
             buf, kraw = model_ops.qkv_rope(hidden_states, w, cos, sin, Hq, Hkv, self.head_dim, nw,
-                                           input_norm.eps if input_norm is not None else 1e-5)
+                                           input_norm.eps if input_norm is not None else 1e-5, ring=ring)
+            if ring is not None or getattr(c, "ring_written_by", None) is not None:
+                c.ring_written_by = self.layer_idx if ring is not None else None
             q = buf[:, :, :Hq].transpose(1, 2)
             k = buf[:, :, Hq:Hq + Hkv].transpose(1, 2)
             v = buf[:, :, Hq + Hkv:].transpose(1, 2)

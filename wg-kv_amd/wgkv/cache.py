@@ -87,6 +87,9 @@ class DualCache:
         # deferred gating: when set, decode steps leave the window re-gate to
         # the caller (layers.refresh_windows after a step that wrote slot W-1)
         self.refresh_by_caller = False
+        # the layer whose decode-step ring write its q/k/v projection's launch
+        # has already done (decode_wrapper then skips the append), else None
+        self.ring_written_by = None
         self.next_free_block_dev = torch.full((1,), n_local, **i32)
         self.status = torch.zeros(1, **i32)
         # random_sparsity ablation: decode-step draws per layer so far (device

@@ -243,6 +243,21 @@ def prefill_wrapper(self, past_key_value, query_states, pre_key, key_states, val
         *meta, softmax_scale=self.scaling, causal=True, return_softmax_lse=False)
 
 
+def ring_write_in_projection(self, c):
+    """Whether this layer's decode-step ring write (decode_wrapper's append
+    without a mask) can run inside the q/k/v projection's launch
+    (model_ops.qkv_rope with ring): device ring pointers, deferred gating (a
+    decode token gets no mask and its pre-RoPE key is stored), no QUEST or
+    SnapKV bookkeeping, and a layer between the first (whose lazy promotion
+    must read the oldest slot before it is overwritten) and the last (whose
+    append advances the ring pointers)."""
+    cfg = self.config
+    return (c is not None and getattr(c, "device_ring", False) and getattr(c, "gated_kv_initialized", False)
+            and c.prefill_length > 0 and c.local_pre_key is not None and "pre_k" in cfg.g_inputs
+            and cfg.g_defer and not cfg.use_baseline and not cfg.use_quest and not cfg.snapkv_enabled
+            and 0 < self.layer_idx < cfg.num_hidden_layers - 1)
+
+
 def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, value_states,
                    device, g_mask, local_blocks_per_head):
     """src/modeling_layers.py:1379-1449.  Tensors are (1, H, 1, D)."""
@@ -252,10 +267,13 @@ def decode_wrapper(self, past_key_value, query_states, pre_key, key_states, valu
     insert_pos = c.local_length if c.local_length < W else c.local_ptr
     seqlens = c.cache_seqlens[self.layer_idx]
     last = self.layer_idx == self.config.num_hidden_layers - 1
-    ops.decode_append(c, self.layer_idx, key_states[0, :, 0], value_states[0, :, 0],
-                      g_mask=None if g_mask is None else g_mask[0, :, 0],
-                      pre_key=pre_key[0, :, 0] if g_mask is None else None,
-                      migrate=False, write=True, cache_seqlens=seqlens[0], advance=last)
+    if getattr(c, "ring_written_by", None) == self.layer_idx and g_mask is None:
+        c.ring_written_by = None  # the q/k/v projection's launch wrote the slot (ring_write_in_projection)
+    else:
+        ops.decode_append(c, self.layer_idx, key_states[0, :, 0], value_states[0, :, 0],
+                          g_mask=None if g_mask is None else g_mask[0, :, 0],
+                          pre_key=pre_key[0, :, 0] if g_mask is None else None,
+                          migrate=False, write=True, cache_seqlens=seqlens[0], advance=last)
     if g_mask is None:
         if c.refresh_by_caller:
             pass  # the caller re-gates the windows after the step (refresh_windows)
@@ -379,6 +397,6 @@ def self_attn_forward_patch(self, gating_mode, attention_mask, past_key_value, i
 
 __all__ = [
     "WGKVConfig", "DualCache", "get_random_g_scores", "decode_random_admission", "refresh_local_is_global",
-    "refresh_windows", "migrate_local_kv_to_global",
+    "refresh_windows", "migrate_local_kv_to_global", "ring_write_in_projection",
     "prefill_wrapper", "decode_wrapper", "self_attn_forward_patch_inference", "self_attn_forward_patch",
 ]

@@ -131,17 +131,34 @@ def swiglu_linear(x, gate_up_weight):
     return F.silu(g) * u
 
 
-def qkv_rope(x, w_qkv, cos, sin, num_q_heads, num_kv_heads, head_dim, norm_weight=None, eps=1e-5):
+def qkv_rope(x, w_qkv, cos, sin, num_q_heads, num_kv_heads, head_dim, norm_weight=None, eps=1e-5, ring=None):
     """One decode row's q/k/v projection with rotary embedding (wgkv_gemv_ex
     mode 3), optionally after the input RMSNorm: x (1, 1, hidden) bf16 (the
     residual stream when norm_weight is given), w_qkv the stacked (n, hidden)
     weight, cos / sin (1, 1, head_dim).  Returns (buf (1, 1, Hq + 2 Hkv, D)
     with rotated q, rotated k and v, the unrotated k (1, 1, Hkv, D)), the
-    values wgkv_rms_norm, the product and wgkv_rope_qkv give."""
+    values wgkv_rms_norm, the product and wgkv_rope_qkv give.
+
+    ring = (cache, layer, cache_seqlens): the same launch also does the
+    decode step's ring write of a DualCache with device ring pointers and
+    deferred gating (wgkv_qkv_rope_ring_write): rotated k, v and the
+    unrotated k into the ring slot, cache_seqlens (the layer's (Hkv,) int32)
+    and the written slot, as wgkv_decode_append_ring without a mask, a
+    migration or an advance would."""
     n = (num_q_heads + 2 * num_kv_heads) * head_dim
     buf = torch.empty(1, 1, num_q_heads + 2 * num_kv_heads, head_dim, dtype=x.dtype, device=x.device)
     kraw = torch.empty(1, 1, num_kv_heads, head_dim, dtype=x.dtype, device=x.device)
     c, s_ = cos.reshape(-1), sin.reshape(-1)
+    if ring is not None:
+        cache, layer, seqlens = ring
+        st = _lib.lib().wgkv_qkv_rope_ring_write(
+            _ptr(w_qkv), w_qkv.stride(0), w_qkv.shape[-1], _ptr(x), _ptr(buf), _ptr(norm_weight), float(eps),
+            _ptr(c), _ptr(s_), _ptr(kraw), num_q_heads, num_kv_heads, head_dim,
+            layer, cache.num_layers, cache.local_window_size, _ptr(cache.ring_state),
+            _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.local_pre_key),
+            _ptr(cache.global_lengths), _ptr(seqlens), _lib.stream_handle(x.device))
+        _lib.check(st, "wgkv_qkv_rope_ring_write")
+        return buf, kraw
     st = _lib.lib().wgkv_gemv_ex(_ptr(w_qkv), w_qkv.stride(0), n, w_qkv.shape[-1], _ptr(x), _ptr(buf), 3, None,
                                  _ptr(norm_weight), None, None, float(eps), _ptr(c), _ptr(s_), _ptr(kraw),
                                  num_q_heads, num_kv_heads, head_dim, _lib.stream_handle(x.device))
