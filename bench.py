@@ -30,7 +30,9 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=50)
-    p.add_argument("--warmup", type=int, default=10)
+    # untimed steps first: the GPU's clocks settle over ~0.1 s of sustained
+    # work (config 3 at 10 warm-up steps 0.2210-0.2220 ms, at 400 0.2164-0.2173)
+    p.add_argument("--warmup", type=int, default=400)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="wall-time budget of the CPU-oracle baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
@@ -101,6 +103,58 @@ def time_op(fn, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+class DeviceEvent:
+    """A HIP timing event recorded with a device-scope release
+    (hipEventCreateWithFlags(hipEventReleaseToDevice), the flag HIP documents
+    for timing the commands between events).  torch's events take the
+    default system-scope release, which writes back the L2 when recorded and
+    leaves the GPU idle for ~5.5 us between the two kernels an event
+    separates -- a cost the pipeline itself never pays.  Recorded on torch's
+    current stream, the stream the kernels are launched on."""
+    FLAGS = 0x40000000  # hipEventReleaseToDevice
+    _hip = None
+    KIND = "hipEventReleaseToDevice"
+
+    @classmethod
+    def runtime(cls):
+        if cls._hip is None:
+            import ctypes
+            import torch  # noqa: F401  (the HIP runtime torch loaded; same SONAME, so dlopen returns it)
+            h = ctypes.CDLL("libamdhip64.so.7")
+            h.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+            h.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+            h.hipEventDestroy.argtypes = [ctypes.c_void_p]
+            cls._hip = h
+        return cls._hip
+
+    def __init__(self):
+        import ctypes
+        self.ev = ctypes.c_void_p()
+        st = self.runtime().hipEventCreateWithFlags(ctypes.byref(self.ev), self.FLAGS)
+        if st != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags(hipEventReleaseToDevice) failed: {st}")
+
+    def record(self):
+        import torch
+        st = self.runtime().hipEventRecord(self.ev, torch.cuda.current_stream().cuda_stream)
+        if st != 0:
+            raise RuntimeError(f"hipEventRecord failed: {st}")
+
+    def elapsed_time(self, end):
+        import ctypes
+        ms = ctypes.c_float()
+        st = self.runtime().hipEventElapsedTime(ctypes.byref(ms), self.ev, end.ev)
+        if st != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {st}")
+        return ms.value
+
+    def __del__(self):
+        if self.ev:
+            self.runtime().hipEventDestroy(self.ev)
+            self.ev = None
+
+
 def time_graph(fn, calls=20, replays=10):
     """Average time of fn() per call with the host out of the way: `calls`
     calls captured in one HIP graph, replayed `replays` times between HIP
@@ -115,6 +169,11 @@ def time_graph(fn, calls=20, replays=10):
             fn()
     g.replay()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.15:  # untimed: the GPU's clocks settle under sustained work
+        for _ in range(10):
+            g.replay()
+        torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -177,8 +236,10 @@ def prefill_section(dev, steps, warmup):
     Llama-3.1-8B-shaped layer.  Per chunk: the write gate (fp32 scores and the
     admission mask), admission into the dual cache (compaction, page scatter,
     column counts), the chunk's sparse attention over admitted columns plus
-    the local band, and the ring rewrite.  Each phase is bracketed by HIP
-    events on the launch stream; ms/chunk is the whole prompt's time / 8.
+    the local band, and the ring rewrite.  ms/chunk is the whole prompt's
+    time / 8 between two HIP events; the phases come from timed runs with a
+    HIP event between every two phases (device-scope release events,
+    DeviceEvent), alternating with the first kind; medians over the runs.
     MFMA utilisation: attention FLOPs = sum over query heads and rows of
     4*D*|visible keys| (the ideal mask), gate FLOPs = 2*(2D*inner + inner)
     per token and head, against the dense bf16 / fp32 peaks."""
@@ -203,24 +264,30 @@ def prefill_section(dev, steps, warmup):
             cache.local_is_global.clone())
     chunks = [(c0, min(CH, S - c0)) for c0 in range(0, S, CH)]
     phases = ("gate", "admit", "sparse_attn", "ring")
-    acc = {p: 0.0 for p in phases}
-    total = [0.0]
+    # per timed run: the prompt between two events, the phase-timed prompt
+    # (first to last event) and its phases, the host's enqueue time
+    runs = {"total": [], "marked": [], "phases": [], "host": []}
     gate_mod = [w.gate]
 
+    pool = [DeviceEvent() for _ in range(1 + len(phases) * len(chunks))]  # created once, re-recorded
+
     def run(timed):
+        """timed: None (warm-up), "total" (events around the prompt) or
+        "phases" (an event between every two phases)."""
         cache.block_table.copy_(snap[0])
         cache.global_lengths.copy_(snap[1])
         cache.next_free_block_dev.copy_(snap[2])
         cache.local_is_global.copy_(snap[3])
         ev = []
 
-        def mark():
-            if timed:
-                e = torch.cuda.Event(enable_timing=True)
+        def mark(force=False):
+            if timed == "phases" or (timed == "total" and force):
+                e = pool[len(ev)]
                 e.record()
                 ev.append(e)
 
-        mark()
+        mark(True)
+        h0 = time.perf_counter()
         for c0, C in chunks:
             sl = slice(c0, c0 + C)
             gate_mod[0].scores_and_mask(pk[:, :, sl], kk[:, :, sl], None, w.threshold,
@@ -234,22 +301,36 @@ def prefill_section(dev, steps, warmup):
             mark()
             st.ring()
             mark()
+        if timed == "total":
+            mark(True)
+            runs["host"].append((time.perf_counter() - h0) * 1000)
         if timed:
             torch.cuda.synchronize()
-            for n in range(len(chunks)):
-                for k, p in enumerate(phases):
-                    acc[p] += ev[4 * n + k].elapsed_time(ev[4 * n + k + 1])
-            total[0] += ev[0].elapsed_time(ev[-1])
+        if timed == "phases":
+            runs["phases"].append({p: sum(ev[4 * n + k].elapsed_time(ev[4 * n + k + 1]) for n in range(len(chunks)))
+                                   for k, p in enumerate(phases)})
+            runs["marked"].append(ev[0].elapsed_time(ev[-1]))
+        elif timed == "total":
+            runs["total"].append(ev[0].elapsed_time(ev[-1]))
 
-    for _ in range(warmup):
-        run(False)
-    torch.cuda.synchronize()
-    for _ in range(steps):
-        run(True)
+    def timed_runs():
+        """Medians over the timed runs (the two kinds alternate, so both see
+        the same warm GPU)."""
+        for v in runs.values():
+            v.clear()
+        for _ in range(warmup):
+            run(None)
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            run("total")
+            run("phases")
+        med = lambda xs: sorted(xs)[len(xs) // 2]
+        return (med(runs["total"]), med(runs["marked"]), {p: med([r[p] for r in runs["phases"]]) for p in phases},
+                med(runs["host"]))
+
+    t_total, t_marked, ms, t_host = timed_runs()
     if int(cache.status.item()) != 0:
         raise RuntimeError("config-4 prefill ran out of cache capacity")
-    ms = {p: acc[p] / steps for p in phases}
-    t_total = total[0] / steps
     pairs = workloads.visible_pairs(mask[0], W)
     attn_flop = float((pairs * (Hq // Hkv)).sum().item()) * 4 * D
     inner = 4 * D
@@ -275,21 +356,15 @@ def prefill_section(dev, steps, warmup):
     # work); run after the bf16 pipeline's figures and masks are taken
     bf16_mask = mask.clone()
     gate_mod[0] = g32
-    acc.update({p: 0.0 for p in phases})
-    total[0] = 0.0
-    for _ in range(warmup):
-        run(False)
-    torch.cuda.synchronize()
-    for _ in range(steps):
-        run(True)
+    t_total32, t_marked32, ms32, _ = timed_runs()
     if int(cache.status.item()) != 0:
         raise RuntimeError("config-4 prefill (fp32 scores) ran out of cache capacity")
-    ms32 = {p: acc[p] / steps for p in phases}
     pairs32 = workloads.visible_pairs(mask[0], W)
     attn_flop32 = float((pairs32 * (Hq // Hkv)).sum().item()) * 4 * D
     as_stated = {"gate_parameters": "float32", "scores": "float32",
                  "admitted_frac": round(mask.float().mean().item(), 4),
-                 "ms_per_chunk": round(total[0] / steps / len(chunks), 4),
+                 "ms_per_chunk": round(t_total32 / len(chunks), 4),
+                 "ms_per_chunk_phase_timed": round(t_marked32 / len(chunks), 4),
                  "ms_per_chunk_by_phase": {p: round(ms32[p] / len(chunks), 4) for p in phases},
                  "sparse_attn_tflop": round(attn_flop32 / 1e12, 4),
                  "sparse_attn_mfma_frac_bf16": round(attn_flop32 / ms32["sparse_attn"] / 1e9 / BF16_PEAK_TFLOPS, 4)}
@@ -304,6 +379,9 @@ def prefill_section(dev, steps, warmup):
         "ms_per_chunk": round(t_total / len(chunks), 4),
         "ms_prompt": round(t_total, 4),
         "ms_per_chunk_by_phase": {p: round(ms[p] / len(chunks), 4) for p in phases},
+        "ms_per_chunk_phase_timed": round(t_marked / len(chunks), 4),
+        "host_enqueue_ms_per_chunk": round(t_host / len(chunks), 4),
+        "phase_events": DeviceEvent.KIND + " (device-scope release), one between every two phases",
         "gate_parameters": "bfloat16 (the reference's inference loads the gate in bf16)",
         "config4_as_stated": as_stated,
         "sparse_attn": {"tflop": round(attn_flop / 1e12, 4), "tflops": round(attn_flop / ms["sparse_attn"] / 1e9, 1),
@@ -781,7 +859,7 @@ def main():
     del w, out
     torch.cuda.empty_cache()
     if not args.no_prefill:
-        result["prefill"] = prefill_section(dev, max(5, args.steps // 5), max(2, args.warmup // 5))
+        result["prefill"] = prefill_section(dev, max(10, args.steps // 2), max(4, args.warmup // 2))
         torch.cuda.empty_cache()
     if not args.no_secondary:
         result["quest"] = quest_section(dev, args.steps, args.warmup)
