@@ -104,16 +104,19 @@ def time_op(fn, steps, warmup):
 
 
 class DeviceEvent:
-    """A HIP timing event recorded with a device-scope release
-    (hipEventCreateWithFlags(hipEventReleaseToDevice), the flag HIP documents
-    for timing the commands between events).  torch's events take the
-    default system-scope release, which writes back the L2 when recorded and
-    leaves the GPU idle for ~5.5 us between the two kernels an event
-    separates -- a cost the pipeline itself never pays.  Recorded on torch's
-    current stream, the stream the kernels are launched on."""
-    FLAGS = 0x40000000  # hipEventReleaseToDevice
+    """A HIP timing event without the system-scope fence
+    (hipEventCreateWithFlags(hipEventDisableSystemFence), which HIP documents
+    for events used only to measure time).  torch's events take the default
+    system-scope release, which writes back the L2 when recorded and leaves
+    the GPU idle for ~5.5 us between the two kernels an event separates -- a
+    cost the pipeline itself never pays (hipEventReleaseToDevice still
+    leaves ~5 us).  The AQL barrier bit still orders the event after the
+    kernels before it; its times are read after torch.cuda.synchronize(),
+    which waits for the device.  Recorded on torch's current stream, the
+    stream the kernels are launched on."""
+    FLAGS = 0x20000000  # hipEventDisableSystemFence
     _hip = None
-    KIND = "hipEventReleaseToDevice"
+    KIND = "hipEventDisableSystemFence"
 
     @classmethod
     def runtime(cls):
@@ -133,7 +136,7 @@ class DeviceEvent:
         self.ev = ctypes.c_void_p()
         st = self.runtime().hipEventCreateWithFlags(ctypes.byref(self.ev), self.FLAGS)
         if st != 0:
-            raise RuntimeError(f"hipEventCreateWithFlags(hipEventReleaseToDevice) failed: {st}")
+            raise RuntimeError(f"hipEventCreateWithFlags({self.KIND}) failed: {st}")
 
     def record(self):
         import torch
@@ -238,8 +241,9 @@ def prefill_section(dev, steps, warmup):
     column counts), the chunk's sparse attention over admitted columns plus
     the local band, and the ring rewrite.  ms/chunk is the whole prompt's
     time / 8 between two HIP events; the phases come from timed runs with a
-    HIP event between every two phases (device-scope release events,
-    DeviceEvent), alternating with the first kind; medians over the runs.
+    HIP event between every two phases (timing-only events without the
+    system-scope fence, DeviceEvent), alternating with the first kind;
+    medians over the runs.
     MFMA utilisation: attention FLOPs = sum over query heads and rows of
     4*D*|visible keys| (the ideal mask), gate FLOPs = 2*(2D*inner + inner)
     per token and head, against the dense bf16 / fp32 peaks."""
@@ -381,7 +385,7 @@ def prefill_section(dev, steps, warmup):
         "ms_per_chunk_by_phase": {p: round(ms[p] / len(chunks), 4) for p in phases},
         "ms_per_chunk_phase_timed": round(t_marked / len(chunks), 4),
         "host_enqueue_ms_per_chunk": round(t_host / len(chunks), 4),
-        "phase_events": DeviceEvent.KIND + " (device-scope release), one between every two phases",
+        "phase_events": DeviceEvent.KIND + " (timing-only events), one between every two phases",
         "gate_parameters": "bfloat16 (the reference's inference loads the gate in bf16)",
         "config4_as_stated": as_stated,
         "sparse_attn": {"tflop": round(attn_flop / 1e12, 4), "tflops": round(attn_flop / ms["sparse_attn"] / 1e9, 1),
