@@ -122,13 +122,16 @@ def test_gemv_epilogues_equal_the_torch_compositions(n, k):
 
 @pytest.mark.parametrize("with_res", [False, True])
 @pytest.mark.parametrize("mode", [0, 2])
-def test_gemv_norm_prologue_equals_rms_norm_then_gemv(with_res, mode):
+@pytest.mark.parametrize("H", [4096, 512, 256])
+def test_gemv_norm_prologue_equals_rms_norm_then_gemv(with_res, mode, H):
     """The workgroups' own RMSNorm of x (+ residual) gives wgkv_rms_norm's
-    bits, so the fused launch equals rms_norm followed by the product."""
+    bits, so the fused launch equals rms_norm followed by the product (the
+    decode step's post-attention norm before the SwiGLU product, and the
+    input norm before a q/k/v product without the RoPE epilogue)."""
     from wgkv import model_ops
-    print(f"[model_ops] gemv norm prologue res={with_res} mode={mode}", flush=True)
-    g = torch.Generator().manual_seed(5 + mode + int(with_res))
-    H, N = 4096, 1024
+    print(f"[model_ops] gemv norm prologue H={H} res={with_res} mode={mode}", flush=True)
+    g = torch.Generator().manual_seed(5 + mode + int(with_res) + H)
+    N = 1024
     x = torch.randn(1, 1, H, generator=g).to(torch.bfloat16).to(DEV)
     r = torch.randn(1, 1, H, generator=g).to(torch.bfloat16).to(DEV) if with_res else None
     nw = (1 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).to(DEV)

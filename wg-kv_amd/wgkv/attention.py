@@ -142,11 +142,18 @@ class LlamaAttention(nn.Module):
                 self, gating_mode, attention_mask, past_key_value, input_shape, q, pre_key, k, v)
             out = out.reshape(*input_shape, -1).to(hidden_states.dtype).contiguous()
             return self.o_proj(out), attn_weights, g_scores
-        if input_norm is not None:
+        qkv = None
+        if (input_norm is not None and w is not None and w.device == hidden_states.device
+                and model_ops.rms_norm_linear_usable(hidden_states, input_norm.weight, w)):
+            # a decode row without the fused RoPE (Qwen3's q/k norms sit between
+            # the product and RoPE): the input norm as the product's prologue
+            qkv, _ = model_ops.rms_norm_linear(hidden_states, input_norm.weight, input_norm.eps, w)
+        elif input_norm is not None:
             hidden_states = input_norm(hidden_states)
         if self._qkv_weight is not None and self._qkv_weight.device == hidden_states.device:
             nq, nk = self.q_proj.weight.shape[0], self.k_proj.weight.shape[0]
-            qkv = model_ops.linear(hidden_states, self._qkv_weight)
+            if qkv is None:
+                qkv = model_ops.linear(hidden_states, self._qkv_weight)
             q = qkv[..., :nq].view(hidden_shape)
             k = qkv[..., nq:nq + nk].view(hidden_shape)
             v_src = qkv[..., nq + nk:]
