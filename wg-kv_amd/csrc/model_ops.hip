@@ -334,8 +334,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
   // with the other inputs so the epilogue does not wait for it
   int slot = 0, cur = 0;
   if (a.ring) {
-    const int lp = a.ring[0], ll = a.ring[1];
-    slot = ll < a.W ? ll : lp;
+    const int lp = a.ring[0], ll = max(a.ring[1], 0);
+    slot = min(max(ll < a.W ? ll : lp, 0), a.W - 1);  // pointers out of range stay inside the ring
     cur = ll < a.W ? ll + 1 : a.W;
   }
   const u32x4_t* w0 = (const u32x4_t*)(a.w + (int64_t)r0 * a.w_rs);
