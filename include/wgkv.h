@@ -588,6 +588,27 @@ int wgkv_qkv_rope_ring_write(const void* w, int64_t w_row_stride, int32_t k, con
                              void* pool_k, void* pool_v, void* local_pre_key,
                              const int32_t* global_lengths, int32_t* cache_seqlens, void* stream);
 
+/* wgkv_rope_qkv_norm_ring_write -- wgkv_rope_qkv_norm for one decode row
+ * (batch = seq_len = 1; element strides between heads only; v and v_out
+ * required) whose threads also do the ring write of wgkv_qkv_rope_ring_write
+ * (same ring arguments and layout): the rotated k, v and the pre-RoPE k --
+ * after Qwen3's k head norm when k_norm_weight is given -- into ring row
+ * (layer, h, slot), the layer's attention lengths and ring_state[2] = slot;
+ * pool_k, pool_v and local_pre_key 16-byte aligned.  For decode steps whose
+ * q/k head norms keep RoPE out of the q/k/v product's epilogue
+ * (modeling_qwen3.py:235-239).  No counterpart in the reference, which
+ * writes the ring after its projections (modeling_layers.py:1390-1407). */
+int wgkv_rope_qkv_norm_ring_write(const void* q, int64_t q_sh, const void* k, int64_t k_sh,
+                                  const void* v, int64_t v_sh, const void* cos, const void* sin,
+                                  void* q_out, int64_t qo_sh, void* k_out, int64_t ko_sh,
+                                  void* v_out, int64_t vo_sh,
+                                  int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                  const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                  void* k_pre, int64_t kp_sh,
+                                  int32_t layer, int32_t num_layers, int32_t local_window,
+                                  int32_t* ring_state, void* pool_k, void* pool_v, void* local_pre_key,
+                                  const int32_t* global_lengths, int32_t* cache_seqlens, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -147,9 +147,9 @@ def test_graph_decode_matches_eager(gated, qwen3):
     assert ca.local_ptr == cb.local_ptr and ca.local_length == cb.local_length
 
 
-@pytest.mark.parametrize("defer,random_sparsity", [(True, None), (False, None), (True, 0.0), (True, 0.5),
-                                                   (False, 0.5)])
-def test_graph_decode_deferred_gating(defer, random_sparsity):
+@pytest.mark.parametrize("defer,random_sparsity,qwen3", [(True, None, False), (False, None, False), (True, 0.0, False),
+                                                         (True, 0.5, False), (False, 0.5, False), (True, None, True)])
+def test_graph_decode_deferred_gating(defer, random_sparsity, qwen3):
     """Deferred gating (the reference profiling harness's mode): 150 captured
     decode steps with a 64-token window re-gate each layer's window twice (on
     the steps that write slot 63, decided on the device) and equal the eager
@@ -161,12 +161,16 @@ def test_graph_decode_deferred_gating(defer, random_sparsity):
     draws, which the graph replays continue exactly as the eager steps.
     Four layers: with deferred gating the captured steps of the two middle
     layers write the ring from the q/k/v projection's launch
-    (ring_write_in_projection), the eager steps by the append."""
+    (ring_write_in_projection), the eager steps by the append; with qwen3
+    (per-head q/k norms, g_expand 1.5) from the launch of the norms and the
+    rotation."""
     from wgkv import e2e, layers
     from wgkv.cache import DualCache
-    print(f"[e2e] graph decode, g_defer={defer}, random_sparsity={random_sparsity}, 150 steps, W=64", flush=True)
+    print(f"[e2e] graph decode, g_defer={defer}, random_sparsity={random_sparsity}, qwen3={qwen3}, 150 steps, W=64",
+          flush=True)
     W, S, chunk, n = 64, 640, 256, 150
-    m = tiny_model(True, S=S, steps=n, W=W, layers=4, g_defer=defer)
+    m = tiny_model(True, S=S, steps=n, W=W, layers=4, g_defer=defer,
+                   **({"qk_norm": True, "g_expand": 1.5} if qwen3 else {}))
     ids = torch.randint(0, 1000, (1, S), generator=torch.Generator().manual_seed(5)).to(DEV)
     if random_sparsity is None:
         e2e.calibrate_gates(m, ids, 0.3, chunk=256)

@@ -233,6 +233,62 @@ def test_qkv_ring_write_equals_projection_then_append(ring_full, Hq, Hkv, D, lay
     assert torch.equal(a.local_pre_key[layer, :, slot], kraw_a[0, 0])
 
 
+@pytest.mark.parametrize("ring_full", [False, True])
+@pytest.mark.parametrize("norm", [True, False])
+def test_rope_ring_write_equals_rope_then_append(ring_full, norm):
+    """wgkv_rope_qkv_norm_ring_write gives wgkv_rope_qkv_norm's outputs for
+    one decode row and writes the ring row, pre-RoPE key (normalised with
+    the k head norm), attention lengths and slot that
+    wgkv_decode_append_ring without a mask, promotion or advance writes from
+    them, bit for bit, every other byte of the pools left as it was."""
+    from types import SimpleNamespace
+    from wgkv import model_ops, ops
+    from wgkv.attention import LlamaRotaryEmbedding
+    print(f"[model_ops] rope ring write norm={norm} full={ring_full}", flush=True)
+    g = torch.Generator().manual_seed(41 + int(norm) + 2 * int(ring_full))
+    Hq, Hkv, D, layer, L, W, page = 32, 8, 128, 2, 4, 64, 16
+    qkv = torch.randn(1, 1, (Hq + 2 * Hkv) * D, generator=g).to(torch.bfloat16).to(DEV)
+    q = qkv[..., :Hq * D].view(1, 1, Hq, D).transpose(1, 2)
+    k = qkv[..., Hq * D:(Hq + Hkv) * D].view(1, 1, Hkv, D).transpose(1, 2)
+    v = qkv[..., (Hq + Hkv) * D:].view(1, 1, Hkv, D).transpose(1, 2)
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV) if norm else None
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).to(torch.bfloat16).to(DEV) if norm else None
+    rot = LlamaRotaryEmbedding(D, 1e6, device=DEV)
+    cos, sin = rot(qkv, torch.tensor([[98765]], device=DEV))
+    total_pages = L * Hkv * W // page + 16
+    i32 = dict(dtype=torch.int32, device=DEV)
+
+    def cache():
+        g2 = torch.Generator().manual_seed(9)
+        return SimpleNamespace(
+            num_layers=L, num_kv_heads=Hkv, head_dim=D, local_window_size=W, block_size=page,
+            max_tokens_per_head=10 ** 6, total_blocks=total_pages, device_ring=True,
+            block_pool_k=torch.randn(total_pages * page, D, generator=g2).to(torch.bfloat16).to(DEV),
+            block_pool_v=torch.randn(total_pages * page, D, generator=g2).to(torch.bfloat16).to(DEV),
+            local_pre_key=torch.randn(L, Hkv, W, D, generator=g2).to(torch.bfloat16).to(DEV),
+            global_lengths=torch.randint(0, 5000, (L * Hkv,), generator=g2).to(**i32),
+            block_table=torch.zeros(L, Hkv, 4, **i32),
+            local_is_global=torch.zeros(L, Hkv, W, dtype=torch.bool, device=DEV),
+            next_free_block_dev=torch.zeros(1, **i32), status=torch.zeros(1, **i32),
+            ring_state=torch.tensor([13, W, -1] if ring_full else [0, 40, -1], **i32),
+            seqlens=torch.full((Hkv,), -5, **i32))
+
+    a, b = cache(), cache()
+    ra = model_ops.rope_qkv(q, k, v, cos, sin, qn, kn, 1e-6, ring=(a, layer, a.seqlens))
+    rb_ = model_ops.rope_qkv(q, k, v, cos, sin, qn, kn, 1e-6)
+    pre = rb_[3] if norm else k
+    ops.decode_append(b, layer, rb_[1][0, :, 0], rb_[2][0, :, 0], g_mask=None, pre_key=pre[0, :, 0],
+                      migrate=False, write=True, cache_seqlens=b.seqlens, advance=False)
+    torch.cuda.synchronize()
+    for x, y in zip(ra, rb_):
+        assert torch.equal(x, y)
+    for name in ("block_pool_k", "block_pool_v", "local_pre_key", "seqlens", "ring_state", "status",
+                 "local_is_global", "global_lengths", "block_table"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    slot = 13 if ring_full else 40
+    assert a.ring_state.tolist()[2] == slot
+
+
 @pytest.mark.parametrize("S,D", [(1, 128), (300, 128), (77, 64)])
 def test_rope_with_qwen3_head_norms_matches_torch(S, D):
     """Qwen3's per-head q_norm / k_norm fused into the RoPE launch against

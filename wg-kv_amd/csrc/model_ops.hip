@@ -157,6 +157,19 @@ struct RopeArgs {
   float eps;
   uint16_t* kpre;
   int64_t kp[3];
+  // optional, one decode row (B = S = 1): the step's ring write of the dual
+  // cache under deferred gating, as GemvArgs' ring fields: ring[0..1] =
+  // (local_ptr, local_length), ring[2] <- the slot; ring_k / ring_v /
+  // ring_pk the layer's (Hkv, W, D) ring rows of the K pool, the V pool and
+  // the pre-RoPE key store; glen / seqlens the layer's global and attention
+  // lengths
+  int32_t* ring;
+  uint16_t* ring_k;
+  uint16_t* ring_v;
+  uint16_t* ring_pk;
+  const int32_t* glen;
+  int32_t* seqlens;
+  int W;
 };
 
 __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
@@ -164,6 +177,16 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   const int Ht = a.H[0] + a.H[1] + a.H[2];
   const int64_t total = (int64_t)a.B * a.S * Ht * hch;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  int slot = 0;
+  if (a.ring) {
+    const int lp = a.ring[0], ll = max(a.ring[1], 0);
+    slot = min(max(ll < a.W ? ll : lp, 0), a.W - 1);  // pointers out of range stay inside the ring
+    if (idx == 0) {
+      const int cur = ll < a.W ? ll + 1 : a.W;
+      for (int h = 0; h < a.H[1]; ++h) a.seqlens[h] = cur + a.glen[h];
+      a.ring[2] = slot;
+    }
+  }
   if (idx >= total) return;
   const int c = (int)(idx % hch);
   int64_t r = idx / hch;
@@ -183,9 +206,15 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   uint16_t* dst = a.out[ten] + b * a.os[ten][0] + s * a.os[ten][1] + hh * a.os[ten][2];
   const int d0 = c * 8;
   const u32x4_t w1 = *(const u32x4_t*)(src + d0), w2 = *(const u32x4_t*)(src + half + d0);
+  // this head's row of the ring (decode row: b = s = 0)
+  const int64_t rrow = ((int64_t)hh * a.W + slot) * a.D;
   if (ten == 2) {
     *(u32x4_t*)(dst + d0) = w1;
     *(u32x4_t*)(dst + half + d0) = w2;
+    if (a.ring) {
+      *(u32x4_t*)(a.ring_v + rrow + d0) = w1;
+      *(u32x4_t*)(a.ring_v + rrow + half + d0) = w2;
+    }
     return;
   }
   const uint16_t* cs = a.cos + b * a.cs_sb + s * a.cs_ss;
@@ -219,6 +248,10 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
       *(u32x4_t*)(kp + half + d0) = pack8(x2);
     }
   }
+  if (ten == 1 && a.ring) {  // the pre-RoPE key (normalised when the head norm is on)
+    *(u32x4_t*)(a.ring_pk + rrow + d0) = pack8(x1);
+    *(u32x4_t*)(a.ring_pk + rrow + half + d0) = pack8(x2);
+  }
   unpack8(*(const u32x4_t*)(cs + d0), c1);
   unpack8(*(const u32x4_t*)(cs + half + d0), c2);
   unpack8(*(const u32x4_t*)(sn + d0), s1);
@@ -230,6 +263,10 @@ __global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
   }
   *(u32x4_t*)(dst + d0) = pack8(o1);
   *(u32x4_t*)(dst + half + d0) = pack8(o2);
+  if (ten == 1 && a.ring) {
+    *(u32x4_t*)(a.ring_k + rrow + d0) = pack8(o1);
+    *(u32x4_t*)(a.ring_k + rrow + half + d0) = pack8(o2);
+  }
 }
 
 // ---- SwiGLU: out = bf16(bf16(silu(g)) * u) ----------------------------------
@@ -481,16 +518,19 @@ extern "C" int wgkv_rms_norm(const void* x, int64_t x_row_stride, const void* re
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
 }
 
-extern "C" int wgkv_rope_qkv_norm(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
-                             const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
-                             const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
-                             const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
-                             void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
-                             void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
-                             void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
-                             int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
-                             int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight, float eps,
-                             void* k_pre, int64_t kp_sb, int64_t kp_ss, int64_t kp_sh, void* stream) {
+namespace {
+
+// wgkv_rope_qkv_norm with the ring fields of RopeArgs (all null / 0 without the ring write)
+int rope_launch(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
+                int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight, float eps,
+                void* k_pre, int64_t kp_sb, int64_t kp_ss, int64_t kp_sh, const RopeArgs& ring, void* stream) {
   if (!q || !k || !cos || !sin || !q_out || !k_out || (v == nullptr) != (v_out == nullptr)) return WGKV_ERR_ARG;
   if (batch <= 0 || seq_len <= 0 || num_q_heads <= 0 || num_kv_heads <= 0) return WGKV_ERR_ARG;
   if (head_dim % 16) return WGKV_ERR_UNSUPPORTED;
@@ -535,9 +575,64 @@ extern "C" int wgkv_rope_qkv_norm(const void* q, int64_t q_sb, int64_t q_ss, int
   a.kp[0] = kp_sb;
   a.kp[1] = kp_ss;
   a.kp[2] = kp_sh;
+  a.ring = ring.ring;
+  a.ring_k = ring.ring_k;
+  a.ring_v = ring.ring_v;
+  a.ring_pk = ring.ring_pk;
+  a.glen = ring.glen;
+  a.seqlens = ring.seqlens;
+  a.W = ring.W;
   const int64_t total = (int64_t)batch * seq_len * (a.H[0] + a.H[1] + a.H[2]) * (head_dim / 16);
   hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, a);
   return hipGetLastError() == hipSuccess ? WGKV_OK : WGKV_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int wgkv_rope_qkv_norm(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,
+                             const void* k, int64_t k_sb, int64_t k_ss, int64_t k_sh,
+                             const void* v, int64_t v_sb, int64_t v_ss, int64_t v_sh,
+                             const void* cos, const void* sin, int64_t cs_sb, int64_t cs_ss,
+                             void* q_out, int64_t qo_sb, int64_t qo_ss, int64_t qo_sh,
+                             void* k_out, int64_t ko_sb, int64_t ko_ss, int64_t ko_sh,
+                             void* v_out, int64_t vo_sb, int64_t vo_ss, int64_t vo_sh,
+                             int32_t batch, int32_t seq_len, int32_t num_q_heads, int32_t num_kv_heads,
+                             int32_t head_dim, const void* q_norm_weight, const void* k_norm_weight, float eps,
+                             void* k_pre, int64_t kp_sb, int64_t kp_ss, int64_t kp_sh, void* stream) {
+  return rope_launch(q, q_sb, q_ss, q_sh, k, k_sb, k_ss, k_sh, v, v_sb, v_ss, v_sh, cos, sin, cs_sb, cs_ss, q_out,
+                     qo_sb, qo_ss, qo_sh, k_out, ko_sb, ko_ss, ko_sh, v_out, vo_sb, vo_ss, vo_sh, batch, seq_len,
+                     num_q_heads, num_kv_heads, head_dim, q_norm_weight, k_norm_weight, eps, k_pre, kp_sb, kp_ss,
+                     kp_sh, RopeArgs{}, stream);
+}
+
+extern "C" int wgkv_rope_qkv_norm_ring_write(const void* q, int64_t q_sh, const void* k, int64_t k_sh,
+                                             const void* v, int64_t v_sh, const void* cos, const void* sin,
+                                             void* q_out, int64_t qo_sh, void* k_out, int64_t ko_sh,
+                                             void* v_out, int64_t vo_sh,
+                                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                             const void* q_norm_weight, const void* k_norm_weight, float eps,
+                                             void* k_pre, int64_t kp_sh,
+                                             int32_t layer, int32_t num_layers, int32_t local_window,
+                                             int32_t* ring_state, void* pool_k, void* pool_v, void* local_pre_key,
+                                             const int32_t* global_lengths, int32_t* cache_seqlens, void* stream) {
+  if (!v || !v_out || !ring_state || !pool_k || !pool_v || !local_pre_key || !global_lengths || !cache_seqlens)
+    return WGKV_ERR_ARG;
+  if (layer < 0 || layer >= num_layers || local_window <= 0 || num_kv_heads <= 0 || head_dim <= 0)
+    return WGKV_ERR_ARG;
+  if (misaligned(pool_k) || misaligned(pool_v) || misaligned(local_pre_key)) return WGKV_ERR_UNSUPPORTED;
+  const int64_t base = (int64_t)layer * num_kv_heads * local_window * head_dim;
+  RopeArgs r = {};
+  r.ring = ring_state;
+  r.ring_k = (uint16_t*)pool_k + base;
+  r.ring_v = (uint16_t*)pool_v + base;
+  r.ring_pk = (uint16_t*)local_pre_key + base;
+  r.glen = global_lengths + (int64_t)layer * num_kv_heads;
+  r.seqlens = cache_seqlens;
+  r.W = local_window;
+  // one decode row: batch and sequence strides do not matter
+  return rope_launch(q, 0, 0, q_sh, k, 0, 0, k_sh, v, 0, 0, v_sh, cos, sin, 0, 0, q_out, 0, 0, qo_sh, k_out, 0, 0,
+                     ko_sh, v_out, 0, 0, vo_sh, 1, 1, num_q_heads, num_kv_heads, head_dim, q_norm_weight,
+                     k_norm_weight, eps, k_pre, 0, 0, kp_sh, r, stream);
 }
 
 extern "C" int wgkv_rope_qkv(const void* q, int64_t q_sb, int64_t q_ss, int64_t q_sh,

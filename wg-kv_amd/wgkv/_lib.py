@@ -134,6 +134,11 @@ SIGNATURES = {
     "wgkv_qkv_rope_ring_write": (ctypes.c_int, [c_ptr, c_i64, c_i32, c_ptr, c_ptr, c_ptr, c_f32, c_ptr, c_ptr, c_ptr,
                                                 c_i32, c_i32, c_i32, c_i32, c_i32, c_i32, c_ptr,
                                                 c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr]),
+    "wgkv_rope_qkv_norm_ring_write": (ctypes.c_int, [c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_ptr,
+                                                     c_ptr, c_i64, c_ptr, c_i64, c_ptr, c_i64,
+                                                     c_i32, c_i32, c_i32, c_ptr, c_ptr, c_f32, c_ptr, c_i64,
+                                                     c_i32, c_i32, c_i32, c_ptr, c_ptr, c_ptr, c_ptr,
+                                                     c_ptr, c_ptr, c_ptr]),
     "wgkv_sparse_prefill_attn": (ctypes.c_int, [
         c_ptr, c_i64, c_i64, c_i64,
         c_ptr, c_ptr, c_i64, c_i64, c_i64,

@@ -174,16 +174,25 @@ class LlamaAttention(nn.Module):
         k = k.transpose(1, 2)
         v = v.transpose(1, 2)
         pre_key = k if "pre_k" in self.config.g_inputs else None
+        c = past_key_value
+        ring = None
+        if (fused_rope and input_shape.numel() == 1 and self.ring_write_fused
+                and layers.ring_write_in_projection(self, c)):
+            # a decode row: the rotation's launch also writes the ring slot
+            ring = (c, self.layer_idx, c.cache_seqlens[self.layer_idx][0])
         if fused_norm:
             # one launch: per-head norms, then the rotation; the normalised,
             # unrotated k is the gate's pre-RoPE key (modeling_qwen3.py:235-239)
             q, k, v, kn = model_ops.rope_qkv(q, k, v, cos, sin, self.q_norm.weight, self.k_norm.weight,
-                                             self.q_norm.eps)
+                                             self.q_norm.eps, ring=ring)
             pre_key = kn if "pre_k" in self.config.g_inputs else None
         elif fused_rope:
-            q, k, v = model_ops.rope_qkv(q, k, v, cos, sin)  # one launch, the same bf16 rounding; v copied beside k
+            # one launch, the same bf16 rounding; v copied beside k
+            q, k, v = model_ops.rope_qkv(q, k, v, cos, sin, ring=ring)
         else:
             q, k = apply_rotary_pos_emb(q, k, cos, sin)
+        if ring is not None or getattr(c, "ring_written_by", None) is not None:
+            c.ring_written_by = self.layer_idx if ring is not None else None
         out, attn_weights, g_scores = self.self_attn_forward_patch(
             self, gating_mode, attention_mask, past_key_value, input_shape, q, pre_key, k, v)
         out = out.reshape(*input_shape, -1).to(hidden_states.dtype).contiguous()

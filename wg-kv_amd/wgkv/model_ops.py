@@ -44,12 +44,17 @@ def rms_norm(x, weight, eps, residual=None):
     return out.view(x.shape), None if ores is None else ores.view(x.shape)
 
 
-def rope_qkv(q, k, v, cos, sin, q_norm_weight=None, k_norm_weight=None, eps=1e-6):
+def rope_qkv(q, k, v, cos, sin, q_norm_weight=None, k_norm_weight=None, eps=1e-6, ring=None):
     """q (B,Hq,S,D), k / v (B,Hkv,S,D) views (d contiguous), cos/sin (B,S,D)
     -> (rotated q, rotated k, v) as (B,H,S,D) views of one contiguous
     (B, S, Hq+2*Hkv, D) buffer, so k and v share strides.  With Qwen3's head
     norm weights (both given) q and k are normalised per head first and the
-    normalised, unrotated k is returned as a fourth (B,Hkv,S,D) view."""
+    normalised, unrotated k is returned as a fourth (B,Hkv,S,D) view.
+
+    ring = (cache, layer, cache_seqlens), for one decode row (B = S = 1) of a
+    DualCache with device ring pointers and deferred gating: the same launch
+    also does the step's ring write (wgkv_rope_qkv_norm_ring_write), as
+    qkv_rope's ring argument does."""
     B, Hq, S, D = q.shape
     Hkv = k.shape[1]
     if cos.stride(-1) != 1:
@@ -57,6 +62,22 @@ def rope_qkv(q, k, v, cos, sin, q_norm_weight=None, k_norm_weight=None, eps=1e-6
     buf = torch.empty(B, S, Hq + 2 * Hkv, D, dtype=q.dtype, device=q.device)
     qo, ko, vo = buf[:, :, :Hq], buf[:, :, Hq:Hq + Hkv], buf[:, :, Hq + Hkv:]
     norm = q_norm_weight is not None
+    if ring is not None:
+        if B != 1 or S != 1:
+            raise ValueError("rope_qkv: the ring write takes one decode row")
+        cache, layer, seqlens = ring
+        kp = torch.empty(B, S, Hkv, D, dtype=q.dtype, device=q.device) if norm else None
+        r = _lib.lib().wgkv_rope_qkv_norm_ring_write(
+            _ptr(q), q.stride(1), _ptr(k), k.stride(1), _ptr(v), v.stride(1), _ptr(cos), _ptr(sin),
+            _ptr(qo), qo.stride(2), _ptr(ko), ko.stride(2), _ptr(vo), vo.stride(2), Hq, Hkv, D,
+            _ptr(q_norm_weight), _ptr(k_norm_weight), float(eps), _ptr(kp), kp.stride(2) if norm else 0,
+            layer, cache.num_layers, cache.local_window_size, _ptr(cache.ring_state),
+            _ptr(cache.block_pool_k), _ptr(cache.block_pool_v), _ptr(cache.local_pre_key),
+            _ptr(cache.global_lengths), _ptr(seqlens), _lib.stream_handle(q.device))
+        _lib.check(r, "wgkv_rope_qkv_norm_ring_write")
+        if norm:
+            return qo.transpose(1, 2), ko.transpose(1, 2), vo.transpose(1, 2), kp.transpose(1, 2)
+        return qo.transpose(1, 2), ko.transpose(1, 2), vo.transpose(1, 2)
 
     def st(t):  # (batch, seq, head) strides of a (B, H, S, D) view
         return t.stride(0), t.stride(2), t.stride(1)
