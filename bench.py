@@ -153,7 +153,7 @@ class DeviceEvent:
         return ms.value
 
     def __del__(self):
-        if self.ev:
+        if getattr(self, "ev", None):
             self.runtime().hipEventDestroy(self.ev)
             self.ev = None
 
@@ -273,7 +273,13 @@ def prefill_section(dev, steps, warmup):
     runs = {"total": [], "marked": [], "phases": [], "host": []}
     gate_mod = [w.gate]
 
-    pool = [DeviceEvent() for _ in range(1 + len(phases) * len(chunks))]  # created once, re-recorded
+    n_ev = 1 + len(phases) * len(chunks)
+    try:  # created once, re-recorded
+        pool = [DeviceEvent() for _ in range(n_ev)]
+        ev_kind = DeviceEvent.KIND + " (timing-only events)"
+    except (OSError, AttributeError, RuntimeError) as exc:  # the runtime's symbols not reachable: torch's events
+        pool = [torch.cuda.Event(enable_timing=True) for _ in range(n_ev)]
+        ev_kind = f"torch.cuda.Event (default release; {type(exc).__name__}: {exc})"
 
     def run(timed):
         """timed: None (warm-up), "total" (events around the prompt) or
@@ -385,7 +391,7 @@ def prefill_section(dev, steps, warmup):
         "ms_per_chunk_by_phase": {p: round(ms[p] / len(chunks), 4) for p in phases},
         "ms_per_chunk_phase_timed": round(t_marked / len(chunks), 4),
         "host_enqueue_ms_per_chunk": round(t_host / len(chunks), 4),
-        "phase_events": DeviceEvent.KIND + " (timing-only events), one between every two phases",
+        "phase_events": ev_kind + ", one between every two phases",
         "gate_parameters": "bfloat16 (the reference's inference loads the gate in bf16)",
         "config4_as_stated": as_stated,
         "sparse_attn": {"tflop": round(attn_flop / 1e12, 4), "tflops": round(attn_flop / ms["sparse_attn"] / 1e9, 1),
