@@ -108,3 +108,34 @@ def test_random_admission_argument_checks_without_gpu():
     assert call(p=-0.1) == _lib.ERR_ARG
     assert call(p=1.5) == _lib.ERR_ARG
     assert call(p=float("nan")) == _lib.ERR_ARG
+
+
+def test_ring_write_entry_points_argument_checks_without_gpu():
+    """wgkv_qkv_rope_ring_write and wgkv_rope_qkv_norm_ring_write reject
+    missing ring buffers, a layer outside the model, an empty window and
+    (the q/k/v product) more KV heads than one wave writes lengths for, on
+    the host before any launch (the fake pointers are never dereferenced)."""
+    from wgkv import _lib
+    L = _lib.lib()
+    f = 0x1000  # 16-byte aligned, never dereferenced
+
+    def gemv(ring=f, pool=f, layer=1, L_=4, W=64, hkv=8):
+        return L.wgkv_qkv_rope_ring_write(f, 4096, 4096, f, f, f, 1e-5, f, f, f, 32, hkv, 128,
+                                          layer, L_, W, ring, pool, f, f, f, f, None)
+
+    assert gemv(ring=None) == _lib.ERR_ARG
+    assert gemv(pool=None) == _lib.ERR_ARG
+    assert gemv(layer=4) == _lib.ERR_ARG
+    assert gemv(layer=-1) == _lib.ERR_ARG
+    assert gemv(W=0) == _lib.ERR_ARG
+    assert gemv(hkv=65) == _lib.ERR_UNSUPPORTED
+
+    def rope(ring=f, v=f, layer=1, W=64, pool=f):
+        return L.wgkv_rope_qkv_norm_ring_write(f, 128, f, 128, v, 128, f, f, f, 128, f, 128, f, 128, 32, 8, 128,
+                                               f, f, 1e-6, f, 128, layer, 4, W, ring, pool, f, f, f, f, None)
+
+    assert rope(ring=None) == _lib.ERR_ARG
+    assert rope(v=None) == _lib.ERR_ARG
+    assert rope(layer=4) == _lib.ERR_ARG
+    assert rope(W=0) == _lib.ERR_ARG
+    assert rope(pool=0x1002) == _lib.ERR_UNSUPPORTED  # ring rows are written 16 bytes at a time
